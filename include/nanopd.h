@@ -1,0 +1,200 @@
+/*
+ * nanopd.h -- C ABI of libnanopd_hip.so, the MI355X (gfx950) implementation of
+ * nanoPD's `paged_kernels` extension: the paged KV store and paged attention
+ * that ModelRunner.paged_forward calls once per attention layer.
+ *
+ * Conventions (all entry points):
+ *   - Every pointer is a device pointer unless stated otherwise; the caller owns
+ *     all memory. The library keeps no pointer after a call returns.
+ *   - Caches are the reference layout [num_blocks, num_kv_heads, block_size,
+ *     head_dim], contiguous (nanoPD/engine/model_runner.py:24-31).
+ *   - dtype: NPD_DTYPE_F16 or NPD_DTYPE_BF16 (elements of 2 bytes).
+ *   - stream: a hipStream_t passed as void* (NULL = the null stream). Work is
+ *     enqueued on it; no call synchronises the host.
+ *   - Return value: 0 on success, a negative NPD_E* code on failure. Nothing is
+ *     launched when validation fails. npd_last_error() gives a message for the
+ *     last failure on the calling thread. No C++ exception crosses the ABI, and
+ *     the process is never terminated (the reference calls exit(), see
+ *     PA/csrc/utils/cuda_utils.h:18-29).
+ *   - Index contents are checked in the kernels, not on the host (that would
+ *     need a device-to-host sync): a token whose slot or block falls outside the
+ *     pool is skipped by the stores, and attention clamps block ids into the
+ *     pool so that no access leaves it.
+ *   - Thread-safe and reentrant: no mutable global state beyond the per-thread
+ *     error message.
+ * Citations are relative to the reference tree; PA/ = nanoPD/paged_attention/.
+ */
+#ifndef NANOPD_H
+#define NANOPD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NPD_DTYPE_F16  0
+#define NPD_DTYPE_BF16 1
+
+#define NPD_OK              0
+#define NPD_E_INVALID      -1  /* bad shape, size, stride or argument */
+#define NPD_E_DTYPE        -2  /* unsupported element type */
+#define NPD_E_ALIGN        -3  /* pointer or stride not 16-byte aligned */
+#define NPD_E_WORKSPACE    -4  /* workspace missing or too small */
+#define NPD_E_LAUNCH       -5  /* the HIP runtime reported an error */
+
+/* Message for the last failed call on this thread ("" if none). */
+const char* npd_last_error(void);
+
+/* Library version, e.g. 100 for 0.1.0. */
+int npd_version(void);
+
+/*
+ * Paged KV store, per-token block tables.
+ * Replaces paged_kv_store (PA/csrc/kvstore/paged_kv_store.h:23-27,
+ * PA/csrc/kvstore/paged_kv_store_ops.cu:7-50, kernel
+ * PA/csrc/kvstore/paged_kv_store_kernel.cu:16-58).
+ * For token t < num_tokens and head h < num_kv_heads:
+ *   pos = positions[t];  blk = block_tables[t * max_blocks_per_seq + pos / block_size]
+ *   k_cache[blk, h, pos % block_size, :] = k_src[h * src_stride_head + t * src_stride_token + :]
+ *   (same for v). Strides are in elements; the reference passes k_src
+ *   [kvh, T, D] contiguous, i.e. src_stride_head = T*D, src_stride_token = D.
+ * Tokens with pos < 0, pos / block_size >= max_blocks_per_seq or blk outside
+ * [0, num_blocks) are skipped.
+ */
+int npd_paged_kv_store(void* k_cache, void* v_cache,
+                       const void* k_src, const void* v_src,
+                       const int32_t* block_tables, const int32_t* positions,
+                       int64_t num_tokens, int64_t num_kv_heads, int64_t head_dim,
+                       int64_t num_blocks, int64_t block_size,
+                       int64_t max_blocks_per_seq,
+                       int64_t src_stride_head, int64_t src_stride_token,
+                       int32_t dtype, void* stream);
+
+/*
+ * Paged KV store driven by a flat slot mapping (no reference counterpart; the
+ * reference builds a [T, max_bps] table per prefill sequence per layer for it,
+ * nanoPD/engine/model_runner.py:132-150):
+ *   slot = slot_mapping[t]; if slot < 0 or slot >= num_blocks*block_size: skip
+ *   k_cache[slot / block_size, h, slot % block_size, :] = k_src[t*src_stride_token + h*src_stride_head + :]
+ * Accepts token-major sources ([T, kvh, D] straight from k_proj) without a copy.
+ */
+int npd_paged_kv_store_slots(void* k_cache, void* v_cache,
+                             const void* k_src, const void* v_src,
+                             const int32_t* slot_mapping,
+                             int64_t num_tokens, int64_t num_kv_heads, int64_t head_dim,
+                             int64_t num_blocks, int64_t block_size,
+                             int64_t src_stride_head, int64_t src_stride_token,
+                             int32_t dtype, void* stream);
+
+/*
+ * Bytes of device workspace npd_paged_attention needs for these shapes (split-
+ * context partials). 0 means no workspace is needed.
+ */
+int64_t npd_paged_attention_workspace_size(int64_t num_seqs, int64_t num_heads,
+                                           int64_t head_dim, int64_t block_size,
+                                           int64_t max_blocks_per_seq);
+
+/*
+ * Paged decode attention (one query token per sequence).
+ * Replaces paged_attention_forward (PA/csrc/attention/paged_attention.h:24-34,
+ * PA/csrc/attention/paged_attention_ops.cu:7-59, kernel
+ * PA/csrc/attention/paged_attention_kernel.cu:39-151):
+ *   out[s, h, :] = softmax(scale * q[s,h] . K[s, h / (H/kvh)]^T) . V[s, h / (H/kvh)]
+ * over the first seq_lens[s] tokens, gathered through block_tables[s, :].
+ * query/out strides are in elements (head_dim contiguous). seq_lens[s] <= 0
+ * gives zeros; seq_lens[s] is clamped to max_blocks_per_seq * block_size.
+ * Every output element is written: out need not be zeroed.
+ * workspace: at least npd_paged_attention_workspace_size(...) bytes, 256-byte
+ * aligned (may be NULL when that size is 0).
+ */
+int npd_paged_attention(void* out, const void* query,
+                        const void* key_cache, const void* value_cache,
+                        const int32_t* block_tables, const int32_t* seq_lens,
+                        int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads,
+                        int64_t head_dim, int64_t num_blocks, int64_t block_size,
+                        int64_t max_blocks_per_seq, float scale,
+                        int64_t q_stride_seq, int64_t q_stride_head,
+                        int64_t out_stride_seq, int64_t out_stride_head,
+                        void* workspace, int64_t workspace_bytes,
+                        int32_t dtype, void* stream);
+
+/*
+ * Bytes of device workspace npd_paged_prefill_attention needs.
+ */
+int64_t npd_paged_prefill_workspace_size(int64_t num_seqs, int64_t total_q,
+                                         int64_t num_heads, int64_t head_dim,
+                                         int64_t max_q_len, int64_t max_context_len);
+
+/*
+ * Chunked-prefill attention over a paged prefix plus the new chunk (varlen).
+ * Replaces the prefill branch of paged_forward, which runs
+ * F.scaled_dot_product_attention over the chunk alone with a block-diagonal
+ * causal mask (nanoPD/engine/model_runner.py:152-168); this op also reads the
+ * prefix already in the pool, which the reference ignores.
+ * Sequence s owns query rows cu_seqlens_q[s] .. cu_seqlens_q[s+1]-1 of query
+ * [total_q, H, D]; its chunk K/V must already be stored in the pool;
+ * context_lens[s] counts prefix + chunk tokens. Query row i of s sits at
+ * position p = context_lens[s] - q_len_s + i and attends to keys 0..p.
+ * Rows with p < 0 (context shorter than the chunk) get zeros.
+ * max_q_len / max_context_len: host-known upper bounds used to size the grid.
+ */
+int npd_paged_prefill_attention(void* out, const void* query,
+                                const void* key_cache, const void* value_cache,
+                                const int32_t* block_tables,
+                                const int32_t* cu_seqlens_q,
+                                const int32_t* context_lens,
+                                int64_t num_seqs, int64_t total_q,
+                                int64_t num_heads, int64_t num_kv_heads,
+                                int64_t head_dim, int64_t num_blocks,
+                                int64_t block_size, int64_t max_blocks_per_seq,
+                                int64_t max_q_len, int64_t max_context_len,
+                                float scale,
+                                int64_t q_stride_token, int64_t q_stride_head,
+                                int64_t out_stride_token, int64_t out_stride_head,
+                                void* workspace, int64_t workspace_bytes,
+                                int32_t dtype, void* stream);
+
+/*
+ * Copy-on-write block copy (no reference counterpart: the reference returns
+ * the (src, dst) pair from BlockSpaceManager.append_slot,
+ * nanoPD/block_manager/block_manager.py:91-96, and never copies).
+ * For each pair i: k_cache[pairs[2i+1]] = k_cache[pairs[2i]], same for v;
+ * a whole block is num_kv_heads * block_size * head_dim elements.
+ * Pairs with an index outside [0, num_blocks) are skipped.
+ */
+int npd_copy_blocks(void* k_cache, void* v_cache, const int32_t* pairs,
+                    int64_t num_pairs, int64_t num_blocks,
+                    int64_t block_elems, int32_t dtype, void* stream);
+
+/*
+ * Ragged-batch metadata packing on the GPU (no reference counterpart: the
+ * reference re-tensorises its context dict per layer with host loops,
+ * nanoPD/engine/model_runner.py:129-187, from nanoPD/engine/engine.py:45-90).
+ * Input, one compact upload: seq_desc[s] = {q_len, ctx_before, table_len} for
+ * s < num_seqs (prefill chunks and decodes alike, in batch order) and the
+ * concatenation of every sequence's block table, table_len entries each.
+ * Outputs (device, caller-allocated):
+ *   cu_seqlens_q[num_seqs+1]  prefix sums of q_len
+ *   seq_lens[num_seqs]        ctx_before + q_len (context after the step)
+ *   block_tables[num_seqs, max_blocks_per_seq]  zero-padded rows
+ *   positions[total_q]        ctx_before + i for the i-th new token
+ *   slot_mapping[total_q]     table[pos / block_size] * block_size + pos % block_size,
+ *                             or -1 when pos / block_size >= table_len
+ *   token_seq[total_q]        owning sequence of each token
+ * total_q must equal the sum of q_len (checked by the kernel: entries past
+ * the true total are left untouched). num_seqs <= 4096.
+ */
+int npd_pack_metadata(const int32_t* seq_desc, const int32_t* flat_tables,
+                      int64_t num_seqs, int64_t total_q, int64_t flat_len,
+                      int64_t max_blocks_per_seq, int64_t block_size,
+                      int32_t* cu_seqlens_q, int32_t* seq_lens,
+                      int32_t* block_tables, int32_t* positions,
+                      int32_t* slot_mapping, int32_t* token_seq,
+                      void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NANOPD_H */

@@ -1,0 +1,60 @@
+// Shared helpers for the gfx950 kernels and their C-ABI wrappers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/nanopd.h"
+
+namespace npd {
+
+// Records a formatted message as this thread's last error and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Maps a failed HIP call (or a failed launch) to NPD_E_LAUNCH.
+int check_launch(const char* what);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---------------------------------------------------------------------------
+// Element conversions. Both storage types are 2 bytes; arithmetic is fp32.
+// bf16 -> f32 is exact (the bf16 bits are the high half of the f32 bits);
+// f32 -> bf16 rounds to nearest even, NaN stays NaN.
+// ---------------------------------------------------------------------------
+struct BF16 {
+  static __device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  static __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+  static __device__ __forceinline__ uint32_t from_float(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;  // NaN
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+  }
+  // Dot product of two packed pairs, accumulated in fp32 (v_dot2_f32_bf16).
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
+  }
+};
+
+struct F16 {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  static __device__ __forceinline__ float lo(uint32_t w) {
+    return static_cast<float>(__builtin_bit_cast(h2, w).x);
+  }
+  static __device__ __forceinline__ float hi(uint32_t w) {
+    return static_cast<float>(__builtin_bit_cast(h2, w).y);
+  }
+  static __device__ __forceinline__ uint32_t from_float(float f) {
+    _Float16 h = static_cast<_Float16>(f);  // round to nearest even
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h));
+  }
+  // v_dot2_f32_f16: products of fp16 pairs summed into an fp32 accumulator.
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
+  }
+};
+
+}  // namespace npd

@@ -1,0 +1,477 @@
+// Paged decode attention (one query token per sequence), GQA, split-context.
+//
+// Reference computation: PA/csrc/attention/paged_attention_kernel.cu:39-151
+// (one 128-thread block per (seq, q-head), scores and probabilities rounded to
+// the storage type) with host wrapper PA/csrc/attention/paged_attention_ops.cu:7-59;
+// the split-context math (partials plus a log-sum-exp merge) follows the
+// unbuilt PA/csrc/paged_attention_optimized/paged_attention_optimized.cu:66-219.
+//
+// MI355X design. The work unit is one wave64 per (sequence, kv-head, context
+// partition of PS tokens); the wave serves all G = H / kvh query heads of the
+// group, so every K/V row is read from HBM once, not G times.
+//   lanes:  a head row of D 2-byte elements is D/8 lanes x 16 bytes (LPT lanes);
+//           the wave covers TPL = 64 / LPT tokens per dwordx4 load and a step is
+//           16 tokens (NL = 16 / TPL loads of K, later NL loads of V).
+//   pass 1: K rows -> q.k with v_dot2_f32_{bf16,f16} (fp32 accumulate), then a
+//           butterfly reduce-scatter across the LPT lanes of each token so that
+//           each lane ends with its own (token, head) scores; scores go to LDS.
+//   pass 2: exact softmax statistics over the partition in LDS (max, exp2, sum),
+//           reduced across lanes with shuffles; probabilities stay in fp32.
+//   pass 3: V rows -> acc[h][8 dims] += p * v in fp32; rows of the wave are
+//           combined with shuffles at the end.
+// A sequence that fits in one partition writes its output directly; longer
+// ones write fp32 partials (acc, max, sum) and merge_partitions_kernel
+// combines them (log-sum-exp merge). No MFMA: at one query row per sequence
+// the op is HBM-bound.
+#include "common.h"
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMaxPartition = 512;   // tokens per partition, upper bound (LDS sizing)
+constexpr int kStep = 16;            // tokens per step
+constexpr float kLog2e = 1.4426950408889634f;
+
+constexpr int ilog2(int x) { return x <= 1 ? 0 : 1 + ilog2(x >> 1); }
+constexpr int pow2ceil(int x) { return x <= 1 ? 1 : 2 * pow2ceil((x + 1) / 2); }
+constexpr int cmin(int a, int b) { return a < b ? a : b; }
+
+__device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+template <class TT>
+__device__ __forceinline__ void store_row8(uint16_t* dst, const float* v, float inv) {
+  u32x4 w;
+  w.x = TT::from_float(v[0] * inv) | (TT::from_float(v[1] * inv) << 16);
+  w.y = TT::from_float(v[2] * inv) | (TT::from_float(v[3] * inv) << 16);
+  w.z = TT::from_float(v[4] * inv) | (TT::from_float(v[5] * inv) << 16);
+  w.w = TT::from_float(v[6] * inv) | (TT::from_float(v[7] * inv) << 16);
+  *reinterpret_cast<u32x4*>(dst) = w;
+}
+
+struct DecodeArgs {
+  uint16_t* out;
+  const uint16_t* q;
+  const u32x4* k_cache;
+  const u32x4* v_cache;
+  const int32_t* block_tables;
+  const int32_t* seq_lens;
+  float* part_acc;   // [S*kvh, max_parts, G, D]
+  float* part_ml;    // [S*kvh, max_parts, G, 2]
+  int num_kv_heads;
+  int block_size;
+  int num_blocks;
+  int max_bps;
+  int partition;     // PS, multiple of kStep, <= kMaxPartition
+  int max_parts;
+  float scale_log2;  // softmax scale * log2(e)
+  int64_t q_stride_seq, q_stride_head, out_stride_seq, out_stride_head;
+};
+
+template <class TT, int D, int G>
+__global__ __launch_bounds__(64) void decode_partition_kernel(DecodeArgs a) {
+  constexpr int LPT = D / 8;             // lanes per token row
+  constexpr int TPL = 64 / LPT;          // tokens per load
+  constexpr int NL = kStep / TPL;        // loads per step
+  constexpr int GP = pow2ceil(G);        // heads padded to a power of two
+  constexpr int NV = NL * GP;            // partial dot products per lane per step
+  constexpr int LOG_LPT = ilog2(LPT);
+  constexpr int NH = cmin(LOG_LPT, ilog2(NV));  // halving steps of the reduce-scatter
+  constexpr int HELD = NV >> NH;                 // values a lane keeps
+  static_assert(TPL * NL == kStep, "step shape");
+
+  __shared__ float s_p[kMaxPartition * GP];      // scores, then probabilities
+  __shared__ int s_blk[kMaxPartition + 1];       // block ids of the partition
+  __shared__ float s_ml[2 * GP];                 // per-head max and sum
+
+  const int lane = threadIdx.x;
+  const int r = lane / LPT;   // token row within a load
+  const int j = lane % LPT;   // 16-byte chunk of the head row
+  const int unit = blockIdx.x;
+  const int s = unit / a.num_kv_heads;
+  const int kh = unit - s * a.num_kv_heads;
+  const int part = blockIdx.y;
+
+  int ctx = a.seq_lens[s];
+  const int cap = a.max_bps * a.block_size;
+  ctx = ctx < cap ? ctx : cap;
+  if (ctx <= 0) {
+    if (part == 0 && lane < LPT) {
+      const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      for (int h = 0; h < G; ++h)
+        store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + j * 8, z, 0.f);
+    }
+    return;
+  }
+  const int nparts = (ctx + a.partition - 1) / a.partition;
+  if (part >= nparts) return;
+  const int t0 = part * a.partition;
+  const int ntok = (ctx - t0) < a.partition ? (ctx - t0) : a.partition;
+  const int nsteps = (ntok + kStep - 1) / kStep;
+  const int bs = a.block_size;
+  const int b0 = t0 / bs;
+  const int nb = (t0 + ntok - 1) / bs - b0 + 1;
+
+  // Block ids of this partition -> LDS, clamped into the pool.
+  const int32_t* bt_row = a.block_tables + (int64_t)s * a.max_bps;
+  for (int e = lane; e < nb; e += 64) {
+    int b = bt_row[b0 + e];
+    b = b < 0 ? 0 : (b >= a.num_blocks ? a.num_blocks - 1 : b);
+    s_blk[e] = b;
+  }
+
+  // Query chunk j of each head in the group, as packed pairs.
+  u32x4 qv[G];
+  const uint16_t* qbase = a.q + s * a.q_stride_seq + (kh * G) * a.q_stride_head + j * 8;
+#pragma unroll
+  for (int h = 0; h < G; ++h) qv[h] = *reinterpret_cast<const u32x4*>(qbase + h * a.q_stride_head);
+  __syncthreads();
+
+  const int64_t head_off = (int64_t)kh * bs;  // rows of kv-head kh inside a block
+  auto row_index = [&](int tl) -> int64_t {
+    // 16-byte index of chunk j of token tl (clamped to the last valid token)
+    const int t = t0 + (tl < ntok ? tl : ntok - 1);
+    const int lb = t / bs;
+    const int off = t - lb * bs;
+    const int blk = s_blk[lb - b0];
+    return (((int64_t)blk * a.num_kv_heads * bs) + head_off + off) * LPT + j;
+  };
+
+  // ---------------- pass 1: scores ----------------
+  u32x4 kcur[NL];
+#pragma unroll
+  for (int i = 0; i < NL; ++i) kcur[i] = a.k_cache[row_index(i * TPL + r)];
+  for (int st = 0; st < nsteps; ++st) {
+    u32x4 knext[NL];
+    if (st + 1 < nsteps) {
+#pragma unroll
+      for (int i = 0; i < NL; ++i) knext[i] = a.k_cache[row_index((st + 1) * kStep + i * TPL + r)];
+    }
+    float v[NV];
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+#pragma unroll
+      for (int h = 0; h < GP; ++h) {
+        float d = 0.f;
+        if (h < G) {
+          d = TT::dot2(kcur[i].x, qv[h].x, d);
+          d = TT::dot2(kcur[i].y, qv[h].y, d);
+          d = TT::dot2(kcur[i].z, qv[h].z, d);
+          d = TT::dot2(kcur[i].w, qv[h].w, d);
+        }
+        v[i * GP + h] = d;
+      }
+    }
+    // Butterfly over the LPT lanes of a token: halving steps first (high lane
+    // bits), then plain xor-sums for the remaining bits.
+    int cnt = NV;
+#pragma unroll
+    for (int m = LPT / 2, stepi = 0; m >= 1; m >>= 1, ++stepi) {
+      if (stepi < NH) {
+        const bool upper = (j & m) != 0;
+        const int half = cnt / 2;
+#pragma unroll
+        for (int k = 0; k < NV / 2; ++k) {
+          if (k < half) {
+            const float send = upper ? v[k] : v[k + half];
+            const float keep = upper ? v[k + half] : v[k];
+            v[k] = keep + shfl_xor(send, m);
+          }
+        }
+        cnt = half;
+      } else {
+        v[0] += shfl_xor(v[0], m);
+      }
+    }
+    const int prefix = j >> (LOG_LPT - NH);
+#pragma unroll
+    for (int e = 0; e < HELD; ++e) {
+      const int k = prefix * HELD + e;
+      const int i = k / GP, h = k % GP;
+      const int tl = st * kStep + i * TPL + r;
+      if (h < G) s_p[tl * GP + h] = (tl < ntok) ? v[e] * a.scale_log2 : -INFINITY;
+    }
+    if (st + 1 < nsteps) {
+#pragma unroll
+      for (int i = 0; i < NL; ++i) kcur[i] = knext[i];
+    }
+  }
+
+  // Issue the first V loads before the softmax pass so they are in flight.
+  u32x4 vcur[NL];
+#pragma unroll
+  for (int i = 0; i < NL; ++i) vcur[i] = a.v_cache[row_index(i * TPL + r)];
+  __syncthreads();
+
+  // ---------------- pass 2: softmax over the partition ----------------
+  {
+    const int n = nsteps * kStep * GP;
+    float m = -INFINITY;
+    for (int idx = lane; idx < n; idx += 64) m = fmaxf(m, s_p[idx]);
+#pragma unroll
+    for (int mask = GP; mask < 64; mask <<= 1) m = fmaxf(m, shfl_xor(m, mask));
+    float l = 0.f;
+    for (int idx = lane; idx < n; idx += 64) {
+      const float p = exp2f(s_p[idx] - m);
+      s_p[idx] = p;
+      l += p;
+    }
+#pragma unroll
+    for (int mask = GP; mask < 64; mask <<= 1) l += shfl_xor(l, mask);
+    if (lane < GP) {
+      s_ml[lane] = m;
+      s_ml[GP + lane] = l;
+    }
+  }
+  __syncthreads();
+
+  // ---------------- pass 3: probabilities x V ----------------
+  float acc[G][8];
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int d = 0; d < 8; ++d) acc[h][d] = 0.f;
+  for (int st = 0; st < nsteps; ++st) {
+    u32x4 vnext[NL];
+    if (st + 1 < nsteps) {
+#pragma unroll
+      for (int i = 0; i < NL; ++i) vnext[i] = a.v_cache[row_index((st + 1) * kStep + i * TPL + r)];
+    }
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int tl = st * kStep + i * TPL + r;
+      float p[GP];
+#pragma unroll
+      for (int h4 = 0; h4 < GP; h4 += 4) {
+        if constexpr (GP >= 4) {
+          const f32x4 pv = *reinterpret_cast<const f32x4*>(&s_p[tl * GP + h4]);
+          p[h4] = pv.x; p[h4 + 1] = pv.y; p[h4 + 2] = pv.z; p[h4 + 3] = pv.w;
+        }
+      }
+      if constexpr (GP < 4) {
+#pragma unroll
+        for (int h = 0; h < GP; ++h) p[h] = s_p[tl * GP + h];
+      }
+      const uint32_t w[4] = {vcur[i].x, vcur[i].y, vcur[i].z, vcur[i].w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float f0 = TT::lo(w[c]), f1 = TT::hi(w[c]);
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+          acc[h][2 * c] = fmaf(p[h], f0, acc[h][2 * c]);
+          acc[h][2 * c + 1] = fmaf(p[h], f1, acc[h][2 * c + 1]);
+        }
+      }
+    }
+    if (st + 1 < nsteps) {
+#pragma unroll
+      for (int i = 0; i < NL; ++i) vcur[i] = vnext[i];
+    }
+  }
+  // Combine the TPL token rows of the wave.
+#pragma unroll
+  for (int mask = LPT; mask < 64; mask <<= 1)
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc[h][d] += shfl_xor(acc[h][d], mask);
+
+  if (lane >= LPT) return;
+  if (nparts == 1) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float l = s_ml[GP + h];
+      store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + j * 8,
+                     acc[h], 1.f / l);
+    }
+  } else {
+    const int64_t base = (int64_t)unit * a.max_parts + part;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      f32x4* dst = reinterpret_cast<f32x4*>(a.part_acc + ((base * G + h) * D + j * 8));
+      dst[0] = f32x4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
+      dst[1] = f32x4{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
+    }
+    if (j < G) {
+      a.part_ml[(base * G + j) * 2] = s_ml[j];
+      a.part_ml[(base * G + j) * 2 + 1] = s_ml[GP + j];
+    }
+  }
+}
+
+// Log-sum-exp merge of the partitions of each (sequence, kv-head) with more
+// than one partition (formula of paged_attention_optimized.cu:185-217, in the
+// log2 domain used by the partition kernel):
+//   M = max_p m_p;  L = sum_p l_p 2^(m_p - M);  out = sum_p acc_p 2^(m_p - M) / L
+template <class TT, int D, int G>
+__global__ __launch_bounds__(256) void merge_partitions_kernel(DecodeArgs a) {
+  const int unit = blockIdx.x;
+  const int s = unit / a.num_kv_heads;
+  const int kh = unit - s * a.num_kv_heads;
+  int ctx = a.seq_lens[s];
+  const int cap = a.max_bps * a.block_size;
+  ctx = ctx < cap ? ctx : cap;
+  if (ctx <= 0) return;
+  const int nparts = (ctx + a.partition - 1) / a.partition;
+  if (nparts <= 1) return;
+  const int64_t base = (int64_t)unit * a.max_parts;
+  constexpr int CH = D / 8;  // 8-dim chunks per head
+  for (int idx = threadIdx.x; idx < G * CH; idx += blockDim.x) {
+    const int h = idx / CH, c = idx % CH;
+    float M = -INFINITY;
+    for (int p = 0; p < nparts; ++p) M = fmaxf(M, a.part_ml[((base + p) * G + h) * 2]);
+    float L = 0.f;
+    float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int p = 0; p < nparts; ++p) {
+      const float mp = a.part_ml[((base + p) * G + h) * 2];
+      const float lp = a.part_ml[((base + p) * G + h) * 2 + 1];
+      const float w = exp2f(mp - M);
+      L = fmaf(lp, w, L);
+      const f32x4* src = reinterpret_cast<const f32x4*>(a.part_acc + (((base + p) * G + h) * D + c * 8));
+      const f32x4 x0 = src[0], x1 = src[1];
+      o[0] = fmaf(x0.x, w, o[0]); o[1] = fmaf(x0.y, w, o[1]);
+      o[2] = fmaf(x0.z, w, o[2]); o[3] = fmaf(x0.w, w, o[3]);
+      o[4] = fmaf(x1.x, w, o[4]); o[5] = fmaf(x1.y, w, o[5]);
+      o[6] = fmaf(x1.z, w, o[6]); o[7] = fmaf(x1.w, w, o[7]);
+    }
+    store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + c * 8, o,
+                   1.f / L);
+  }
+}
+
+// Partition length: 512 tokens normally; 256 when that leaves too few waves to
+// fill 256 CUs. The workspace is always sized for the smaller partition.
+int choose_partition(int64_t num_seqs, int64_t num_kv_heads, int64_t max_ctx) {
+  const int64_t waves512 = num_seqs * num_kv_heads * ((max_ctx + 511) / 512);
+  return waves512 >= 4096 ? 512 : 256;
+}
+
+template <class TT, int D, int G>
+int launch_decode(const DecodeArgs& a, int64_t units, hipStream_t st) {
+  hipLaunchKernelGGL((decode_partition_kernel<TT, D, G>), dim3((unsigned)units, (unsigned)a.max_parts),
+                     dim3(64), 0, st, a);
+  if (a.max_parts > 1)
+    hipLaunchKernelGGL((merge_partitions_kernel<TT, D, G>), dim3((unsigned)units), dim3(256), 0, st, a);
+  return npd::check_launch("npd_paged_attention");
+}
+
+template <class TT, int D>
+int dispatch_g(int g, const DecodeArgs& a, int64_t units, hipStream_t st) {
+  switch (g) {
+    case 1: return launch_decode<TT, D, 1>(a, units, st);
+    case 2: return launch_decode<TT, D, 2>(a, units, st);
+    case 3: return launch_decode<TT, D, 3>(a, units, st);
+    case 4: return launch_decode<TT, D, 4>(a, units, st);
+    case 5: return launch_decode<TT, D, 5>(a, units, st);
+    case 6: return launch_decode<TT, D, 6>(a, units, st);
+    case 7: return launch_decode<TT, D, 7>(a, units, st);
+    default: return launch_decode<TT, D, 8>(a, units, st);
+  }
+}
+
+template <class TT>
+int dispatch_d(int64_t d, int g, const DecodeArgs& a, int64_t units, hipStream_t st) {
+  switch (d) {
+    case 64: return dispatch_g<TT, 64>(g, a, units, st);
+    case 128: return dispatch_g<TT, 128>(g, a, units, st);
+    default: return dispatch_g<TT, 256>(g, a, units, st);
+  }
+}
+
+}  // namespace
+
+extern "C" int64_t npd_paged_attention_workspace_size(int64_t num_seqs, int64_t num_heads,
+                                                      int64_t head_dim, int64_t block_size,
+                                                      int64_t max_blocks_per_seq) {
+  if (num_seqs <= 0 || num_heads <= 0 || head_dim <= 0 || block_size <= 0 || max_blocks_per_seq <= 0)
+    return 0;
+  const int64_t max_ctx = block_size * max_blocks_per_seq;
+  const int64_t parts = (max_ctx + 255) / 256;
+  if (parts <= 1) return 0;
+  return num_seqs * num_heads * parts * (head_dim + 2) * (int64_t)sizeof(float);
+}
+
+extern "C" int npd_paged_attention(void* out, const void* query, const void* key_cache,
+                                   const void* value_cache, const int32_t* block_tables,
+                                   const int32_t* seq_lens, int64_t num_seqs, int64_t num_heads,
+                                   int64_t num_kv_heads, int64_t head_dim, int64_t num_blocks,
+                                   int64_t block_size, int64_t max_blocks_per_seq, float scale,
+                                   int64_t q_stride_seq, int64_t q_stride_head,
+                                   int64_t out_stride_seq, int64_t out_stride_head,
+                                   void* workspace, int64_t workspace_bytes, int32_t dtype,
+                                   void* stream) {
+  using namespace npd;
+  const char* name = "npd_paged_attention";
+  if (dtype != NPD_DTYPE_F16 && dtype != NPD_DTYPE_BF16)
+    return fail(NPD_E_DTYPE, "%s: unsupported dtype code %d (fp16/bf16 only)", name, dtype);
+  if (num_seqs < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_blocks <= 0 ||
+      block_size <= 0 || max_blocks_per_seq <= 0)
+    return fail(NPD_E_INVALID,
+                "%s: bad sizes (seqs %lld, heads %lld, kv heads %lld, blocks %lld, block %lld, "
+                "max blocks/seq %lld)", name, (long long)num_seqs, (long long)num_heads,
+                (long long)num_kv_heads, (long long)num_blocks, (long long)block_size,
+                (long long)max_blocks_per_seq);
+  if (num_heads % num_kv_heads != 0)
+    return fail(NPD_E_INVALID, "%s: num_heads %lld is not a multiple of num_kv_heads %lld", name,
+                (long long)num_heads, (long long)num_kv_heads);
+  const int64_t g = num_heads / num_kv_heads;
+  if (g > 8)
+    return fail(NPD_E_INVALID, "%s: query heads per kv head %lld > 8 is not supported", name,
+                (long long)g);
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(NPD_E_INVALID, "%s: head_dim %lld not in {64, 128, 256}", name, (long long)head_dim);
+  if (num_blocks * block_size * num_kv_heads > INT32_MAX || max_blocks_per_seq * block_size > INT32_MAX)
+    return fail(NPD_E_INVALID, "%s: pool exceeds int32 row indexing", name);
+  if (num_seqs * num_kv_heads > 0x7fffffff)
+    return fail(NPD_E_INVALID, "%s: too many (seq, kv-head) units", name);
+  if (q_stride_seq % 8 || q_stride_head % 8 || out_stride_seq % 8 || out_stride_head % 8 ||
+      q_stride_seq < 0 || q_stride_head < 0 || out_stride_seq < 0 || out_stride_head < 0)
+    return fail(NPD_E_ALIGN, "%s: query/out strides must be non-negative multiples of 8 elements",
+                name);
+  if (num_seqs == 0) return NPD_OK;
+  if (!out || !query || !key_cache || !value_cache || !block_tables || !seq_lens)
+    return fail(NPD_E_INVALID, "%s: null pointer", name);
+  if (!aligned16(out) || !aligned16(query) || !aligned16(key_cache) || !aligned16(value_cache))
+    return fail(NPD_E_ALIGN, "%s: out/query/cache pointers must be 16-byte aligned", name);
+
+  const int64_t max_ctx = block_size * max_blocks_per_seq;
+  const int partition = choose_partition(num_seqs, num_kv_heads, max_ctx);
+  const int64_t max_parts = (max_ctx + partition - 1) / partition;
+  if (max_parts > 65535) return fail(NPD_E_INVALID, "%s: context too long", name);
+  const int64_t need = npd_paged_attention_workspace_size(num_seqs, num_heads, head_dim,
+                                                          block_size, max_blocks_per_seq);
+  if (max_parts > 1) {
+    if (!workspace || workspace_bytes < need)
+      return fail(NPD_E_WORKSPACE, "%s: workspace of %lld bytes needed, %lld given", name,
+                  (long long)need, (long long)workspace_bytes);
+    if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+      return fail(NPD_E_ALIGN, "%s: workspace must be 256-byte aligned", name);
+  }
+
+  DecodeArgs a;
+  a.out = static_cast<uint16_t*>(out);
+  a.q = static_cast<const uint16_t*>(query);
+  a.k_cache = static_cast<const u32x4*>(key_cache);
+  a.v_cache = static_cast<const u32x4*>(value_cache);
+  a.block_tables = block_tables;
+  a.seq_lens = seq_lens;
+  const int64_t units = num_seqs * num_kv_heads;
+  float* ws = static_cast<float*>(workspace);
+  a.part_acc = ws;
+  a.part_ml = ws ? ws + units * max_parts * g * head_dim : nullptr;
+  a.num_kv_heads = (int)num_kv_heads;
+  a.block_size = (int)block_size;
+  a.num_blocks = (int)num_blocks;
+  a.max_bps = (int)max_blocks_per_seq;
+  a.partition = partition;
+  a.max_parts = (int)max_parts;
+  a.scale_log2 = scale * kLog2e;
+  a.q_stride_seq = q_stride_seq;
+  a.q_stride_head = q_stride_head;
+  a.out_stride_seq = out_stride_seq;
+  a.out_stride_head = out_stride_head;
+  hipStream_t st = as_stream(stream);
+  if (dtype == NPD_DTYPE_BF16) return dispatch_d<BF16>(head_dim, (int)g, a, units, st);
+  return dispatch_d<F16>(head_dim, (int)g, a, units, st);
+}

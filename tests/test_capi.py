@@ -1,0 +1,108 @@
+"""CPU tests of the drop-in boundary: the C-ABI library loads, exports every
+symbol include/nanopd.h declares, and rejects bad arguments before touching
+the GPU; the Python mirror raises RuntimeError where the reference's
+TORCH_CHECKs do (PA/csrc/attention/paged_attention_ops.cu:18-22,
+PA/csrc/kvstore/paged_kv_store_ops.cu:13-16; int64 tables ->
+RuntimeError as in PA/tests/test_paged_attention.py:233-247)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from nanopd_amd import _lib
+from nanopd_amd import paged_kernels as pk
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared_symbols():
+    text = (ROOT / "include" / "nanopd.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(npd_\w+)\s*\(", text, re.M)))
+
+
+def test_header_and_binding_agree():
+    assert _declared_symbols() == sorted(_lib.exported_symbols())
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.npd_version() >= 100
+
+
+def test_library_exports_are_plain_c():
+    # no torch / C++ types across the boundary: the .so must not link libtorch
+    import subprocess
+    out = subprocess.run(["ldd", str(_lib.LIB_PATH)], capture_output=True, text=True).stdout
+    assert "libtorch" not in out and "libc10" not in out
+
+
+def _rc(name, *args):
+    return getattr(_lib.load(), name)(*args)
+
+
+@pytest.mark.skipif(torch.cuda.is_available(),
+                    reason="fake pointers: validation-only test, never run where a launch could happen")
+def test_c_validation_paths_need_no_gpu():
+    lib = _lib.load()
+    fake = 0x1000  # never dereferenced: validation fails first
+    # unsupported dtype
+    rc = _rc("npd_paged_kv_store", fake, fake, fake, fake, fake, fake, 4, 2, 128, 16, 16, 4, 512,
+             128, 7, None)
+    assert rc == -2 and b"dtype" in lib.npd_last_error()
+    # bad head dim
+    rc = _rc("npd_paged_kv_store", fake, fake, fake, fake, fake, fake, 4, 2, 96, 16, 16, 4, 384,
+             96, 1, None)
+    assert rc == -1 and b"head_dim" in lib.npd_last_error()
+    # misaligned pointer
+    rc = _rc("npd_paged_kv_store", fake + 2, fake, fake, fake, fake, fake, 4, 2, 128, 16, 16, 4,
+             512, 128, 1, None)
+    assert rc == -3
+    # odd stride
+    rc = _rc("npd_paged_kv_store_slots", fake, fake, fake, fake, fake, 4, 2, 128, 16, 16, 130,
+             260, 1, None)
+    assert rc == -3
+    # heads not a multiple of kv heads
+    rc = _rc("npd_paged_attention", fake, fake, fake, fake, fake, fake, 2, 12, 5, 128, 64, 16, 4,
+             ctypes.c_float(0.1), 1536, 128, 1536, 128, None, 0, 1, None)
+    assert rc == -1 and b"multiple" in lib.npd_last_error()
+    # group > 8
+    rc = _rc("npd_paged_attention", fake, fake, fake, fake, fake, fake, 2, 32, 2, 128, 64, 16, 4,
+             ctypes.c_float(0.1), 4096, 128, 4096, 128, None, 0, 1, None)
+    assert rc == -1
+    # workspace required for a long context and missing
+    rc = _rc("npd_paged_attention", fake, fake, fake, fake, fake, fake, 2, 32, 8, 128, 4096, 16,
+             256, ctypes.c_float(0.1), 4096, 128, 4096, 128, None, 0, 1, None)
+    assert rc == -4 and b"workspace" in lib.npd_last_error()
+    # zero work is a no-op, not an error
+    assert _rc("npd_paged_attention", 0, 0, 0, 0, 0, 0, 0, 32, 8, 128, 4096, 16, 256,
+               ctypes.c_float(0.1), 4096, 128, 4096, 128, None, 0, 1, None) == 0
+    assert _rc("npd_copy_blocks", fake, fake, fake, 0, 10, 1024, 1, None) == 0
+    assert _rc("npd_copy_blocks", fake, fake, fake, 3, 10, 1004, 1, None) == -3
+    assert _rc("npd_pack_metadata", fake, fake, 5000, 1, 1, 4, 16, fake, fake, fake, fake, fake,
+               fake, None) == -1
+
+
+def test_workspace_size():
+    lib = _lib.load()
+    assert lib.npd_paged_attention_workspace_size(64, 32, 128, 16, 16) == 0   # 256 tokens
+    n = lib.npd_paged_attention_workspace_size(8, 32, 128, 16, 2048)          # 32k tokens
+    assert n == 8 * 32 * 128 * (128 + 2) * 4
+
+
+def test_python_mirror_raises_like_torch_check():
+    q = torch.zeros(2, 4, 64, dtype=torch.float16)
+    kc = torch.zeros(4, 4, 8, 64, dtype=torch.float16)
+    bt = torch.zeros(2, 1, dtype=torch.int32)
+    sl = torch.ones(2, dtype=torch.int32)
+    out = torch.zeros_like(q)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        pk.paged_attention_forward(out, q, kc, kc, bt, sl, 0.1, 8, 1)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        pk.paged_kv_store(kc, kc, q, q, bt, sl)
+    with pytest.raises(RuntimeError):
+        pk.paged_prefill_attention(out, q, kc, kc, bt, torch.zeros(3, dtype=torch.int32), sl,
+                                   0.1, 8, 1, 1)

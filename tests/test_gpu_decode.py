@@ -1,0 +1,198 @@
+"""GPU parity of paged decode attention against the float64 oracle.
+
+Tolerance (max-abs, output vs oracle): 2e-3 for fp16, 1e-2 for bf16 -- the
+bar of the task, tighter than the reference tests' atol=rtol=1e-2
+(PA/tests/test_paged_attention.py:144). Cases restate the reference list
+(PA/tests/test_paged_attention.py:127-247) and add the measured configurations
+and properties (permutation invariance, seq_len 0/1, CoW fork, strided query,
+every group size and head dim the kernel instantiates)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from nanopd_amd import paged_kernels as pk
+from nanopd_amd import workloads
+from oracle import paged_oracle as O
+from tests.helpers import ATOL, bits, f32, max_abs, oracle_decode, sha
+
+pytestmark = pytest.mark.gpu
+
+
+def make_inputs(num_seqs, num_heads, num_kv_heads, head_size, seq_lens, block_size, dtype,
+                device, seed=42, shuffle=True):
+    """Like make_inputs of PA/tests/test_paged_attention.py:78-110, with values
+    drawn on the CPU and (optionally) a shuffled block order."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    nbs = [(s + block_size - 1) // block_size for s in seq_lens]
+    mb, total = max(nbs), sum(nbs)
+    q = torch.randn(num_seqs, num_heads, head_size, generator=g).to(dtype)
+    kc = torch.randn(total, num_kv_heads, block_size, head_size, generator=g).to(dtype)
+    vc = torch.randn(total, num_kv_heads, block_size, head_size, generator=g).to(dtype)
+    order = torch.randperm(total, generator=g) if shuffle else torch.arange(total)
+    bt = torch.zeros(num_seqs, mb, dtype=torch.int32)
+    o = 0
+    for i, n in enumerate(nbs):
+        bt[i, :n] = order[o:o + n]
+        o += n
+    sl = torch.tensor(seq_lens, dtype=torch.int32)
+    return (q.to(device), kc.to(device), vc.to(device), bt.to(device), sl.to(device),
+            1.0 / math.sqrt(head_size), mb)
+
+
+def run(q, kc, vc, bt, sl, scale, mb, bs):
+    out = torch.full_like(q, float("nan"))   # the op must overwrite every element
+    pk.paged_attention_forward(out, q, kc, vc, bt, sl, scale, bs, mb)
+    torch.cuda.synchronize()
+    return out
+
+
+def check(out, q, kc, vc, bt, sl, scale):
+    want = oracle_decode(q, kc, vc, bt, sl, scale)
+    err = max_abs(out, want)
+    assert np.isfinite(f32(out)).all()
+    assert err <= ATOL[q.dtype], f"max-abs {err}"
+    return err
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_single_seq_single_head(device, dtype):
+    args = make_inputs(1, 1, 1, 64, [8], 16, dtype, device)
+    q, kc, vc, bt, sl, scale, mb = args
+    check(run(*args, 16), q, kc, vc, bt, sl, scale)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_multi_seq(device, dtype):
+    args = make_inputs(3, 4, 4, 64, [4, 8, 12], 8, dtype, device)
+    q, kc, vc, bt, sl, scale, mb = args
+    check(run(*args, 8), q, kc, vc, bt, sl, scale)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_gqa(device, dtype):
+    args = make_inputs(2, 8, 2, 64, [16, 8], 8, dtype, device)
+    q, kc, vc, bt, sl, scale, mb = args
+    check(run(*args, 8), q, kc, vc, bt, sl, scale)
+
+
+@pytest.mark.parametrize("seq_len", [1, 7, 8, 9, 15, 16, 17, 32, 255, 256, 257, 511, 512, 513])
+def test_various_seq_lens(device, seq_len):
+    args = make_inputs(1, 4, 4, 64, [seq_len], 8, torch.float16, device)
+    q, kc, vc, bt, sl, scale, mb = args
+    check(run(*args, 8), q, kc, vc, bt, sl, scale)
+
+
+@pytest.mark.parametrize("block_size", [4, 8, 16, 32])
+def test_various_block_sizes(device, block_size):
+    args = make_inputs(2, 4, 4, 64, [24, 16], block_size, torch.float16, device)
+    q, kc, vc, bt, sl, scale, mb = args
+    check(run(*args, block_size), q, kc, vc, bt, sl, scale)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("G", [1, 2, 3, 4, 5, 6, 7, 8])
+def test_group_sizes_and_head_dims(device, dtype, D, G):
+    kvh = 2
+    args = make_inputs(3, G * kvh, kvh, D, [1, 300, 1100], 16, dtype, device, seed=G * D)
+    q, kc, vc, bt, sl, scale, mb = args
+    check(run(*args, 16), q, kc, vc, bt, sl, scale)
+
+
+def test_output_shape_and_int64_tables_raise(device):
+    args = make_inputs(4, 8, 8, 128, [10] * 4, 16, torch.float16, device)
+    q, kc, vc, bt, sl, scale, mb = args
+    out = run(*args, 16)
+    assert out.shape == (4, 8, 128)
+    with pytest.raises(RuntimeError):
+        pk.paged_attention_forward(torch.zeros_like(q), q, kc, vc, bt.to(torch.int64), sl, scale,
+                                   16, mb)
+
+
+def test_seq_len_zero_and_one(device):
+    args = make_inputs(3, 8, 2, 128, [1, 40, 1], 16, torch.bfloat16, device)
+    q, kc, vc, bt, sl, scale, mb = args
+    sl = torch.tensor([1, 0, 1], dtype=torch.int32, device=device)
+    out = run(q, kc, vc, bt, sl, scale, mb, 16)
+    assert torch.count_nonzero(out[1]) == 0
+    for s in (0, 2):   # one token: the output is that token's value row, exactly
+        for h in range(8):
+            assert torch.equal(out[s, h], vc[bt[s, 0], h // 4, 0])
+
+
+def test_block_table_permutation_is_bit_invariant(device):
+    args = make_inputs(4, 32, 8, 128, [100, 700, 1500, 3000], 16, torch.bfloat16, device, seed=3)
+    q, kc, vc, bt, sl, scale, mb = args
+    a = run(q, kc, vc, bt, sl, scale, mb, 16)
+    perm = torch.randperm(kc.size(0), generator=torch.Generator().manual_seed(5)).to(device)
+    kc2, vc2 = torch.empty_like(kc), torch.empty_like(vc)
+    kc2[perm] = kc
+    vc2[perm] = vc
+    b = run(q, kc2, vc2, perm[bt.long()].to(torch.int32), sl, scale, mb, 16)
+    assert torch.equal(a, b)
+
+
+def test_strided_query_and_out(device):
+    args = make_inputs(5, 16, 4, 128, [33, 64, 65, 400, 2000], 16, torch.bfloat16, device, seed=11)
+    q, kc, vc, bt, sl, scale, mb = args
+    # (H, S, D) storage viewed as (S, H, D): strides (D, S*D, 1)
+    qt = q.transpose(0, 1).contiguous().transpose(0, 1)
+    out = torch.full((16, 5, 128), float("nan"), dtype=q.dtype, device=device).transpose(0, 1)
+    pk.paged_attention_forward(out, qt, kc, vc, bt, sl, scale, 16, mb)
+    torch.cuda.synchronize()
+    check(out, q, kc, vc, bt, sl, scale)
+
+
+def test_tiny_golden_vector(device):
+    gold = np.load("tests/golden/tiny.npz")
+    t = lambda a: torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).to(device)  # noqa: E731
+    q, kc, vc = t(gold["q"]), t(gold["k_cache"]), t(gold["v_cache"])
+    bt = torch.from_numpy(gold["block_tables"]).to(device)
+    sl = torch.from_numpy(gold["seq_lens"]).to(device)
+    out = run(q, kc, vc, bt, sl, float(gold["scale"]), bt.size(1), kc.size(2))
+    assert max_abs(out, gold["out"]) <= ATOL[torch.bfloat16]
+
+
+def test_config1_store_then_decode_matches_golden(device):
+    w = workloads.config1(device)
+    gold = np.load("tests/golden/cfg1.npz")
+    assert sha(bits(w.query), bits(w.store_k), bits(w.store_v), w.block_tables.cpu().numpy(),
+               w.store_positions.cpu().numpy()) == str(gold["inputs_sha"])
+    pk.paged_kv_store(w.k_cache, w.v_cache, w.store_k, w.store_v, w.store_tables, w.store_positions)
+    out = run(w.query, w.k_cache, w.v_cache, w.block_tables, w.seq_lens, w.scale,
+              w.max_blocks_per_seq, w.block_size)
+    want = O.bits_to_f32(gold["out_bits"], "f16").astype(np.float64)
+    # the golden output is itself rounded to fp16: allow one extra half-ulp
+    assert max_abs(out, want) <= ATOL[torch.float16] + 2 ** -11
+    check(out, w.query, w.k_cache, w.v_cache, w.block_tables, w.seq_lens, w.scale)
+
+
+def test_config2_store_then_decode(device):
+    w = workloads.config2(device)
+    pk.paged_kv_store(w.k_cache, w.v_cache, w.store_k, w.store_v, w.store_tables, w.store_positions)
+    out = run(w.query, w.k_cache, w.v_cache, w.block_tables, w.seq_lens, w.scale,
+              w.max_blocks_per_seq, w.block_size)
+    err = check(out, w.query, w.k_cache, w.v_cache, w.block_tables, w.seq_lens, w.scale)
+    print(f"cfg2 max-abs {err:.2e}")
+
+
+def test_config4_long_context_with_cow_fork(device):
+    w = workloads.config4(device)
+    pk.paged_kv_store(w.k_cache, w.v_cache, w.store_k, w.store_v, w.store_tables, w.store_positions)
+    pk.copy_blocks(w.k_cache, w.v_cache, w.cow_pairs)
+    out = run(w.query, w.k_cache, w.v_cache, w.block_tables, w.seq_lens, w.scale,
+              w.max_blocks_per_seq, w.block_size)
+    for (src, dst) in w.cow_pairs:
+        assert torch.equal(w.k_cache[src], w.k_cache[dst]) and torch.equal(w.v_cache[src], w.v_cache[dst])
+    # children (rows 8, 9) read a copied last block: identical to their parents
+    assert torch.equal(out[8], out[6]) and torch.equal(out[9], out[7])
+    # oracle on a subset (the two shortest and the two longest parents)
+    idx = [0, 1, 6, 7]
+    sub = lambda t: t[idx]  # noqa: E731
+    want = oracle_decode(sub(w.query), w.k_cache, w.v_cache, sub(w.block_tables),
+                         sub(w.seq_lens), w.scale)
+    err = max_abs(out[idx], want)
+    print(f"cfg4 max-abs {err:.2e}")
+    assert err <= ATOL[torch.bfloat16]
