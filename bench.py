@@ -91,7 +91,7 @@ def bench_decode(args, w) -> dict:
     dev = w.k_cache.device
     out = torch.empty_like(w.query)
     ws = torch.empty(max(1, pk.attention_workspace_bytes(
-        w.num_seqs, w.num_heads, w.head_dim, w.block_size, w.max_blocks_per_seq)),
+        w.num_seqs, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size, w.max_blocks_per_seq)),
         dtype=torch.uint8, device=dev)
 
     def store():

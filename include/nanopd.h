@@ -92,8 +92,8 @@ int npd_paged_kv_store_slots(void* k_cache, void* v_cache,
  * context partials). 0 means no workspace is needed.
  */
 int64_t npd_paged_attention_workspace_size(int64_t num_seqs, int64_t num_heads,
-                                           int64_t head_dim, int64_t block_size,
-                                           int64_t max_blocks_per_seq);
+                                           int64_t num_kv_heads, int64_t head_dim,
+                                           int64_t block_size, int64_t max_blocks_per_seq);
 
 /*
  * Paged decode attention (one query token per sequence).

@@ -27,7 +27,7 @@ SIGNATURES = {
                                           _I64, _I64, _I64, _I32, _P]),
     "npd_paged_kv_store_slots": (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
                                                 _I64, _I64, _I32, _P]),
-    "npd_paged_attention_workspace_size": (_I64, [_I64, _I64, _I64, _I64, _I64]),
+    "npd_paged_attention_workspace_size": (_I64, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "npd_paged_attention": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
                                            _I64, _I64, _F, _I64, _I64, _I64, _I64, _P, _I64, _I32,
                                            _P]),

@@ -300,6 +300,287 @@ __global__ __launch_bounds__(64) void decode_partition_kernel(DecodeArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Fast path: head_dim 128, block_size a multiple of 16 (<= 256).
+//
+// Same work unit and passes as decode_partition_kernel, with the per-step
+// cost cut down:
+//   * a step is 16 tokens inside one block, so the block id is one readlane
+//     per step and every lane's load offsets are loop constants;
+//   * the reduce-scatter of the q.k partial sums uses DPP only: partners are
+//     lane^8 (row_ror:8), lane^7 (row_half_mirror), lane^2, lane^1
+//     (quad_perm), and each lane stores its (token, head) slots XOR-permuted by
+//     a lane mask (chosen so that at every stage the half a lane keeps is its
+//     lower half). The permutation costs nothing at run time: it only changes
+//     which token a lane loads into each slot and which head each q slot holds.
+//     One v_add_f32_dpp per value per stage, no selects.
+// ---------------------------------------------------------------------------
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
+                                                               CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppRor8 = 0x128;        // row_ror:8      -> lane ^ 8 within a row of 16
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror -> lane ^ 7 within 8
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
+
+// Storage-permutation mask of lane j (0..15) for a butterfly over nb storage
+// bits. The stage masks m = (8, 7, 2, 1) form a basis of GF(2)^4; the mask is
+// the linear map sending m_s to storage bit nb - s. Writing j in that basis
+// gives coordinates a1 = j3, a2 = j2, a3 = j1 ^ j2, a4 = j0 ^ j2.
+__device__ __forceinline__ int butterfly_mask(int j, int nb) {
+  const int a1 = (j >> 3) & 1, a2 = (j >> 2) & 1;
+  const int a3 = ((j >> 1) & 1) ^ a2, a4 = (j & 1) ^ a2;
+  int m = 0;
+  if (nb >= 1) m |= a1 << (nb - 1);
+  if (nb >= 2) m |= a2 << (nb - 2);
+  if (nb >= 3) m |= a3 << (nb - 3);
+  if (nb >= 4) m |= a4 << (nb - 4);
+  return m;
+}
+
+template <int NV, int HALF, int CTRL>
+__device__ __forceinline__ void bfly_stage(float* v) {
+  if constexpr (HALF >= 1) {
+#pragma unroll
+    for (int p = 0; p < HALF; ++p) v[p] += dpp<CTRL>(v[p + HALF]);
+  } else {
+    v[0] += dpp<CTRL>(v[0]);
+  }
+}
+
+template <class TT, int G, int SPB>
+__global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
+  constexpr int D = 128;
+  constexpr int GP = pow2ceil(G);
+  constexpr int LGP = ilog2(GP);
+  constexpr int NV = 4 * GP;            // 4 token slots x GP head slots
+  constexpr int NB = ilog2(NV);
+  constexpr int NH = NB < 4 ? NB : 4;   // halving stages
+  constexpr int HELD = NV >> NH;
+  constexpr int BS = 16 * SPB;
+
+  __shared__ __attribute__((aligned(16))) float s_p[kMaxPartition * GP];
+
+  const int lane = threadIdx.x;
+  const int r = lane >> 4, j = lane & 15;
+  const int unit = blockIdx.x;
+  const int s = unit / a.num_kv_heads;
+  const int kh = unit - s * a.num_kv_heads;
+  const int part = blockIdx.y;
+
+  int ctx = a.seq_lens[s];
+  const int cap = a.max_bps * BS;
+  ctx = ctx < cap ? ctx : cap;
+  if (ctx <= 0) {
+    if (part == 0 && lane < 16) {
+      const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      for (int h = 0; h < G; ++h)
+        store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + j * 8, z, 0.f);
+    }
+    return;
+  }
+  const int nparts = (ctx + a.partition - 1) / a.partition;
+  if (part >= nparts) return;
+  const int t0 = part * a.partition;
+  const int ntok = (ctx - t0) < a.partition ? (ctx - t0) : a.partition;
+  const int nsteps = (ntok + 15) >> 4;
+  const int b0 = t0 / BS;
+
+  // lane e holds the block id of the e-th block of the partition (clamped)
+  int myblk = 0;
+  {
+    const int nb = (ntok + BS - 1) / BS;
+    if (lane < nb) {
+      int b = a.block_tables[(int64_t)s * a.max_bps + b0 + lane];
+      myblk = b < 0 ? 0 : (b >= a.num_blocks ? a.num_blocks - 1 : b);
+    }
+  }
+  const int mask = butterfly_mask(j, NB);
+  const int tokmask = mask >> LGP, headmask = mask & (GP - 1);
+
+  // q slot h holds head h ^ headmask of the group (zeros for padding heads)
+  u32x4 qv[GP];
+  {
+    const uint16_t* qb = a.q + s * a.q_stride_seq + (kh * G) * a.q_stride_head + j * 8;
+#pragma unroll
+    for (int h = 0; h < GP; ++h) {
+      const int hh = h ^ headmask;
+      qv[h] = hh < G ? *reinterpret_cast<const u32x4*>(qb + hh * a.q_stride_head) : u32x4{0, 0, 0, 0};
+    }
+  }
+  // 16-byte offsets of the lane's rows inside a step (pass 1: permuted slots)
+  int koff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) koff[i] = (((i ^ tokmask) * 4 + r) * 16) + j;
+  const int voff = (r * 16) + j;   // pass 3: slot i is token i*4 + r
+
+  const int64_t head_rows = (int64_t)kh * BS;            // rows of head kh in a block
+  const int64_t blk_rows = (int64_t)a.num_kv_heads * BS; // rows per block
+  auto step_base = [&](int st) -> int64_t {              // 16-byte index of the step's first row
+    const int blk = __builtin_amdgcn_readlane(myblk, st / SPB);
+    return ((int64_t)blk * blk_rows + head_rows + (st % SPB) * 16) * 16;
+  };
+
+  // ---------------- pass 1: scores ----------------
+  u32x4 kcur[4];
+  {
+    const u32x4* p = a.k_cache + step_base(0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kcur[i] = p[koff[i]];
+  }
+  for (int st = 0; st < nsteps; ++st) {
+    u32x4 knext[4];
+    if (st + 1 < nsteps) {
+      const u32x4* p = a.k_cache + step_base(st + 1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) knext[i] = p[koff[i]];
+    }
+    float v[NV];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int h = 0; h < GP; ++h) {
+        float d = TT::dot2(kcur[i].x, qv[h].x, 0.f);
+        d = TT::dot2(kcur[i].y, qv[h].y, d);
+        d = TT::dot2(kcur[i].z, qv[h].z, d);
+        d = TT::dot2(kcur[i].w, qv[h].w, d);
+        v[i * GP + h] = d;
+      }
+    }
+    bfly_stage<NV, (NH >= 1 ? NV / 2 : 0), kDppRor8>(v);
+    bfly_stage<NV, (NH >= 2 ? NV / 4 : 0), kDppHalfMirror>(v);
+    bfly_stage<NV, (NH >= 3 ? NV / 8 : 0), kDppXor2>(v);
+    bfly_stage<NV, (NH >= 4 ? NV / 16 : 0), kDppXor1>(v);
+#pragma unroll
+    for (int e = 0; e < HELD; ++e) {
+      const int key = mask | e;
+      const int h = key & (GP - 1);
+      const int tl = st * 16 + (key >> LGP) * 4 + r;
+      if (h < G) s_p[tl * GP + h] = (tl < ntok) ? v[e] * a.scale_log2 : -INFINITY;
+    }
+    if (st + 1 < nsteps) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) kcur[i] = knext[i];
+    }
+  }
+
+  u32x4 vcur[4];
+  {
+    const u32x4* p = a.v_cache + step_base(0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vcur[i] = p[voff + i * 64];
+  }
+  __syncthreads();
+
+  // ---------------- pass 2: softmax statistics over the partition ----------------
+  float m[GP], l[GP];
+#pragma unroll
+  for (int h = 0; h < GP; ++h) { m[h] = -INFINITY; l[h] = 0.f; }
+  const int ntl = nsteps * 16;
+  for (int t = lane; t < ntl; t += 64) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) m[h] = fmaxf(m[h], s_p[t * GP + h]);
+  }
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int x = 1; x < 64; x <<= 1) m[h] = fmaxf(m[h], shfl_xor(m[h], x));
+  for (int t = lane; t < ntl; t += 64) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float p = __builtin_amdgcn_exp2f(s_p[t * GP + h] - m[h]);
+      s_p[t * GP + h] = p;
+      l[h] += p;
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int x = 1; x < 64; x <<= 1) l[h] += shfl_xor(l[h], x);
+  __syncthreads();
+
+  // ---------------- pass 3: probabilities x V ----------------
+  float acc[G][8];
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int d = 0; d < 8; ++d) acc[h][d] = 0.f;
+  for (int st = 0; st < nsteps; ++st) {
+    u32x4 vnext[4];
+    if (st + 1 < nsteps) {
+      const u32x4* p = a.v_cache + step_base(st + 1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vnext[i] = p[voff + i * 64];
+    }
+    if (st * 16 + 16 > ntok) {   // tail step: rows past the context may hold anything
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (st * 16 + i * 4 + r >= ntok) vcur[i] = u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tl = st * 16 + i * 4 + r;
+      float p[GP];
+      if constexpr (GP >= 4) {
+#pragma unroll
+        for (int h4 = 0; h4 < GP; h4 += 4) {
+          const f32x4 pv = *reinterpret_cast<const f32x4*>(&s_p[tl * GP + h4]);
+          p[h4] = pv.x; p[h4 + 1] = pv.y; p[h4 + 2] = pv.z; p[h4 + 3] = pv.w;
+        }
+      } else {
+#pragma unroll
+        for (int h = 0; h < GP; ++h) p[h] = s_p[tl * GP + h];
+      }
+      const uint32_t w[4] = {vcur[i].x, vcur[i].y, vcur[i].z, vcur[i].w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float f0 = TT::lo(w[c]), f1 = TT::hi(w[c]);
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+          acc[h][2 * c] = fmaf(p[h], f0, acc[h][2 * c]);
+          acc[h][2 * c + 1] = fmaf(p[h], f1, acc[h][2 * c + 1]);
+        }
+      }
+    }
+    if (st + 1 < nsteps) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vcur[i] = vnext[i];
+    }
+  }
+#pragma unroll
+  for (int x = 16; x < 64; x <<= 1)
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc[h][d] += shfl_xor(acc[h][d], x);
+
+  if (lane >= 16) return;
+  if (nparts == 1) {
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+      store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + j * 8,
+                     acc[h], 1.f / l[h]);
+  } else {
+    const int64_t base = (int64_t)unit * a.max_parts + part;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      f32x4* dst = reinterpret_cast<f32x4*>(a.part_acc + ((base * G + h) * D + j * 8));
+      dst[0] = f32x4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
+      dst[1] = f32x4{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
+    }
+    if (j == 0) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        a.part_ml[(base * G + h) * 2] = m[h];
+        a.part_ml[(base * G + h) * 2 + 1] = l[h];
+      }
+    }
+  }
+}
+
 // Log-sum-exp merge of the partitions of each (sequence, kv-head) with more
 // than one partition (formula of paged_attention_optimized.cu:185-217, in the
 // log2 domain used by the partition kernel):
@@ -340,17 +621,53 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(DecodeArgs a) {
   }
 }
 
-// Partition length: 512 tokens normally; 256 when that leaves too few waves to
-// fill 256 CUs. The workspace is always sized for the smaller partition.
-int choose_partition(int64_t num_seqs, int64_t num_kv_heads, int64_t max_ctx) {
-  const int64_t waves512 = num_seqs * num_kv_heads * ((max_ctx + 511) / 512);
-  return waves512 >= 4096 ? 512 : 256;
+bool use_fast_path(int64_t head_dim, int64_t block_size) {
+  return head_dim == 128 && block_size % 16 == 0 && block_size <= 256 &&
+         (block_size & (block_size - 1)) == 0;
+}
+
+// Partition length (tokens per wave). The fast path takes the largest of
+// 256 / 128 / 64 that still gives >= 4096 waves for the longest context (256
+// CUs x 16 resident waves), never below the block size; the generic path uses
+// 512 or 256. The workspace is sized with the same rule.
+int choose_partition(int64_t num_seqs, int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
+                     int64_t max_ctx) {
+  const int64_t units = num_seqs * num_kv_heads;
+  if (use_fast_path(head_dim, block_size)) {
+    for (int ps = 256; ps >= 64; ps >>= 1) {
+      if (ps <= block_size) return (int)block_size;
+      if (units * ((max_ctx + ps - 1) / ps) >= 4096) return ps;
+    }
+    return block_size > 64 ? (int)block_size : 64;
+  }
+  return units * ((max_ctx + 511) / 512) >= 4096 ? 512 : 256;
+}
+
+template <class TT, int G>
+void launch_fast(const DecodeArgs& a, int64_t units, hipStream_t st) {
+  const dim3 grid((unsigned)units, (unsigned)a.max_parts);
+  switch (a.block_size) {
+    case 16: hipLaunchKernelGGL((decode_d128_kernel<TT, G, 1>), grid, dim3(64), 0, st, a); break;
+    case 32: hipLaunchKernelGGL((decode_d128_kernel<TT, G, 2>), grid, dim3(64), 0, st, a); break;
+    case 64: hipLaunchKernelGGL((decode_d128_kernel<TT, G, 4>), grid, dim3(64), 0, st, a); break;
+    case 128: hipLaunchKernelGGL((decode_d128_kernel<TT, G, 8>), grid, dim3(64), 0, st, a); break;
+    default: hipLaunchKernelGGL((decode_d128_kernel<TT, G, 16>), grid, dim3(64), 0, st, a); break;
+  }
 }
 
 template <class TT, int D, int G>
 int launch_decode(const DecodeArgs& a, int64_t units, hipStream_t st) {
-  hipLaunchKernelGGL((decode_partition_kernel<TT, D, G>), dim3((unsigned)units, (unsigned)a.max_parts),
-                     dim3(64), 0, st, a);
+  if constexpr (D == 128) {
+    if (use_fast_path(D, a.block_size)) {
+      launch_fast<TT, G>(a, units, st);
+    } else {
+      hipLaunchKernelGGL((decode_partition_kernel<TT, D, G>),
+                         dim3((unsigned)units, (unsigned)a.max_parts), dim3(64), 0, st, a);
+    }
+  } else {
+    hipLaunchKernelGGL((decode_partition_kernel<TT, D, G>),
+                       dim3((unsigned)units, (unsigned)a.max_parts), dim3(64), 0, st, a);
+  }
   if (a.max_parts > 1)
     hipLaunchKernelGGL((merge_partitions_kernel<TT, D, G>), dim3((unsigned)units), dim3(256), 0, st, a);
   return npd::check_launch("npd_paged_attention");
@@ -382,12 +699,15 @@ int dispatch_d(int64_t d, int g, const DecodeArgs& a, int64_t units, hipStream_t
 }  // namespace
 
 extern "C" int64_t npd_paged_attention_workspace_size(int64_t num_seqs, int64_t num_heads,
-                                                      int64_t head_dim, int64_t block_size,
+                                                      int64_t num_kv_heads, int64_t head_dim,
+                                                      int64_t block_size,
                                                       int64_t max_blocks_per_seq) {
-  if (num_seqs <= 0 || num_heads <= 0 || head_dim <= 0 || block_size <= 0 || max_blocks_per_seq <= 0)
+  if (num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
+      max_blocks_per_seq <= 0)
     return 0;
   const int64_t max_ctx = block_size * max_blocks_per_seq;
-  const int64_t parts = (max_ctx + 255) / 256;
+  const int ps = choose_partition(num_seqs, num_kv_heads, head_dim, block_size, max_ctx);
+  const int64_t parts = (max_ctx + ps - 1) / ps;
   if (parts <= 1) return 0;
   return num_seqs * num_heads * parts * (head_dim + 2) * (int64_t)sizeof(float);
 }
@@ -436,11 +756,14 @@ extern "C" int npd_paged_attention(void* out, const void* query, const void* key
     return fail(NPD_E_ALIGN, "%s: out/query/cache pointers must be 16-byte aligned", name);
 
   const int64_t max_ctx = block_size * max_blocks_per_seq;
-  const int partition = choose_partition(num_seqs, num_kv_heads, max_ctx);
+  const int partition = choose_partition(num_seqs, num_kv_heads, head_dim, block_size, max_ctx);
+  if (partition > kMaxPartition)
+    return fail(NPD_E_INVALID, "%s: block_size %lld is above %d", name, (long long)block_size,
+                kMaxPartition);
   const int64_t max_parts = (max_ctx + partition - 1) / partition;
   if (max_parts > 65535) return fail(NPD_E_INVALID, "%s: context too long", name);
-  const int64_t need = npd_paged_attention_workspace_size(num_seqs, num_heads, head_dim,
-                                                          block_size, max_blocks_per_seq);
+  const int64_t need = npd_paged_attention_workspace_size(num_seqs, num_heads, num_kv_heads,
+                                                          head_dim, block_size, max_blocks_per_seq);
   if (max_parts > 1) {
     if (!workspace || workspace_bytes < need)
       return fail(NPD_E_WORKSPACE, "%s: workspace of %lld bytes needed, %lld given", name,

@@ -164,10 +164,10 @@ def paged_kv_store_slots(k_cache: torch.Tensor, v_cache: torch.Tensor, k_src: to
 # Decode attention
 # ---------------------------------------------------------------------------
 
-def attention_workspace_bytes(num_seqs: int, num_heads: int, head_dim: int, block_size: int,
-                              max_num_blocks_per_seq: int) -> int:
+def attention_workspace_bytes(num_seqs: int, num_heads: int, num_kv_heads: int, head_dim: int,
+                              block_size: int, max_num_blocks_per_seq: int) -> int:
     return int(_lib.load().npd_paged_attention_workspace_size(
-        num_seqs, num_heads, head_dim, block_size, max_num_blocks_per_seq))
+        num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_num_blocks_per_seq))
 
 
 def paged_attention_forward(out: torch.Tensor, query: torch.Tensor, key_cache: torch.Tensor,
@@ -208,7 +208,7 @@ def paged_attention_forward(out: torch.Tensor, query: torch.Tensor, key_cache: t
     _check(query.stride(2) == 1 and out.stride(2) == 1, "head_dim must be the contiguous dim")
     if s == 0:
         return
-    need = attention_workspace_bytes(s, h, d, bs, mb)
+    need = attention_workspace_bytes(s, h, kvh, d, bs, mb)
     ws_ptr = 0
     if need > 0:
         if workspace is None or workspace.numel() * workspace.element_size() < need:
