@@ -90,7 +90,7 @@ def bench_decode(args, w) -> dict:
     from nanopd_amd import paged_kernels as pk
     dev = w.k_cache.device
     out = torch.empty_like(w.query)
-    ws = torch.empty(max(1, pk.attention_workspace_bytes(
+    ws = torch.zeros(max(1, pk.attention_workspace_bytes(
         w.num_seqs, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size, w.max_blocks_per_seq)),
         dtype=torch.uint8, device=dev)
 
@@ -122,9 +122,10 @@ def bench_decode(args, w) -> dict:
     ms_step = wall * 1e3 / args.steps
     attn_avg = statistics.mean(attn_ms)
     store_ms = statistics.median(_events_ms(store, 20))
-    # cold-cache variant: overwrite a 1 GiB buffer (> 256 MB MALL) before each call
-    flush_buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-    cold = statistics.mean(_events_ms(attend, 10, pre=lambda: flush_buf.fill_(1)))
+    # cold-cache variant: read a 1 GiB buffer (> 256 MB MALL + L2) before each
+    # call, so the KV rows come from HBM; a read leaves no dirty lines behind
+    flush_buf = torch.ones(1 << 28, dtype=torch.int32, device=dev)
+    cold = statistics.mean(_events_ms(attend, 10, pre=lambda: flush_buf.max()))
     del flush_buf
     step_bytes = w.attention_bytes() + w.store_bytes()
     achieved = w.attention_bytes() / (attn_avg * 1e-3) / 1e9

@@ -32,6 +32,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMaxPartition = 512;   // tokens per partition, upper bound (LDS sizing)
 constexpr int kStep = 16;            // tokens per step
+constexpr int kRing = 2;             // fast path: K/V steps in flight per wave
 constexpr float kLog2e = 1.4426950408889634f;
 
 constexpr int ilog2(int x) { return x <= 1 ? 0 : 1 + ilog2(x >> 1); }
@@ -59,6 +60,7 @@ struct DecodeArgs {
   const int32_t* seq_lens;
   float* part_acc;   // [S*kvh, max_parts, G, D]
   float* part_ml;    // [S*kvh, max_parts, G, 2]
+  int* counters;     // [S*kvh] arrival counters of the fused merge (zero between calls)
   int num_kv_heads;
   int block_size;
   int num_blocks;
@@ -68,6 +70,39 @@ struct DecodeArgs {
   float scale_log2;  // softmax scale * log2(e)
   int64_t q_stride_seq, q_stride_head, out_stride_seq, out_stride_head;
 };
+
+// Log-sum-exp merge of the partitions of one (sequence, kv-head) (formula of
+// PA/csrc/paged_attention_optimized/paged_attention_optimized.cu:185-217, in
+// the log2 domain used by the partition kernels):
+//   M = max_p m_p;  L = sum_p l_p 2^(m_p - M);  out = sum_p acc_p 2^(m_p - M) / L
+// Threads tid, tid+nthreads, ... each own one (head, 8-dim chunk).
+template <class TT, int D, int G>
+__device__ __forceinline__ void merge_unit(const DecodeArgs& a, int unit, int s, int kh, int nparts,
+                                           int tid, int nthreads) {
+  const int64_t base = (int64_t)unit * a.max_parts;
+  constexpr int CH = D / 8;  // 8-dim chunks per head
+  for (int idx = tid; idx < G * CH; idx += nthreads) {
+    const int h = idx / CH, c = idx % CH;
+    float M = -INFINITY;
+    for (int p = 0; p < nparts; ++p) M = fmaxf(M, a.part_ml[((base + p) * G + h) * 2]);
+    float L = 0.f;
+    float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int p = 0; p < nparts; ++p) {
+      const float mp = a.part_ml[((base + p) * G + h) * 2];
+      const float lp = a.part_ml[((base + p) * G + h) * 2 + 1];
+      const float w = __builtin_amdgcn_exp2f(mp - M);
+      L = fmaf(lp, w, L);
+      const f32x4* src = reinterpret_cast<const f32x4*>(a.part_acc + (((base + p) * G + h) * D + c * 8));
+      const f32x4 x0 = src[0], x1 = src[1];
+      o[0] = fmaf(x0.x, w, o[0]); o[1] = fmaf(x0.y, w, o[1]);
+      o[2] = fmaf(x0.z, w, o[2]); o[3] = fmaf(x0.w, w, o[3]);
+      o[4] = fmaf(x1.x, w, o[4]); o[5] = fmaf(x1.y, w, o[5]);
+      o[6] = fmaf(x1.z, w, o[6]); o[7] = fmaf(x1.w, w, o[7]);
+    }
+    store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + c * 8, o,
+                   1.f / L);
+  }
+}
 
 template <class TT, int D, int G>
 __global__ __launch_bounds__(64) void decode_partition_kernel(DecodeArgs a) {
@@ -361,6 +396,7 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
   constexpr int NH = NB < 4 ? NB : 4;   // halving stages
   constexpr int HELD = NV >> NH;
   constexpr int BS = 16 * SPB;
+  constexpr int NBUF = kRing;           // steps in flight per pass
 
   __shared__ __attribute__((aligned(16))) float s_p[kMaxPartition * GP];
 
@@ -386,18 +422,11 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
   if (part >= nparts) return;
   const int t0 = part * a.partition;
   const int ntok = (ctx - t0) < a.partition ? (ctx - t0) : a.partition;
-  const int nsteps = (ntok + 15) >> 4;
+  // steps rounded up to the ring size; steps past the context read block 0
+  // of the pool (always present) and are masked out
+  const int nsteps = (((ntok + 15) >> 4) + NBUF - 1) / NBUF * NBUF;
   const int b0 = t0 / BS;
 
-  // lane e holds the block id of the e-th block of the partition (clamped)
-  int myblk = 0;
-  {
-    const int nb = (ntok + BS - 1) / BS;
-    if (lane < nb) {
-      int b = a.block_tables[(int64_t)s * a.max_bps + b0 + lane];
-      myblk = b < 0 ? 0 : (b >= a.num_blocks ? a.num_blocks - 1 : b);
-    }
-  }
   const int mask = butterfly_mask(j, NB);
   const int tokmask = mask >> LGP, headmask = mask & (GP - 1);
 
@@ -411,6 +440,16 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
       qv[h] = hh < G ? *reinterpret_cast<const u32x4*>(qb + hh * a.q_stride_head) : u32x4{0, 0, 0, 0};
     }
   }
+  // lane e holds the block id of the e-th block of the partition (clamped);
+  // lanes past the partition hold block 0
+  int myblk = 0;
+  {
+    const int nb = (ntok + BS - 1) / BS;
+    if (lane < nb) {
+      int b = a.block_tables[(int64_t)s * a.max_bps + b0 + lane];
+      myblk = b < 0 ? 0 : (b >= a.num_blocks ? a.num_blocks - 1 : b);
+    }
+  }
   // 16-byte offsets of the lane's rows inside a step (pass 1: permuted slots)
   int koff[4];
 #pragma unroll
@@ -420,33 +459,31 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
   const int64_t head_rows = (int64_t)kh * BS;            // rows of head kh in a block
   const int64_t blk_rows = (int64_t)a.num_kv_heads * BS; // rows per block
   auto step_base = [&](int st) -> int64_t {              // 16-byte index of the step's first row
-    const int blk = __builtin_amdgcn_readlane(myblk, st / SPB);
+    const int blk = __builtin_amdgcn_readlane(myblk, (st / SPB) & 63);
     return ((int64_t)blk * blk_rows + head_rows + (st % SPB) * 16) * 16;
+  };
+  auto load_k = [&](u32x4* buf, int st) {
+    const u32x4* p = a.k_cache + step_base(st);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) buf[i] = p[koff[i]];
+  };
+  auto load_v = [&](u32x4* buf, int st) {
+    const u32x4* p = a.v_cache + step_base(st);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) buf[i] = p[voff + i * 64];
   };
 
   // ---------------- pass 1: scores ----------------
-  u32x4 kcur[4];
-  {
-    const u32x4* p = a.k_cache + step_base(0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) kcur[i] = p[koff[i]];
-  }
-  for (int st = 0; st < nsteps; ++st) {
-    u32x4 knext[4];
-    if (st + 1 < nsteps) {
-      const u32x4* p = a.k_cache + step_base(st + 1);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) knext[i] = p[koff[i]];
-    }
+  auto score_step = [&](const u32x4* kb, int st) {
     float v[NV];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
       for (int h = 0; h < GP; ++h) {
-        float d = TT::dot2(kcur[i].x, qv[h].x, 0.f);
-        d = TT::dot2(kcur[i].y, qv[h].y, d);
-        d = TT::dot2(kcur[i].z, qv[h].z, d);
-        d = TT::dot2(kcur[i].w, qv[h].w, d);
+        float d = TT::dot2(kb[i].x, qv[h].x, 0.f);
+        d = TT::dot2(kb[i].y, qv[h].y, d);
+        d = TT::dot2(kb[i].z, qv[h].z, d);
+        d = TT::dot2(kb[i].w, qv[h].w, d);
         v[i * GP + h] = d;
       }
     }
@@ -461,18 +498,28 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
       const int tl = st * 16 + (key >> LGP) * 4 + r;
       if (h < G) s_p[tl * GP + h] = (tl < ntok) ? v[e] * a.scale_log2 : -INFINITY;
     }
-    if (st + 1 < nsteps) {
+  };
+  {
+    // ring of NBUF steps in flight; the last round is peeled so the steady
+    // loop has no branches and each wait leaves the newer loads pending
+    u32x4 kb[NBUF][4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kcur[i] = knext[i];
+    for (int b = 0; b < NBUF; ++b) load_k(kb[b], b);
+    int st0 = 0;
+    for (; st0 + NBUF < nsteps; st0 += NBUF) {
+#pragma unroll
+      for (int b = 0; b < NBUF; ++b) {
+        score_step(kb[b], st0 + b);
+        load_k(kb[b], st0 + NBUF + b);
+      }
     }
+#pragma unroll
+    for (int b = 0; b < NBUF; ++b) score_step(kb[b], st0 + b);
   }
 
-  u32x4 vcur[4];
-  {
-    const u32x4* p = a.v_cache + step_base(0);
+  u32x4 vb[NBUF][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) vcur[i] = p[voff + i * 64];
-  }
+  for (int b = 0; b < NBUF; ++b) load_v(vb[b], b);
   __syncthreads();
 
   // ---------------- pass 2: softmax statistics over the partition ----------------
@@ -508,17 +555,11 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
   for (int h = 0; h < G; ++h)
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[h][d] = 0.f;
-  for (int st = 0; st < nsteps; ++st) {
-    u32x4 vnext[4];
-    if (st + 1 < nsteps) {
-      const u32x4* p = a.v_cache + step_base(st + 1);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) vnext[i] = p[voff + i * 64];
-    }
+  auto pv_step = [&](u32x4* vbuf, int st) {
     if (st * 16 + 16 > ntok) {   // tail step: rows past the context may hold anything
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (st * 16 + i * 4 + r >= ntok) vcur[i] = u32x4{0, 0, 0, 0};
+        if (st * 16 + i * 4 + r >= ntok) vbuf[i] = u32x4{0, 0, 0, 0};
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -534,7 +575,7 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
 #pragma unroll
         for (int h = 0; h < GP; ++h) p[h] = s_p[tl * GP + h];
       }
-      const uint32_t w[4] = {vcur[i].x, vcur[i].y, vcur[i].z, vcur[i].w};
+      const uint32_t w[4] = {vbuf[i].x, vbuf[i].y, vbuf[i].z, vbuf[i].w};
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const float f0 = TT::lo(w[c]), f1 = TT::hi(w[c]);
@@ -545,10 +586,18 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
         }
       }
     }
-    if (st + 1 < nsteps) {
+  };
+  {
+    int st0 = 0;
+    for (; st0 + NBUF < nsteps; st0 += NBUF) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vcur[i] = vnext[i];
+      for (int b = 0; b < NBUF; ++b) {
+        pv_step(vb[b], st0 + b);
+        load_v(vb[b], st0 + NBUF + b);
+      }
     }
+#pragma unroll
+    for (int b = 0; b < NBUF; ++b) pv_step(vb[b], st0 + b);
   }
 #pragma unroll
   for (int x = 16; x < 64; x <<= 1)
@@ -557,14 +606,20 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
 #pragma unroll
       for (int d = 0; d < 8; ++d) acc[h][d] += shfl_xor(acc[h][d], x);
 
-  if (lane >= 16) return;
   if (nparts == 1) {
+    if (lane < 16) {
 #pragma unroll
-    for (int h = 0; h < G; ++h)
-      store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + j * 8,
-                     acc[h], 1.f / l[h]);
-  } else {
-    const int64_t base = (int64_t)unit * a.max_parts + part;
+      for (int h = 0; h < G; ++h)
+        store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + j * 8,
+                       acc[h], 1.f / l[h]);
+    }
+    return;
+  }
+  // Several partitions: publish this one's partial, then the last wave of the
+  // (sequence, kv-head) to arrive merges them all and resets the counter.
+  const int64_t ubase = (int64_t)unit * a.max_parts;
+  if (lane < 16) {
+    const int64_t base = ubase + part;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
       f32x4* dst = reinterpret_cast<f32x4*>(a.part_acc + ((base * G + h) * D + j * 8));
@@ -579,12 +634,18 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
       }
     }
   }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  int ticket = 0;
+  if (lane == 0)
+    ticket = __hip_atomic_fetch_add(a.counters + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  ticket = __shfl(ticket, 0, 64);
+  if (ticket != nparts - 1) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  merge_unit<TT, D, G>(a, unit, s, kh, nparts, lane, 64);
+  if (lane == 0) __hip_atomic_store(a.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Log-sum-exp merge of the partitions of each (sequence, kv-head) with more
-// than one partition (formula of paged_attention_optimized.cu:185-217, in the
-// log2 domain used by the partition kernel):
-//   M = max_p m_p;  L = sum_p l_p 2^(m_p - M);  out = sum_p acc_p 2^(m_p - M) / L
+// Merge kernel for the generic path: one workgroup per (sequence, kv-head).
 template <class TT, int D, int G>
 __global__ __launch_bounds__(256) void merge_partitions_kernel(DecodeArgs a) {
   const int unit = blockIdx.x;
@@ -596,29 +657,7 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(DecodeArgs a) {
   if (ctx <= 0) return;
   const int nparts = (ctx + a.partition - 1) / a.partition;
   if (nparts <= 1) return;
-  const int64_t base = (int64_t)unit * a.max_parts;
-  constexpr int CH = D / 8;  // 8-dim chunks per head
-  for (int idx = threadIdx.x; idx < G * CH; idx += blockDim.x) {
-    const int h = idx / CH, c = idx % CH;
-    float M = -INFINITY;
-    for (int p = 0; p < nparts; ++p) M = fmaxf(M, a.part_ml[((base + p) * G + h) * 2]);
-    float L = 0.f;
-    float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int p = 0; p < nparts; ++p) {
-      const float mp = a.part_ml[((base + p) * G + h) * 2];
-      const float lp = a.part_ml[((base + p) * G + h) * 2 + 1];
-      const float w = exp2f(mp - M);
-      L = fmaf(lp, w, L);
-      const f32x4* src = reinterpret_cast<const f32x4*>(a.part_acc + (((base + p) * G + h) * D + c * 8));
-      const f32x4 x0 = src[0], x1 = src[1];
-      o[0] = fmaf(x0.x, w, o[0]); o[1] = fmaf(x0.y, w, o[1]);
-      o[2] = fmaf(x0.z, w, o[2]); o[3] = fmaf(x0.w, w, o[3]);
-      o[4] = fmaf(x1.x, w, o[4]); o[5] = fmaf(x1.y, w, o[5]);
-      o[6] = fmaf(x1.z, w, o[6]); o[7] = fmaf(x1.w, w, o[7]);
-    }
-    store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + c * 8, o,
-                   1.f / L);
-  }
+  merge_unit<TT, D, G>(a, unit, s, kh, nparts, threadIdx.x, blockDim.x);
 }
 
 bool use_fast_path(int64_t head_dim, int64_t block_size) {
@@ -660,6 +699,7 @@ int launch_decode(const DecodeArgs& a, int64_t units, hipStream_t st) {
   if constexpr (D == 128) {
     if (use_fast_path(D, a.block_size)) {
       launch_fast<TT, G>(a, units, st);
+      return npd::check_launch("npd_paged_attention");
     } else {
       hipLaunchKernelGGL((decode_partition_kernel<TT, D, G>),
                          dim3((unsigned)units, (unsigned)a.max_parts), dim3(64), 0, st, a);
@@ -709,7 +749,9 @@ extern "C" int64_t npd_paged_attention_workspace_size(int64_t num_seqs, int64_t 
   const int ps = choose_partition(num_seqs, num_kv_heads, head_dim, block_size, max_ctx);
   const int64_t parts = (max_ctx + ps - 1) / ps;
   if (parts <= 1) return 0;
-  return num_seqs * num_heads * parts * (head_dim + 2) * (int64_t)sizeof(float);
+  const int64_t partials = num_seqs * num_heads * parts * (head_dim + 2) * (int64_t)sizeof(float);
+  const int64_t counters = use_fast_path(head_dim, block_size) ? num_seqs * num_kv_heads * 4 : 0;
+  return partials + counters;
 }
 
 extern "C" int npd_paged_attention(void* out, const void* query, const void* key_cache,
@@ -783,6 +825,7 @@ extern "C" int npd_paged_attention(void* out, const void* query, const void* key
   float* ws = static_cast<float*>(workspace);
   a.part_acc = ws;
   a.part_ml = ws ? ws + units * max_parts * g * head_dim : nullptr;
+  a.counters = ws ? reinterpret_cast<int*>(a.part_ml + units * max_parts * g * 2) : nullptr;
   a.num_kv_heads = (int)num_kv_heads;
   a.block_size = (int)block_size;
   a.num_blocks = (int)num_blocks;

@@ -164,6 +164,22 @@ def paged_kv_store_slots(k_cache: torch.Tensor, v_cache: torch.Tensor, k_src: to
 # Decode attention
 # ---------------------------------------------------------------------------
 
+# Cached decode workspaces, one per (device, stream): zero-filled when made.
+# The fast decode path keeps per-(sequence, kv-head) arrival counters at the
+# end of the workspace and leaves them zero after every call, so a workspace
+# only has to be zeroed once; one per stream keeps concurrent streams apart.
+_workspaces: dict = {}
+
+
+def _decode_workspace(dev: torch.device, stream: int, need: int) -> torch.Tensor:
+    key = (dev.index, stream)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+        _workspaces[key] = ws
+    return ws
+
+
 def attention_workspace_bytes(num_seqs: int, num_heads: int, num_kv_heads: int, head_dim: int,
                               block_size: int, max_num_blocks_per_seq: int) -> int:
     return int(_lib.load().npd_paged_attention_workspace_size(
@@ -180,8 +196,9 @@ def paged_attention_forward(out: torch.Tensor, query: torch.Tensor, key_cache: t
     block_size, head_dim]; block_tables: int32 [num_seqs, max_num_blocks_per_seq];
     seq_lens: int32 [num_seqs], the number of cached tokens to attend over
     (including the token just stored). ``out`` is fully overwritten. An optional
-    uint8 ``workspace`` of at least :func:`attention_workspace_bytes` bytes
-    avoids a (cached) allocation per call.
+    uint8 ``workspace`` of at least :func:`attention_workspace_bytes` bytes,
+    zero-filled before its first use, replaces the cached per-stream one; calls
+    that share a workspace must run in stream order.
     """
     _check(isinstance(query, torch.Tensor) and query.is_cuda, "query is must be on CUDA")
     _check(query.dim() == 3, "query must be [num seqs, num_heads, head_size]")
@@ -209,15 +226,18 @@ def paged_attention_forward(out: torch.Tensor, query: torch.Tensor, key_cache: t
     if s == 0:
         return
     need = attention_workspace_bytes(s, h, kvh, d, bs, mb)
+    stream = _stream(dev)
     ws_ptr = 0
     if need > 0:
-        if workspace is None or workspace.numel() * workspace.element_size() < need:
-            workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+        if workspace is None:
+            workspace = _decode_workspace(dev, stream, need)
+        _check(workspace.numel() * workspace.element_size() >= need,
+               f"workspace of {need} bytes needed")
         ws_ptr = workspace.data_ptr()
     _lib.call("npd_paged_attention", out.data_ptr(), query.data_ptr(), key_cache.data_ptr(),
               value_cache.data_ptr(), block_tables.data_ptr(), seq_lens.data_ptr(), s, h, kvh, d,
               num_blocks, bs, mb, float(scale), query.stride(0), query.stride(1), out.stride(0),
-              out.stride(1), ws_ptr, need, code, _stream(dev))
+              out.stride(1), ws_ptr, need, code, stream)
 
 
 # ---------------------------------------------------------------------------
