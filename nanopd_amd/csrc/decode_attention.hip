@@ -32,7 +32,20 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMaxPartition = 512;   // tokens per partition, upper bound (LDS sizing)
 constexpr int kStep = 16;            // tokens per step
-constexpr int kRing = 2;             // fast path: K/V steps in flight per wave
+#ifndef NPD_DECODE_RING
+#define NPD_DECODE_RING 2
+#endif
+#ifndef NPD_DECODE_NT
+#define NPD_DECODE_NT 1
+#endif
+#ifndef NPD_DECODE_PV_DOT2
+#define NPD_DECODE_PV_DOT2 1
+#endif
+constexpr int kRing = NPD_DECODE_RING;   // fast path: K/V steps in flight per wave
+#ifndef NPD_FAST_MAX_PARTITION
+#define NPD_FAST_MAX_PARTITION 256
+#endif
+constexpr int kFastMaxPartition = NPD_FAST_MAX_PARTITION;   // fast path: tokens per wave, max
 constexpr float kLog2e = 1.4426950408889634f;
 
 constexpr int ilog2(int x) { return x <= 1 ? 0 : 1 + ilog2(x >> 1); }
@@ -60,7 +73,9 @@ struct DecodeArgs {
   const int32_t* seq_lens;
   float* part_acc;   // [S*kvh, max_parts, G, D]
   float* part_ml;    // [S*kvh, max_parts, G, 2]
-  int* counters;     // [S*kvh] arrival counters of the fused merge (zero between calls)
+  int* counters;     // [S*kvh] arrival counters of the fused merge
+  int* sched;        // fast path: [1] number of work items
+  int2* items;       // fast path: (unit, partition) work list
   int num_kv_heads;
   int block_size;
   int num_blocks;
@@ -76,7 +91,17 @@ struct DecodeArgs {
 // the log2 domain used by the partition kernels):
 //   M = max_p m_p;  L = sum_p l_p 2^(m_p - M);  out = sum_p acc_p 2^(m_p - M) / L
 // Threads tid, tid+nthreads, ... each own one (head, 8-dim chunk).
-template <class TT, int D, int G>
+// kCoherent: the partials were written by other waves of the running kernel;
+// read them with agent-scope atomic loads (they bypass this XCD's L2).
+template <bool kCoherent>
+__device__ __forceinline__ float ld_part(const float* p) {
+  if constexpr (kCoherent)
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    return *p;
+}
+
+template <class TT, int D, int G, bool kCoherent = false>
 __device__ __forceinline__ void merge_unit(const DecodeArgs& a, int unit, int s, int kh, int nparts,
                                            int tid, int nthreads) {
   const int64_t base = (int64_t)unit * a.max_parts;
@@ -84,20 +109,17 @@ __device__ __forceinline__ void merge_unit(const DecodeArgs& a, int unit, int s,
   for (int idx = tid; idx < G * CH; idx += nthreads) {
     const int h = idx / CH, c = idx % CH;
     float M = -INFINITY;
-    for (int p = 0; p < nparts; ++p) M = fmaxf(M, a.part_ml[((base + p) * G + h) * 2]);
+    for (int p = 0; p < nparts; ++p) M = fmaxf(M, ld_part<kCoherent>(a.part_ml + ((base + p) * G + h) * 2));
     float L = 0.f;
     float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int p = 0; p < nparts; ++p) {
-      const float mp = a.part_ml[((base + p) * G + h) * 2];
-      const float lp = a.part_ml[((base + p) * G + h) * 2 + 1];
+      const float mp = ld_part<kCoherent>(a.part_ml + ((base + p) * G + h) * 2);
+      const float lp = ld_part<kCoherent>(a.part_ml + ((base + p) * G + h) * 2 + 1);
       const float w = __builtin_amdgcn_exp2f(mp - M);
       L = fmaf(lp, w, L);
-      const f32x4* src = reinterpret_cast<const f32x4*>(a.part_acc + (((base + p) * G + h) * D + c * 8));
-      const f32x4 x0 = src[0], x1 = src[1];
-      o[0] = fmaf(x0.x, w, o[0]); o[1] = fmaf(x0.y, w, o[1]);
-      o[2] = fmaf(x0.z, w, o[2]); o[3] = fmaf(x0.w, w, o[3]);
-      o[4] = fmaf(x1.x, w, o[4]); o[5] = fmaf(x1.y, w, o[5]);
-      o[6] = fmaf(x1.z, w, o[6]); o[7] = fmaf(x1.w, w, o[7]);
+      const float* src = a.part_acc + (((base + p) * G + h) * D + c * 8);
+#pragma unroll
+      for (int d = 0; d < 8; ++d) o[d] = fmaf(ld_part<kCoherent>(src + d), w, o[d]);
     }
     store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + c * 8, o,
                    1.f / L);
@@ -342,13 +364,14 @@ __global__ __launch_bounds__(64) void decode_partition_kernel(DecodeArgs a) {
 // cost cut down:
 //   * a step is 16 tokens inside one block, so the block id is one readlane
 //     per step and every lane's load offsets are loop constants;
-//   * the reduce-scatter of the q.k partial sums uses DPP only: partners are
-//     lane^8 (row_ror:8), lane^7 (row_half_mirror), lane^2, lane^1
-//     (quad_perm), and each lane stores its (token, head) slots XOR-permuted by
-//     a lane mask (chosen so that at every stage the half a lane keeps is its
-//     lower half). The permutation costs nothing at run time: it only changes
-//     which token a lane loads into each slot and which head each q slot holds.
-//     One v_add_f32_dpp per value per stage, no selects.
+//   * the reduce-scatter of the q.k partial sums over the 16 lanes of a token
+//     row uses DPP: partners are lane^8 (row_ror:8), lane^7 (row_half_mirror),
+//     lane^2 and lane^1 (quad_perm). A lane's partial sums are indexed
+//     k = head_slot * 4 + token_slot. Stages on head bits need no selects: q
+//     slot h of a lane holds head h ^ hmask(lane), chosen so that at every such
+//     stage the half a lane keeps is its lower half (one v_add_f32_dpp per
+//     value). Stages on token bits pick the kept half with v_cndmask, so the K
+//     loads stay the coalesced layout of the V loads.
 // ---------------------------------------------------------------------------
 
 template <int CTRL>
@@ -361,33 +384,157 @@ constexpr int kDppHalfMirror = 0x141;  // row_half_mirror -> lane ^ 7 within 8
 constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
 constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
 
-// Storage-permutation mask of lane j (0..15) for a butterfly over nb storage
-// bits. The stage masks m = (8, 7, 2, 1) form a basis of GF(2)^4; the mask is
-// the linear map sending m_s to storage bit nb - s. Writing j in that basis
-// gives coordinates a1 = j3, a2 = j2, a3 = j1 ^ j2, a4 = j0 ^ j2.
-__device__ __forceinline__ int butterfly_mask(int j, int nb) {
-  const int a1 = (j >> 3) & 1, a2 = (j >> 2) & 1;
-  const int a3 = ((j >> 1) & 1) ^ a2, a4 = (j & 1) ^ a2;
-  int m = 0;
-  if (nb >= 1) m |= a1 << (nb - 1);
-  if (nb >= 2) m |= a2 << (nb - 2);
-  if (nb >= 3) m |= a3 << (nb - 3);
-  if (nb >= 4) m |= a4 << (nb - 4);
-  return m;
+// Coordinates of lane j (0..15) in the basis of the stage partner masks
+// m = (8, 7, 2, 1) of GF(2)^4: j = a1*8 ^ a2*7 ^ a3*2 ^ a4*1, so a1 = j3,
+// a2 = j2, a3 = j1 ^ j2, a4 = j0 ^ j2. At stage s the partner lane differs from
+// lane j in coordinate a_s only.
+__device__ __forceinline__ int bfly_coord(int j, int s) {
+  const int j2 = (j >> 2) & 1;
+  switch (s) {
+    case 1: return (j >> 3) & 1;
+    case 2: return j2;
+    case 3: return ((j >> 1) & 1) ^ j2;
+    default: return (j & 1) ^ j2;
+  }
 }
 
-template <int NV, int HALF, int CTRL>
-__device__ __forceinline__ void bfly_stage(float* v) {
-  if constexpr (HALF >= 1) {
+__device__ __forceinline__ u32x4 ld_stream(const u32x4* p) {
+#if NPD_DECODE_NT
+  return __builtin_nontemporal_load(p);
+#else
+  return *p;
+#endif
+}
+
+// One reduce-scatter stage over `cnt` values (cnt == 1: plain all-reduce).
+// kFree: the kept half is the lower one on every lane (head stages); else
+// `upper` picks it (token stages).
+template <int CNT, int CTRL, bool kFree>
+__device__ __forceinline__ void bfly_stage(float* v, bool upper) {
+  if constexpr (CNT >= 2) {
+    constexpr int HALF = CNT / 2;
 #pragma unroll
-    for (int p = 0; p < HALF; ++p) v[p] += dpp<CTRL>(v[p + HALF]);
+    for (int p = 0; p < HALF; ++p) {
+      if constexpr (kFree) {
+        v[p] += dpp<CTRL>(v[p + HALF]);
+      } else {
+        const float send = upper ? v[p] : v[p + HALF];
+        const float keep = upper ? v[p + HALF] : v[p];
+        v[p] = keep + dpp<CTRL>(send);
+      }
+    }
   } else {
     v[0] += dpp<CTRL>(v[0]);
   }
 }
 
+// Agent-scope relaxed atomic accesses: written through to, and read from, the
+// device-coherent level, so partials published by one XCD are seen by another
+// without L2 writeback/invalidate. 8-byte granularity.
+__device__ __forceinline__ void st_coherent2(float* p, float x, float y) {
+  const uint64_t v = (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ld_coherent2(const float* p, float& x, float& y) {
+  const uint64_t v = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+  x = __uint_as_float((uint32_t)v);
+  y = __uint_as_float((uint32_t)(v >> 32));
+}
+
+// Merge of one (sequence, kv-head) by a single wave (fast path, D = 128), the
+// same log-sum-exp merge as merge_unit but latency-bound work done in parallel:
+//   A: lanes take partitions, load (m, l) per head, and wave-reduce M and L;
+//   B: per chunk of 64 partitions, the weights 2^(m_p - M) go to LDS and each
+//      lane accumulates its (head, 8-dim chunk) with 4 partitions of loads in
+//      flight at a time.
+template <class TT, int G>
+__device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int unit, int s, int kh,
+                                                int nparts, int lane, float* s_w) {
+  constexpr int D = 128, GP = pow2ceil(G), CH = D / 8;
+  constexpr int OWN = (G * CH + 63) / 64;   // (head, chunk) pairs per lane
+  const int64_t base = (int64_t)unit * a.max_parts;
+  float M[G], L[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) { M[h] = -INFINITY; L[h] = 0.f; }
+  for (int p = lane; p < nparts; p += 64) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float mp, lp;
+      ld_coherent2(a.part_ml + ((base + p) * G + h) * 2, mp, lp);
+      M[h] = fmaxf(M[h], mp);
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int x = 1; x < 64; x <<= 1) M[h] = fmaxf(M[h], shfl_xor(M[h], x));
+  float o[OWN][8];
+#pragma unroll
+  for (int k = 0; k < OWN; ++k)
+#pragma unroll
+    for (int d = 0; d < 8; ++d) o[k][d] = 0.f;
+  for (int p0 = 0; p0 < nparts; p0 += 64) {
+    const int p = p0 + lane;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float w = 0.f;
+      if (p < nparts) {
+        float mp, lp;
+        ld_coherent2(a.part_ml + ((base + p) * G + h) * 2, mp, lp);
+        w = __builtin_amdgcn_exp2f(mp - M[h]);
+        L[h] = fmaf(lp, w, L[h]);
+      }
+      s_w[lane * GP + h] = w;
+    }
+    __syncthreads();
+    const int n = nparts - p0 < 64 ? nparts - p0 : 64;
+#pragma unroll
+    for (int k = 0; k < OWN; ++k) {
+      const int idx = lane + 64 * k;
+      if (idx < G * CH) {
+        const int h = idx / CH, c = idx % CH;
+        for (int q0 = 0; q0 < n; q0 += 4) {
+          float x[4][8];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            if (q0 + q < n) {
+              const float* src = a.part_acc + (((base + p0 + q0 + q) * G + h) * D + c * 8);
+#pragma unroll
+              for (int d = 0; d < 8; d += 2) ld_coherent2(src + d, x[q][d], x[q][d + 1]);
+            }
+          }
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            if (q0 + q < n) {
+              const float w = s_w[(q0 + q) * GP + h];
+#pragma unroll
+              for (int d = 0; d < 8; ++d) o[k][d] = fmaf(x[q][d], w, o[k][d]);
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int x = 1; x < 64; x <<= 1) L[h] += shfl_xor(L[h], x);
+#pragma unroll
+  for (int k = 0; k < OWN; ++k) {
+    const int idx = lane + 64 * k;
+    if (idx < G * CH) {
+      const int h = idx / CH, c = idx % CH;
+      store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + c * 8,
+                     o[k], 1.f / L[h]);
+    }
+  }
+}
+
 template <class TT, int G, int SPB>
-__global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
+__device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, int part,
+                                                 float* s_p, uint32_t* s_pp) {
   constexpr int D = 128;
   constexpr int GP = pow2ceil(G);
   constexpr int LGP = ilog2(GP);
@@ -397,15 +544,13 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
   constexpr int HELD = NV >> NH;
   constexpr int BS = 16 * SPB;
   constexpr int NBUF = kRing;           // steps in flight per pass
+  constexpr int MAXT = kFastMaxPartition + 16 * NBUF;   // tokens incl. ring padding
 
-  __shared__ __attribute__((aligned(16))) float s_p[kMaxPartition * GP];
-
+  (void)MAXT;
   const int lane = threadIdx.x;
   const int r = lane >> 4, j = lane & 15;
-  const int unit = blockIdx.x;
   const int s = unit / a.num_kv_heads;
   const int kh = unit - s * a.num_kv_heads;
-  const int part = blockIdx.y;
 
   int ctx = a.seq_lens[s];
   const int cap = a.max_bps * BS;
@@ -427,8 +572,14 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
   const int nsteps = (((ntok + 15) >> 4) + NBUF - 1) / NBUF * NBUF;
   const int b0 = t0 / BS;
 
-  const int mask = butterfly_mask(j, NB);
-  const int tokmask = mask >> LGP, headmask = mask & (GP - 1);
+  // stages 1..LGP split head bits (q slots permuted by hmask), the next two
+  // split token bits (selects); see bfly_coord
+  int hmask = 0;
+#pragma unroll
+  for (int st = 1; st <= LGP && st <= 4; ++st) hmask |= bfly_coord(j, st) << (LGP - st);
+  const int headmask = hmask;
+  const bool tup1 = bfly_coord(j, LGP + 1) != 0;   // token bit 1 kept
+  const bool tup0 = bfly_coord(j, LGP + 2) != 0;   // token bit 0 kept
 
   // q slot h holds head h ^ headmask of the group (zeros for padding heads)
   u32x4 qv[GP];
@@ -450,11 +601,7 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
       myblk = b < 0 ? 0 : (b >= a.num_blocks ? a.num_blocks - 1 : b);
     }
   }
-  // 16-byte offsets of the lane's rows inside a step (pass 1: permuted slots)
-  int koff[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) koff[i] = (((i ^ tokmask) * 4 + r) * 16) + j;
-  const int voff = (r * 16) + j;   // pass 3: slot i is token i*4 + r
+  const int voff = (r * 16) + j;   // 16-byte offset of the lane's chunk: slot i is token i*4 + r
 
   const int64_t head_rows = (int64_t)kh * BS;            // rows of head kh in a block
   const int64_t blk_rows = (int64_t)a.num_kv_heads * BS; // rows per block
@@ -462,20 +609,22 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
     const int blk = __builtin_amdgcn_readlane(myblk, (st / SPB) & 63);
     return ((int64_t)blk * blk_rows + head_rows + (st % SPB) * 16) * 16;
   };
+  // K/V rows are read once per call: nontemporal loads keep them from
+  // displacing reusable lines in L2
   auto load_k = [&](u32x4* buf, int st) {
     const u32x4* p = a.k_cache + step_base(st);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) buf[i] = p[koff[i]];
+    for (int i = 0; i < 4; ++i) buf[i] = ld_stream(p + voff + i * 64);
   };
   auto load_v = [&](u32x4* buf, int st) {
     const u32x4* p = a.v_cache + step_base(st);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) buf[i] = p[voff + i * 64];
+    for (int i = 0; i < 4; ++i) buf[i] = ld_stream(p + voff + i * 64);
   };
 
   // ---------------- pass 1: scores ----------------
   auto score_step = [&](const u32x4* kb, int st) {
-    float v[NV];
+    float v[NV];   // v[h * 4 + i]: q slot h . token slot i
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -484,18 +633,25 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
         d = TT::dot2(kb[i].y, qv[h].y, d);
         d = TT::dot2(kb[i].z, qv[h].z, d);
         d = TT::dot2(kb[i].w, qv[h].w, d);
-        v[i * GP + h] = d;
+        v[h * 4 + i] = d;
       }
     }
-    bfly_stage<NV, (NH >= 1 ? NV / 2 : 0), kDppRor8>(v);
-    bfly_stage<NV, (NH >= 2 ? NV / 4 : 0), kDppHalfMirror>(v);
-    bfly_stage<NV, (NH >= 3 ? NV / 8 : 0), kDppXor2>(v);
-    bfly_stage<NV, (NH >= 4 ? NV / 16 : 0), kDppXor1>(v);
+    // head stages (free), then token stages (select), then all-reduce
+    constexpr int C1 = NV, C2 = NV / 2 > 0 ? NV / 2 : 1, C3 = NV / 4 > 0 ? NV / 4 : 1;
+    constexpr int C4 = NV / 8 > 0 ? NV / 8 : 1;
+    bfly_stage<C1, kDppRor8, (LGP >= 1)>(v, LGP == 0 ? tup1 : false);
+    bfly_stage<C2, kDppHalfMirror, (LGP >= 2)>(v, LGP == 1 ? tup1 : (LGP == 0 ? tup0 : false));
+    bfly_stage<(NV >= 8 ? C3 : 1), kDppXor2, (LGP >= 3)>(
+        v, LGP == 2 ? tup1 : (LGP == 1 ? tup0 : false));
+    bfly_stage<(NV >= 16 ? C4 : 1), kDppXor1, (LGP >= 4)>(
+        v, LGP == 3 ? tup1 : (LGP == 2 ? tup0 : false));
+    // held: head hmask, token bits (tup1, tup0) -- for GP = 8 two values,
+    // token bit 0 = e
 #pragma unroll
     for (int e = 0; e < HELD; ++e) {
-      const int key = mask | e;
-      const int h = key & (GP - 1);
-      const int tl = st * 16 + (key >> LGP) * 4 + r;
+      const int h = headmask;
+      const int ti = (tup1 ? 2 : 0) + (HELD == 2 ? e : (tup0 ? 1 : 0));
+      const int tl = st * 16 + ti * 4 + r;
       if (h < G) s_p[tl * GP + h] = (tl < ntok) ? v[e] * a.scale_log2 : -INFINITY;
     }
   };
@@ -535,6 +691,21 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
   for (int h = 0; h < G; ++h)
 #pragma unroll
     for (int x = 1; x < 64; x <<= 1) m[h] = fmaxf(m[h], shfl_xor(m[h], x));
+#if NPD_DECODE_PV_DOT2
+  // Probabilities of the token pair (8q + rr, 8q + 4 + rr) of each step, packed
+  // as two 2-byte values per head: the pair a pass-3 lane multiplies into one
+  // v_dot2 with V. l sums the rounded values, so the normalisation matches them.
+  for (int pi = lane; pi < ntl / 2; pi += 64) {
+    const int ta = (pi >> 3) * 16 + ((pi >> 2) & 1) * 8 + (pi & 3), tb = ta + 4;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const uint32_t ua = TT::from_float(__builtin_amdgcn_exp2f(s_p[ta * GP + h] - m[h]));
+      const uint32_t ub = TT::from_float(__builtin_amdgcn_exp2f(s_p[tb * GP + h] - m[h]));
+      l[h] += TT::lo(ua) + TT::lo(ub);
+      s_pp[pi * GP + h] = ua | (ub << 16);
+    }
+  }
+#else
   for (int t = lane; t < ntl; t += 64) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -543,6 +714,7 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
       l[h] += p;
     }
   }
+#endif
 #pragma unroll
   for (int h = 0; h < G; ++h)
 #pragma unroll
@@ -561,6 +733,38 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
       for (int i = 0; i < 4; ++i)
         if (st * 16 + i * 4 + r >= ntok) vbuf[i] = u32x4{0, 0, 0, 0};
     }
+#if NPD_DECODE_PV_DOT2
+    // slots 2q and 2q+1 hold tokens 8q + r and 8q + 4 + r: pack their values
+    // per dim (v_perm) and take both products with one v_dot2
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      uint32_t pp[GP];
+      const uint32_t* src = &s_pp[(st * 8 + q * 4 + r) * GP];
+      if constexpr (GP >= 4) {
+#pragma unroll
+        for (int h4 = 0; h4 < GP; h4 += 4) {
+          const u32x4 t4 = *reinterpret_cast<const u32x4*>(src + h4);
+          pp[h4] = t4.x; pp[h4 + 1] = t4.y; pp[h4 + 2] = t4.z; pp[h4 + 3] = t4.w;
+        }
+      } else {
+#pragma unroll
+        for (int h = 0; h < GP; ++h) pp[h] = src[h];
+      }
+      const uint32_t wa[4] = {vbuf[2 * q].x, vbuf[2 * q].y, vbuf[2 * q].z, vbuf[2 * q].w};
+      const uint32_t wb[4] = {vbuf[2 * q + 1].x, vbuf[2 * q + 1].y, vbuf[2 * q + 1].z,
+                              vbuf[2 * q + 1].w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint32_t lo = __builtin_amdgcn_perm(wb[c], wa[c], 0x05040100u);
+        const uint32_t hi = __builtin_amdgcn_perm(wb[c], wa[c], 0x07060302u);
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+          acc[h][2 * c] = TT::dot2(lo, pp[h], acc[h][2 * c]);
+          acc[h][2 * c + 1] = TT::dot2(hi, pp[h], acc[h][2 * c + 1]);
+        }
+      }
+    }
+#else
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int tl = st * 16 + i * 4 + r;
@@ -586,6 +790,7 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
         }
       }
     }
+#endif
   };
   {
     int st0 = 0;
@@ -617,32 +822,139 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
   }
   // Several partitions: publish this one's partial, then the last wave of the
   // (sequence, kv-head) to arrive merges them all and resets the counter.
+  // Partials go out as agent-scope atomic stores (written through to the
+  // device-coherent level) and are read back with agent-scope atomic loads, so
+  // no L2 writeback or invalidate is needed; the store completion wait orders
+  // them before the counter update.
   const int64_t ubase = (int64_t)unit * a.max_parts;
   if (lane < 16) {
     const int64_t base = ubase + part;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      f32x4* dst = reinterpret_cast<f32x4*>(a.part_acc + ((base * G + h) * D + j * 8));
-      dst[0] = f32x4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
-      dst[1] = f32x4{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
+      float* dst = a.part_acc + ((base * G + h) * D + j * 8);
+#pragma unroll
+      for (int d = 0; d < 8; d += 2)
+        st_coherent2(dst + d, acc[h][d], acc[h][d + 1]);
     }
     if (j == 0) {
 #pragma unroll
       for (int h = 0; h < G; ++h) {
-        a.part_ml[(base * G + h) * 2] = m[h];
-        a.part_ml[(base * G + h) * 2 + 1] = l[h];
+        st_coherent2(a.part_ml + (base * G + h) * 2, m[h], l[h]);
       }
     }
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);   // every store of this wave has completed
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   int ticket = 0;
   if (lane == 0)
     ticket = __hip_atomic_fetch_add(a.counters + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   ticket = __shfl(ticket, 0, 64);
   if (ticket != nparts - 1) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  merge_unit<TT, D, G>(a, unit, s, kh, nparts, lane, 64);
+  merge_unit_fast<TT, G>(a, unit, s, kh, nparts, lane, s_p);
   if (lane == 0) __hip_atomic_store(a.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+
+// Fast-path kernel: workgroup i (one wave) takes item i of the work list that
+// decode_schedule_kernel built -- longest sequences first, a unit's partitions
+// consecutive -- so long units start together, finish and merge early, and the
+// short ones fill the tail. The grid is sized for the most items possible;
+// workgroups past the list (all at the end of the grid) exit at once.
+template <class TT, int G, int SPB>
+__global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
+  constexpr int GP = pow2ceil(G);
+  constexpr int MAXT = kFastMaxPartition + 16 * kRing;
+  __shared__ __attribute__((aligned(16))) float s_p[MAXT * GP];
+#if NPD_DECODE_PV_DOT2
+  __shared__ __attribute__((aligned(16))) uint32_t s_pp[MAXT / 2 * GP];
+#else
+  uint32_t* s_pp = nullptr;
+#endif
+  if ((int)blockIdx.x >= a.sched[1]) return;
+  const int2 it = a.items[blockIdx.x];
+  decode_d128_item<TT, G, SPB>(a, it.x, it.y, s_p, s_pp);
+}
+
+// Builds the work list of decode_d128_kernel (one workgroup):
+//   - zeroes the per-unit merge counters;
+//   - counting-sorts the sequences by partition count, descending;
+//   - lists the items of each sequence in that order, unit by unit
+//     (item = (unit, partition)); a sequence with no context gets one item,
+//     which writes zeros.
+constexpr int kSchedThreads = 1024;
+constexpr int kSchedMaxSeqs = 4096;
+constexpr int kSchedBins = 1024;
+
+__global__ __launch_bounds__(kSchedThreads) void decode_schedule_kernel(DecodeArgs a, int num_seqs) {
+  __shared__ int s_order[kSchedMaxSeqs];
+  __shared__ int s_offs[kSchedMaxSeqs + 1];
+  __shared__ int s_hist[kSchedBins];
+  __shared__ int s_wsum[kSchedThreads / 64];
+  __shared__ int s_carry;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int kvh = a.num_kv_heads;
+  const int cap = a.max_bps * a.block_size;
+  const int units = num_seqs * kvh;
+  auto nparts_of = [&](int s) {
+    int c = a.seq_lens[s];
+    c = c < cap ? c : cap;
+    return c <= 0 ? 1 : (c + a.partition - 1) / a.partition;
+  };
+  for (int u = tid; u < units; u += kSchedThreads) a.counters[u] = 0;
+  for (int b = tid; b < kSchedBins; b += kSchedThreads) s_hist[b] = 0;
+  if (tid == 0) s_carry = 0;
+  __syncthreads();
+  // histogram of keys (bin 0 = most partitions)
+  for (int s = tid; s < num_seqs; s += kSchedThreads) {
+    const int np = nparts_of(s);
+    atomicAdd(&s_hist[kSchedBins - 1 - (np < kSchedBins ? np : kSchedBins - 1)], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {   // exclusive scan of the 1024 bins (cheap, one thread)
+    int run = 0;
+    for (int b = 0; b < kSchedBins; ++b) { const int c = s_hist[b]; s_hist[b] = run; run += c; }
+  }
+  __syncthreads();
+  for (int s = tid; s < num_seqs; s += kSchedThreads) {
+    const int np = nparts_of(s);
+    const int pos = atomicAdd(&s_hist[kSchedBins - 1 - (np < kSchedBins ? np : kSchedBins - 1)], 1);
+    s_order[pos] = s;
+  }
+  __syncthreads();
+  // offsets of each sorted sequence's items (kvh * nparts each)
+  for (int base = 0; base < num_seqs; base += kSchedThreads) {
+    const int k = base + tid;
+    const int cnt = k < num_seqs ? kvh * nparts_of(s_order[k]) : 0;
+    int inc = cnt;
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(inc, o, 64);
+      if (lane >= o) inc += v;
+    }
+    if (lane == 63) s_wsum[wid] = inc;
+    __syncthreads();
+    int pre = s_carry;
+    for (int w = 0; w < wid; ++w) pre += s_wsum[w];
+    if (k < num_seqs) s_offs[k] = pre + inc - cnt;
+    __syncthreads();
+    if (tid == kSchedThreads - 1) s_carry = pre + inc;
+    __syncthreads();
+  }
+  if (tid == 0) { s_offs[num_seqs] = s_carry; a.sched[1] = s_carry; }
+  __syncthreads();
+  const int total = s_offs[num_seqs];
+  for (int i = tid; i < total; i += kSchedThreads) {
+    int lo = 0, hi = num_seqs - 1;   // last k with s_offs[k] <= i
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_offs[mid] <= i) lo = mid; else hi = mid - 1;
+    }
+    const int sq = s_order[lo];
+    const int np = nparts_of(sq);
+    const int jj = i - s_offs[lo];
+    const int kh = jj / np;
+    a.items[i] = make_int2(sq * kvh + kh, jj - kh * np);
+  }
 }
 
 // Merge kernel for the generic path: one workgroup per (sequence, kv-head).
@@ -660,9 +972,9 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(DecodeArgs a) {
   merge_unit<TT, D, G>(a, unit, s, kh, nparts, threadIdx.x, blockDim.x);
 }
 
-bool use_fast_path(int64_t head_dim, int64_t block_size) {
+bool use_fast_path(int64_t head_dim, int64_t block_size, int64_t num_seqs) {
   return head_dim == 128 && block_size % 16 == 0 && block_size <= 256 &&
-         (block_size & (block_size - 1)) == 0;
+         (block_size & (block_size - 1)) == 0 && num_seqs <= kSchedMaxSeqs;
 }
 
 // Partition length (tokens per wave). The fast path takes the largest of
@@ -672,7 +984,10 @@ bool use_fast_path(int64_t head_dim, int64_t block_size) {
 int choose_partition(int64_t num_seqs, int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
                      int64_t max_ctx) {
   const int64_t units = num_seqs * num_kv_heads;
-  if (use_fast_path(head_dim, block_size)) {
+  if (use_fast_path(head_dim, block_size, num_seqs)) {
+#ifdef NPD_DECODE_PARTITION
+    if (NPD_DECODE_PARTITION >= block_size) return NPD_DECODE_PARTITION;
+#endif
     for (int ps = 256; ps >= 64; ps >>= 1) {
       if (ps <= block_size) return (int)block_size;
       if (units * ((max_ctx + ps - 1) / ps) >= 4096) return ps;
@@ -682,23 +997,30 @@ int choose_partition(int64_t num_seqs, int64_t num_kv_heads, int64_t head_dim, i
   return units * ((max_ctx + 511) / 512) >= 4096 ? 512 : 256;
 }
 
+template <class TT, int G, int SPB>
+int launch_fast_bs(const DecodeArgs& a, int num_seqs, int64_t max_items, hipStream_t st) {
+  hipLaunchKernelGGL(decode_schedule_kernel, dim3(1), dim3(kSchedThreads), 0, st, a, num_seqs);
+  hipLaunchKernelGGL((decode_d128_kernel<TT, G, SPB>), dim3((unsigned)max_items), dim3(64), 0, st, a);
+  return NPD_OK;
+}
+
 template <class TT, int G>
-void launch_fast(const DecodeArgs& a, int64_t units, hipStream_t st) {
-  const dim3 grid((unsigned)units, (unsigned)a.max_parts);
+int launch_fast(const DecodeArgs& a, int num_seqs, int64_t max_items, hipStream_t st) {
   switch (a.block_size) {
-    case 16: hipLaunchKernelGGL((decode_d128_kernel<TT, G, 1>), grid, dim3(64), 0, st, a); break;
-    case 32: hipLaunchKernelGGL((decode_d128_kernel<TT, G, 2>), grid, dim3(64), 0, st, a); break;
-    case 64: hipLaunchKernelGGL((decode_d128_kernel<TT, G, 4>), grid, dim3(64), 0, st, a); break;
-    case 128: hipLaunchKernelGGL((decode_d128_kernel<TT, G, 8>), grid, dim3(64), 0, st, a); break;
-    default: hipLaunchKernelGGL((decode_d128_kernel<TT, G, 16>), grid, dim3(64), 0, st, a); break;
+    case 16: return launch_fast_bs<TT, G, 1>(a, num_seqs, max_items, st);
+    case 32: return launch_fast_bs<TT, G, 2>(a, num_seqs, max_items, st);
+    case 64: return launch_fast_bs<TT, G, 4>(a, num_seqs, max_items, st);
+    case 128: return launch_fast_bs<TT, G, 8>(a, num_seqs, max_items, st);
+    default: return launch_fast_bs<TT, G, 16>(a, num_seqs, max_items, st);
   }
 }
 
 template <class TT, int D, int G>
 int launch_decode(const DecodeArgs& a, int64_t units, hipStream_t st) {
   if constexpr (D == 128) {
-    if (use_fast_path(D, a.block_size)) {
-      launch_fast<TT, G>(a, units, st);
+    if (use_fast_path(D, a.block_size, units / a.num_kv_heads)) {
+      const int rc = launch_fast<TT, G>(a, (int)(units / a.num_kv_heads), units * a.max_parts, st);
+      if (rc != NPD_OK) return rc;
       return npd::check_launch("npd_paged_attention");
     } else {
       hipLaunchKernelGGL((decode_partition_kernel<TT, D, G>),
@@ -748,10 +1070,13 @@ extern "C" int64_t npd_paged_attention_workspace_size(int64_t num_seqs, int64_t 
   const int64_t max_ctx = block_size * max_blocks_per_seq;
   const int ps = choose_partition(num_seqs, num_kv_heads, head_dim, block_size, max_ctx);
   const int64_t parts = (max_ctx + ps - 1) / ps;
-  if (parts <= 1) return 0;
+  if (parts <= 1 && !use_fast_path(head_dim, block_size, num_seqs)) return 0;
   const int64_t partials = num_seqs * num_heads * parts * (head_dim + 2) * (int64_t)sizeof(float);
-  const int64_t counters = use_fast_path(head_dim, block_size) ? num_seqs * num_kv_heads * 4 : 0;
-  return partials + counters;
+  if (!use_fast_path(head_dim, block_size, num_seqs)) return partials;
+  // fast path: merge counters, item count (padded to 16 B), work list
+  const int64_t units = num_seqs * num_kv_heads;
+  const int64_t counters = (units * 4 + 15) / 16 * 16;
+  return partials + counters + 16 + units * parts * 8;
 }
 
 extern "C" int npd_paged_attention(void* out, const void* query, const void* key_cache,
@@ -799,14 +1124,15 @@ extern "C" int npd_paged_attention(void* out, const void* query, const void* key
 
   const int64_t max_ctx = block_size * max_blocks_per_seq;
   const int partition = choose_partition(num_seqs, num_kv_heads, head_dim, block_size, max_ctx);
-  if (partition > kMaxPartition)
+  if (partition > kMaxPartition ||
+      (use_fast_path(head_dim, block_size, num_seqs) && partition > kFastMaxPartition))
     return fail(NPD_E_INVALID, "%s: block_size %lld is above %d", name, (long long)block_size,
-                kMaxPartition);
+                use_fast_path(head_dim, block_size, num_seqs) ? kFastMaxPartition : kMaxPartition);
   const int64_t max_parts = (max_ctx + partition - 1) / partition;
   if (max_parts > 65535) return fail(NPD_E_INVALID, "%s: context too long", name);
   const int64_t need = npd_paged_attention_workspace_size(num_seqs, num_heads, num_kv_heads,
                                                           head_dim, block_size, max_blocks_per_seq);
-  if (max_parts > 1) {
+  if (need > 0) {
     if (!workspace || workspace_bytes < need)
       return fail(NPD_E_WORKSPACE, "%s: workspace of %lld bytes needed, %lld given", name,
                   (long long)need, (long long)workspace_bytes);
@@ -826,6 +1152,8 @@ extern "C" int npd_paged_attention(void* out, const void* query, const void* key
   a.part_acc = ws;
   a.part_ml = ws ? ws + units * max_parts * g * head_dim : nullptr;
   a.counters = ws ? reinterpret_cast<int*>(a.part_ml + units * max_parts * g * 2) : nullptr;
+  a.sched = ws ? a.counters + (units * 4 + 15) / 16 * 4 : nullptr;
+  a.items = ws ? reinterpret_cast<int2*>(a.sched + 4) : nullptr;
   a.num_kv_heads = (int)num_kv_heads;
   a.block_size = (int)block_size;
   a.num_blocks = (int)num_blocks;

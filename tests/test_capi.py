@@ -88,19 +88,21 @@ def test_c_validation_paths_need_no_gpu():
 
 def test_workspace_size():
     lib = _lib.load()
-    # 1024 seqs x 8 kv heads x 256 tokens: one partition of 256 each, no workspace
-    assert lib.npd_paged_attention_workspace_size(1024, 32, 8, 128, 16, 16) == 0
-    # fast path (head_dim 128): fp32 partials + one int32 merge counter per
-    # (sequence, kv head). 64 seqs x 8 kv heads x 256 tokens: 512 waves ->
-    # partitions of 64 (4 each)
-    n = lib.npd_paged_attention_workspace_size(64, 32, 8, 128, 16, 16)
-    assert n == 64 * 32 * 4 * 130 * 4 + 64 * 8 * 4
+    # fast path (head_dim 128): fp32 partials (G*D + 2G floats per partition),
+    # one int32 merge counter per (sequence, kv head) padded to 16 bytes, a
+    # 16-byte item count, and an 8-byte (unit, partition) work-list entry per
+    # possible partition.
+    def fast(S, H, kvh, P):
+        units = S * kvh
+        return S * H * P * 130 * 4 + (units * 4 + 15) // 16 * 16 + 16 + units * P * 8
+    # 1024 seqs x 8 kv heads x 256 tokens: one partition of 256 each
+    assert lib.npd_paged_attention_workspace_size(1024, 32, 8, 128, 16, 16) == fast(1024, 32, 8, 1)
+    # 64 seqs x 8 kv heads x 256 tokens: 512 waves -> partitions of 64 (4 each)
+    assert lib.npd_paged_attention_workspace_size(64, 32, 8, 128, 16, 16) == fast(64, 32, 8, 4)
     # 8 seqs x 8 kv heads x 32k tokens: 128 partitions of 256 already give >= 4096 waves
-    n = lib.npd_paged_attention_workspace_size(8, 32, 8, 128, 16, 2048)
-    assert n == 8 * 32 * 128 * (128 + 2) * 4 + 8 * 8 * 4
+    assert lib.npd_paged_attention_workspace_size(8, 32, 8, 128, 16, 2048) == fast(8, 32, 8, 128)
     # 1 seq x 8 kv heads x 4k tokens: too few waves -> partitions of 64
-    n = lib.npd_paged_attention_workspace_size(1, 32, 8, 128, 16, 256)
-    assert n == 1 * 32 * 64 * (128 + 2) * 4 + 8 * 4
+    assert lib.npd_paged_attention_workspace_size(1, 32, 8, 128, 16, 256) == fast(1, 32, 8, 64)
     # generic path (head_dim 64): partitions of 256 below 4096 waves
     n = lib.npd_paged_attention_workspace_size(2, 8, 8, 64, 16, 64)
     assert n == 2 * 8 * 4 * (64 + 2) * 4
