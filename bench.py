@@ -149,13 +149,40 @@ def bench_decode(args, w) -> dict:
     }
 
 
+def bench_copy(args, dev) -> int:
+    """Device copy of 256 MiB (reads 256 MiB, writes 256 MiB): counter
+    calibration for the roofline traffic field."""
+    n = 256 << 20
+    src = torch.ones(n, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(args.warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    b.record()
+    b.synchronize()
+    ms = a.elapsed_time(b) / args.steps
+    print(json.dumps({"metric": "device copy GB/s (read + write)", "value": round(2 * n / ms / 1e6, 1),
+                      "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                      "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+                      "vs_baseline": None, "dtype": "u8", "data": "synthetic",
+                      "config": {"workload": "copy_256MiB", "bytes_read": n, "bytes_written": n}}),
+          flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=["decode", "long"], default="decode",
-                    help="decode: config 2 (default); long: config 4 (8 seqs, 8k-32k)")
+    ap.add_argument("--workload", choices=["decode", "long", "copy"], default="decode",
+                    help="decode: config 2 (default); long: config 4 (8 seqs, 8k-32k); "
+                         "copy: a plain 256 MiB device copy, the calibration kernel for "
+                         "the FETCH_SIZE / WRITE_SIZE counters")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -168,6 +195,8 @@ def main() -> int:
     from nanopd_amd import _lib, workloads
     _lib.load()
     dev = torch.device("cuda:0")
+    if args.workload == "copy":
+        return bench_copy(args, dev)
     if args.workload == "decode":
         w = workloads.config2(dev)
     else:

@@ -106,7 +106,10 @@ int64_t npd_paged_attention_workspace_size(int64_t num_seqs, int64_t num_heads,
  * gives zeros; seq_lens[s] is clamped to max_blocks_per_seq * block_size.
  * Every output element is written: out need not be zeroed.
  * workspace: at least npd_paged_attention_workspace_size(...) bytes, 256-byte
- * aligned (may be NULL when that size is 0).
+ * aligned (may be NULL when that size is 0), zero-filled before its first
+ * use: it holds split-context partials and, for head_dim 128, per-(sequence,
+ * kv-head) merge counters that every call leaves at zero, and a work list.
+ * Calls sharing a workspace must be stream-ordered.
  */
 int npd_paged_attention(void* out, const void* query,
                         const void* key_cache, const void* value_cache,

@@ -46,6 +46,10 @@ constexpr int kRing = NPD_DECODE_RING;   // fast path: K/V steps in flight per w
 #define NPD_FAST_MAX_PARTITION 256
 #endif
 constexpr int kFastMaxPartition = NPD_FAST_MAX_PARTITION;   // fast path: tokens per wave, max
+#ifndef NPD_DECODE_INLINE_SCHED_MAX
+#define NPD_DECODE_INLINE_SCHED_MAX 64
+#endif
+constexpr int kInlineSchedMax = NPD_DECODE_INLINE_SCHED_MAX;   // at most 64 (one per lane)
 constexpr float kLog2e = 1.4426950408889634f;
 
 constexpr int ilog2(int x) { return x <= 1 ? 0 : 1 + ilog2(x >> 1); }
@@ -74,7 +78,8 @@ struct DecodeArgs {
   float* part_acc;   // [S*kvh, max_parts, G, D]
   float* part_ml;    // [S*kvh, max_parts, G, 2]
   int* counters;     // [S*kvh] arrival counters of the fused merge
-  int* sched;        // fast path: [1] number of work items
+  int* sched;        // fast path, more than 64 sequences: [1] number of work items
+  int num_seqs;
   int2* items;       // fast path: (unit, partition) work list
   int num_kv_heads;
   int block_size;
@@ -499,9 +504,9 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int unit, i
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             if (q0 + q < n) {
-              const float* src = a.part_acc + (((base + p0 + q0 + q) * G + h) * D + c * 8);
+              const float* src = a.part_acc + ((base + p0 + q0 + q) * G + h) * D + c * 2;
 #pragma unroll
-              for (int d = 0; d < 8; d += 2) ld_coherent2(src + d, x[q][d], x[q][d + 1]);
+              for (int k = 0; k < 4; ++k) ld_coherent2(src + k * 32, x[q][2 * k], x[q][2 * k + 1]);
             }
           }
 #pragma unroll
@@ -826,16 +831,23 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
   // device-coherent level) and are read back with agent-scope atomic loads, so
   // no L2 writeback or invalidate is needed; the store completion wait orders
   // them before the counter update.
+  // Partial rows are stored transposed, [dim pair k][chunk j][2], so that the
+  // 16 lanes of a row write 128 contiguous bytes per store; after the row
+  // reduction every row of the wave holds the sums, so row r stores heads
+  // r, r + 4, ...
   const int64_t ubase = (int64_t)unit * a.max_parts;
-  if (lane < 16) {
+  {
     const int64_t base = ubase + part;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      float* dst = a.part_acc + ((base * G + h) * D + j * 8);
+      if ((h & 3) != r) continue;
+      float* dst = a.part_acc + (base * G + h) * D + j * 2;
 #pragma unroll
-      for (int d = 0; d < 8; d += 2)
-        st_coherent2(dst + d, acc[h][d], acc[h][d + 1]);
+      for (int k = 0; k < 4; ++k) st_coherent2(dst + k * 32, acc[h][2 * k], acc[h][2 * k + 1]);
     }
+  }
+  if (lane < 16) {
+    const int64_t base = ubase + part;
     if (j == 0) {
 #pragma unroll
       for (int h = 0; h < G; ++h) {
@@ -871,9 +883,42 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
 #else
   uint32_t* s_pp = nullptr;
 #endif
-  if ((int)blockIdx.x >= a.sched[1]) return;
-  const int2 it = a.items[blockIdx.x];
-  decode_d128_item<TT, G, SPB>(a, it.x, it.y, s_p, s_pp);
+  int unit, part;
+  if (a.num_seqs <= kInlineSchedMax) {
+    // Small batch: every workgroup derives the work list itself. Lane i holds
+    // sequence i's partition count; its rank (more partitions first, then
+    // index) and the item offset come from one pass over the lanes.
+    const int lane = threadIdx.x;
+    const int cap = a.max_bps * a.block_size;
+    int np = 0;
+    if (lane < a.num_seqs) {
+      int c = a.seq_lens[lane];
+      c = c < cap ? c : cap;
+      np = c <= 0 ? 1 : (c + a.partition - 1) / a.partition;
+    }
+    int off = 0;
+    for (int jj = 0; jj < a.num_seqs; ++jj) {
+      const int nj = __builtin_amdgcn_readlane(np, jj);
+      if (nj > np || (nj == np && jj < lane)) off += nj;
+    }
+    off *= a.num_kv_heads;
+    const int id = blockIdx.x;
+    const bool mine = lane < a.num_seqs && id >= off && id < off + a.num_kv_heads * np;
+    const uint64_t ballot = __ballot(mine);
+    if (ballot == 0) return;   // past the last item
+    const int owner = __builtin_ctzll(ballot);
+    const int o = __builtin_amdgcn_readlane(off, owner);
+    const int n = __builtin_amdgcn_readlane(np, owner);
+    const int kh = (id - o) / n;
+    unit = owner * a.num_kv_heads + kh;
+    part = id - o - kh * n;
+  } else {
+    if ((int)blockIdx.x >= a.sched[1]) return;
+    const int2 it = a.items[blockIdx.x];
+    unit = it.x;
+    part = it.y;
+  }
+  decode_d128_item<TT, G, SPB>(a, unit, part, s_p, s_pp);
 }
 
 // Builds the work list of decode_d128_kernel (one workgroup):
@@ -887,8 +932,9 @@ constexpr int kSchedMaxSeqs = 4096;
 constexpr int kSchedBins = 1024;
 
 __global__ __launch_bounds__(kSchedThreads) void decode_schedule_kernel(DecodeArgs a, int num_seqs) {
-  __shared__ int s_order[kSchedMaxSeqs];
-  __shared__ int s_offs[kSchedMaxSeqs + 1];
+  __shared__ int s_np[kSchedMaxSeqs];      // partitions per sequence
+  __shared__ int s_order[kSchedMaxSeqs];   // sequences, most partitions first
+  __shared__ int s_offs[kSchedMaxSeqs];    // first item of each sorted sequence
   __shared__ int s_hist[kSchedBins];
   __shared__ int s_wsum[kSchedThreads / 64];
   __shared__ int s_carry;
@@ -896,64 +942,59 @@ __global__ __launch_bounds__(kSchedThreads) void decode_schedule_kernel(DecodeAr
   const int kvh = a.num_kv_heads;
   const int cap = a.max_bps * a.block_size;
   const int units = num_seqs * kvh;
-  auto nparts_of = [&](int s) {
-    int c = a.seq_lens[s];
-    c = c < cap ? c : cap;
-    return c <= 0 ? 1 : (c + a.partition - 1) / a.partition;
-  };
-  for (int u = tid; u < units; u += kSchedThreads) a.counters[u] = 0;
-  for (int b = tid; b < kSchedBins; b += kSchedThreads) s_hist[b] = 0;
-  if (tid == 0) s_carry = 0;
-  __syncthreads();
-  // histogram of keys (bin 0 = most partitions)
-  for (int s = tid; s < num_seqs; s += kSchedThreads) {
-    const int np = nparts_of(s);
-    atomicAdd(&s_hist[kSchedBins - 1 - (np < kSchedBins ? np : kSchedBins - 1)], 1);
-  }
-  __syncthreads();
-  if (tid == 0) {   // exclusive scan of the 1024 bins (cheap, one thread)
-    int run = 0;
-    for (int b = 0; b < kSchedBins; ++b) { const int c = s_hist[b]; s_hist[b] = run; run += c; }
-  }
-  __syncthreads();
-  for (int s = tid; s < num_seqs; s += kSchedThreads) {
-    const int np = nparts_of(s);
-    const int pos = atomicAdd(&s_hist[kSchedBins - 1 - (np < kSchedBins ? np : kSchedBins - 1)], 1);
-    s_order[pos] = s;
-  }
-  __syncthreads();
-  // offsets of each sorted sequence's items (kvh * nparts each)
-  for (int base = 0; base < num_seqs; base += kSchedThreads) {
-    const int k = base + tid;
-    const int cnt = k < num_seqs ? kvh * nparts_of(s_order[k]) : 0;
-    int inc = cnt;
+  auto bin_of = [](int np) { return kSchedBins - 1 - (np < kSchedBins ? np : kSchedBins - 1); };
+  // block-wide exclusive scan of one value per thread (chunk of kSchedThreads)
+  auto block_scan = [&](int c, int carry_in) {
+    int inc = c;
     for (int o = 1; o < 64; o <<= 1) {
       const int v = __shfl_up(inc, o, 64);
       if (lane >= o) inc += v;
     }
     if (lane == 63) s_wsum[wid] = inc;
     __syncthreads();
-    int pre = s_carry;
+    int pre = carry_in;
     for (int w = 0; w < wid; ++w) pre += s_wsum[w];
-    if (k < num_seqs) s_offs[k] = pre + inc - cnt;
     __syncthreads();
-    if (tid == kSchedThreads - 1) s_carry = pre + inc;
+    return pre + inc - c;   // exclusive prefix; pre + inc is the inclusive one
+  };
+  for (int u = tid; u < units; u += kSchedThreads) a.counters[u] = 0;
+  s_hist[tid] = 0;
+  __syncthreads();
+  for (int sq = tid; sq < num_seqs; sq += kSchedThreads) {
+    int c = a.seq_lens[sq];
+    c = c < cap ? c : cap;
+    const int np = c <= 0 ? 1 : (c + a.partition - 1) / a.partition;
+    s_np[sq] = np;
+    atomicAdd(&s_hist[bin_of(np)], 1);
+  }
+  __syncthreads();
+  static_assert(kSchedBins == kSchedThreads, "one bin per thread");
+  const int start = block_scan(s_hist[tid], 0);
+  s_hist[tid] = start;
+  __syncthreads();
+  for (int sq = tid; sq < num_seqs; sq += kSchedThreads)
+    s_order[atomicAdd(&s_hist[bin_of(s_np[sq])], 1)] = sq;
+  __syncthreads();
+  int carry = 0;
+  for (int base = 0; base < num_seqs; base += kSchedThreads) {
+    const int k = base + tid;
+    const int cnt = k < num_seqs ? kvh * s_np[s_order[k]] : 0;
+    const int ex = block_scan(cnt, carry);
+    if (k < num_seqs) s_offs[k] = ex;
+    if (tid == kSchedThreads - 1) s_carry = ex + cnt;
+    __syncthreads();
+    carry = s_carry;
     __syncthreads();
   }
-  if (tid == 0) { s_offs[num_seqs] = s_carry; a.sched[1] = s_carry; }
-  __syncthreads();
-  const int total = s_offs[num_seqs];
-  for (int i = tid; i < total; i += kSchedThreads) {
-    int lo = 0, hi = num_seqs - 1;   // last k with s_offs[k] <= i
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (s_offs[mid] <= i) lo = mid; else hi = mid - 1;
+  if (tid == 0) a.sched[1] = carry;
+  // items of sorted sequence k: (unit kh, partition p) for kh < kvh, p < np,
+  // unit by unit; one wave per sequence
+  for (int k = wid; k < num_seqs; k += kSchedThreads / 64) {
+    const int sq = s_order[k], np = s_np[sq], n = kvh * np, o = s_offs[k];
+    for (int e = lane; e < n; e += 64) {
+      const int kh = e / np;
+      a.items[o + e] = make_int2(sq * kvh + kh, e - kh * np);
     }
-    const int sq = s_order[lo];
-    const int np = nparts_of(sq);
-    const int jj = i - s_offs[lo];
-    const int kh = jj / np;
-    a.items[i] = make_int2(sq * kvh + kh, jj - kh * np);
   }
 }
 
@@ -999,7 +1040,8 @@ int choose_partition(int64_t num_seqs, int64_t num_kv_heads, int64_t head_dim, i
 
 template <class TT, int G, int SPB>
 int launch_fast_bs(const DecodeArgs& a, int num_seqs, int64_t max_items, hipStream_t st) {
-  hipLaunchKernelGGL(decode_schedule_kernel, dim3(1), dim3(kSchedThreads), 0, st, a, num_seqs);
+  if (num_seqs > kInlineSchedMax)
+    hipLaunchKernelGGL(decode_schedule_kernel, dim3(1), dim3(kSchedThreads), 0, st, a, num_seqs);
   hipLaunchKernelGGL((decode_d128_kernel<TT, G, SPB>), dim3((unsigned)max_items), dim3(64), 0, st, a);
   return NPD_OK;
 }
@@ -1155,6 +1197,7 @@ extern "C" int npd_paged_attention(void* out, const void* query, const void* key
   a.sched = ws ? a.counters + (units * 4 + 15) / 16 * 4 : nullptr;
   a.items = ws ? reinterpret_cast<int2*>(a.sched + 4) : nullptr;
   a.num_kv_heads = (int)num_kv_heads;
+  a.num_seqs = (int)num_seqs;
   a.block_size = (int)block_size;
   a.num_blocks = (int)num_blocks;
   a.max_bps = (int)max_blocks_per_seq;

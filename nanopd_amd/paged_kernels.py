@@ -164,10 +164,10 @@ def paged_kv_store_slots(k_cache: torch.Tensor, v_cache: torch.Tensor, k_src: to
 # Decode attention
 # ---------------------------------------------------------------------------
 
-# Cached decode workspaces, one per (device, stream): zero-filled when made.
-# The fast decode path keeps per-(sequence, kv-head) arrival counters at the
-# end of the workspace and leaves them zero after every call, so a workspace
-# only has to be zeroed once; one per stream keeps concurrent streams apart.
+# Cached decode workspaces, one per (device, stream), so that calls on
+# different streams never share one. They are zero-filled when made: the fast
+# decode path keeps per-(sequence, kv-head) merge counters in the workspace and
+# leaves them zero after every call, so zeroing once is enough.
 _workspaces: dict = {}
 
 

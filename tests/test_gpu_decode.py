@@ -198,22 +198,26 @@ def test_config4_long_context_with_cow_fork(device):
     assert err <= ATOL[torch.bfloat16]
 
 
-def test_fused_merge_counters_reset_between_calls(device):
-    """The fast path merges partitions in the last-arriving wave, using counters
-    kept in the workspace; they must be left zero so the next call (with other
-    lengths, hence other partition counts) is right too."""
-    args = make_inputs(6, 32, 8, 128, [4000, 300, 2500, 17, 1024, 3333], 16, torch.bfloat16,
-                       device, seed=21)
+@pytest.mark.parametrize("num_seqs", [6, 70])
+def test_workspace_reuse_across_calls(device, num_seqs):
+    """The fast path merges partitions in the last-arriving wave through
+    counters in the workspace that every call leaves at zero: a workspace
+    zeroed once and reused across calls with other lengths (other partition
+    counts) stays right. 70 sequences take the scheduled (work-list) path,
+    6 the in-kernel one."""
+    g = torch.Generator().manual_seed(num_seqs)
+    top = 4000 if num_seqs < 64 else 1500
+    lens_a = torch.randint(1, top + 1, (num_seqs,), generator=g).tolist()
+    lens_b = torch.randint(1, top + 1, (num_seqs,), generator=g).tolist()
+    lens_a[0], lens_b[1] = top, top
+    args = make_inputs(num_seqs, 32, 8, 128, [top] * num_seqs, 16, torch.bfloat16, device,
+                       seed=21)
     q, kc, vc, bt, sl, scale, mb = args
-    ws = torch.zeros(pk.attention_workspace_bytes(6, 32, 8, 128, 16, mb), dtype=torch.uint8,
-                     device=device)
-    for lens in ([4000, 300, 2500, 17, 1024, 3333], [100, 3999, 1, 2049, 700, 4000],
-                 [4000, 300, 2500, 17, 1024, 3333]):
+    ws = torch.zeros(pk.attention_workspace_bytes(num_seqs, 32, 8, 128, 16, mb),
+                     dtype=torch.uint8, device=device)
+    for lens in (lens_a, lens_b, lens_a):
         sl = torch.tensor(lens, dtype=torch.int32, device=device)
         out = torch.full_like(q, float("nan"))
         pk.paged_attention_forward(out, q, kc, vc, bt, sl, scale, 16, mb, workspace=ws)
         torch.cuda.synchronize()
         check(out, q, kc, vc, bt, sl, scale)
-    units = 6 * 8
-    counters = ws[-4 * units:].view(torch.int32)
-    assert torch.count_nonzero(counters) == 0
