@@ -144,7 +144,7 @@ def bench_decode(args, w) -> dict:
             "attention_bytes": w.attention_bytes(),
             "store_bytes": w.store_bytes(),
             "kv_tokens": sum(w.seq_lens_list),
-            "kernels": "decode_partition_kernel + merge_partitions_kernel (one op)",
+            "kernels": "decode_d128_kernel (partitions + fused log-sum-exp merge)",
         },
     }
 
