@@ -37,6 +37,12 @@ struct BF16 {
     typedef __bf16 v2 __attribute__((ext_vector_type(2)));
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
   }
+  // Two floats -> packed pair, round to nearest even (v_cvt_pk_bf16_f32).
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+    const v2 v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+  }
 };
 
 struct F16 {
@@ -54,6 +60,11 @@ struct F16 {
   // v_dot2_f32_f16: products of fp16 pairs summed into an fp32 accumulator.
   static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
+  }
+  // Two floats -> packed pair, round to nearest even.
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    const h2 v = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, v);
   }
 };
 

@@ -10,18 +10,24 @@
 // them before attending, model_runner.py:146). For an empty prefix both agree.
 //
 // MI355X design (gfx950, v_mfma_f32_16x16x32_{bf16,f16}, wave64):
-//   workgroup = one (sequence, kv-head, tile of 64 query positions); its G
-//   waves are the G query heads of the GQA group, so each K/V tile is gathered
-//   from the pool once into LDS and used by all of them.
-//   per step of 32 keys, wave w (query head kv*G + w):
-//     S^T = K . Q^T   -- A = K rows from LDS, B = the wave's 64 query rows,
-//                        kept in registers for the whole key loop;
-//     online softmax  -- lane l owns query (mb*16 + l%16) in each 16-query
-//                        block: 8 of its 32 scores per step are in-lane, the
-//                        rest in lanes l^16, l^32;
-//     O^T += V^T . P^T -- P^T comes straight out of the S^T accumulators in the
-//                        B-operand layout; V is stored transposed in LDS so the
-//                        A operand is two 8-byte reads per lane.
+//   workgroup = one (sequence, kv-head, tile of 64 query positions) with 2*G
+//   waves: wave w serves query head kv*G + w/2 and the 32 query rows
+//   (w%2)*32 .. +32 of the tile. Each 64-key K/V tile is gathered from the
+//   pool once into LDS and used by all 2*G waves (GQA reuse); two waves per
+//   SIMD let one wave's softmax (VALU) run under the other's MFMAs.
+//   per step of 64 keys, each wave:
+//     S^T = K . Q^T   -- A = K rows from LDS, B = the wave's query rows, kept
+//                        in registers for the whole key loop;
+//     online softmax  -- lane l owns query (mb*16 + l%16) of each 16-row block:
+//                        16 of its 64 scores per step are in-lane, the rest in
+//                        lanes l^16, l^32; the O rescale is skipped when no
+//                        row maximum moved;
+//     O^T += V^T . P^T -- P^T is the S^T accumulator, already in B-operand
+//                        layout (packed with v_cvt_pk_bf16_f32); V stays
+//                        row-major in LDS like K, and the V^T A operand is two
+//                        ds_read_b64_tr_b16 (gfx950 transposing LDS read: in a
+//                        group of 16 lanes, lane j receives element j%4 of the
+//                        8-byte chunks addressed by lanes 4e + j/4, e = 0..3).
 //   Operand layouts of v_mfma_f32_16x16x32 (checked on the hardware):
 //     A[m = lane%16][k = 8*(lane/16) + e], B[k = 8*(lane/16) + e][n = lane%16],
 //     D[m = 4*(lane/16) + i][n = lane%16].
@@ -39,10 +45,13 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kD = 128;          // head_dim of this kernel
-constexpr int kQT = 64;          // query positions per workgroup (per wave)
-constexpr int kKT = 32;          // keys per step
-constexpr int kKRow = kD + 8;    // LDS row of the K tile (elements, padded: 4-bank shift per row)
-constexpr int kVRow = kKT + 4;   // LDS row of the transposed V tile (elements)
+constexpr int kQT = 64;          // query positions per workgroup
+constexpr int kQW = 32;          // query rows per wave
+constexpr int kKT = 64;          // keys per step
+// LDS row of the K and V tiles (elements): 72 dwords, an 8-bank shift per row,
+// so 16 rows of K read at one column and 4 rows x 32 bytes of a transposing
+// V read both hit distinct banks
+constexpr int kRow = kD + 16;
 constexpr int kMaxBlocksLds = 1024;   // block ids of one workgroup's key range kept in LDS
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -80,10 +89,19 @@ struct Mfma<npd::F16> {
 
 __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16 on an LDS address given as a generic pointer to __shared__
+__device__ __forceinline__ u32x2 lds_read_tr(const uint16_t* p) {
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p)));
+}
+
 template <class TT, int G>
-__global__ __launch_bounds__(64 * G) void prefill_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kKT * kKRow];
-  __shared__ __attribute__((aligned(16))) uint16_t s_v[2][kD * kVRow];
+__global__ __launch_bounds__(128 * G) void prefill_kernel(PrefillArgs a) {
+  constexpr int NT = 128 * G;                          // threads
+  constexpr int MB = kQW / 16;                         // 16-row query blocks per wave
+  __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kKT * kRow];
+  __shared__ __attribute__((aligned(16))) uint16_t s_v[2][kKT * kRow];
   __shared__ int s_blk[kMaxBlocksLds];
 
   const int tid = threadIdx.x;
@@ -108,22 +126,24 @@ __global__ __launch_bounds__(64 * G) void prefill_kernel(PrefillArgs a) {
   const int pos0 = prefix + t * kQT;                   // position of the tile's first row
   int nkeys = pos0 + rows;                             // keys 0 .. last row's position
   nkeys = nkeys < 0 ? 0 : nkeys;
-  const int h = kh * G + wave;
+  const int h = kh * G + (wave >> 1);
+  const int wrow0 = (wave & 1) * kQW;                  // this wave's first row in the tile
+  const int wpos0 = pos0 + wrow0;
   const int nsteps = (nkeys + kKT - 1) / kKT;
   const int bs = a.block_size;
   const int nblk = (nkeys + bs - 1) / bs;
 
   // block ids of the key range -> LDS (clamped into the pool)
-  for (int e = tid; e < nblk && e < kMaxBlocksLds; e += 64 * G) {
+  for (int e = tid; e < nblk && e < kMaxBlocksLds; e += NT) {
     int b = a.block_tables[(int64_t)s * a.max_bps + e];
     s_blk[e] = b < 0 ? 0 : (b >= a.num_blocks ? a.num_blocks - 1 : b);
   }
 
   // the wave's query rows as B operands: qb[mb][c] = Q[row mb*16 + r][c*32 + 8g .. +8]
-  u32x4 qb[4][4];
+  u32x4 qb[MB][4];
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    const int row = t * kQT + mb * 16 + r;
+  for (int mb = 0; mb < MB; ++mb) {
+    const int row = t * kQT + wrow0 + mb * 16 + r;
     const bool ok = row < qlen;
     const uint16_t* qp = a.q + (int64_t)(q0 + (ok ? row : 0)) * a.q_stride_token +
                          (int64_t)h * a.q_stride_head + g * 8;
@@ -133,14 +153,14 @@ __global__ __launch_bounds__(64 * G) void prefill_kernel(PrefillArgs a) {
   }
   __syncthreads();
 
-  // K/V tile loaders: chunk ch (16 bytes) of the 32 x 256-byte tile
-  constexpr int kChunks = kKT * kD / 8;                // 512
-  constexpr int kPer = (kChunks + 64 * G - 1) / (64 * G);
+  // K/V tile loaders: chunk ch (16 bytes) of the 64 x 256-byte tile
+  constexpr int kChunks = kKT * kD / 8;                // 1024
+  constexpr int kPer = (kChunks + NT - 1) / NT;
   u32x4 kst[kPer], vst[kPer];
   auto fetch = [&](int step) {
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
-      const int ch = tid + e * 64 * G;
+      const int ch = tid + e * NT;
       kst[e] = u32x4{0, 0, 0, 0};
       vst[e] = u32x4{0, 0, 0, 0};
       if (ch < kChunks) {
@@ -165,28 +185,23 @@ __global__ __launch_bounds__(64 * G) void prefill_kernel(PrefillArgs a) {
   auto stash = [&](int buf) {
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
-      const int ch = tid + e * 64 * G;
+      const int ch = tid + e * NT;
       if (ch < kChunks) {
         const int kk = ch >> 4, col = ch & 15;
-        *reinterpret_cast<u32x4*>(&s_k[buf][kk * kKRow + col * 8]) = kst[e];
-        const uint32_t w[4] = {vst[e].x, vst[e].y, vst[e].z, vst[e].w};
-#pragma unroll
-        for (int x = 0; x < 4; ++x) {
-          s_v[buf][(col * 8 + 2 * x) * kVRow + kk] = (uint16_t)(w[x] & 0xffffu);
-          s_v[buf][(col * 8 + 2 * x + 1) * kVRow + kk] = (uint16_t)(w[x] >> 16);
-        }
+        *reinterpret_cast<u32x4*>(&s_k[buf][kk * kRow + col * 8]) = kst[e];
+        *reinterpret_cast<u32x4*>(&s_v[buf][kk * kRow + col * 8]) = vst[e];
       }
     }
   };
 
-  f32x4 oacc[8][4];   // O^T[d = nb*16 + 4g + i][q = mb*16 + r]
+  f32x4 oacc[8][MB];   // O^T[d = nb*16 + 4g + i][q = mb*16 + r]
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb)
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) oacc[nb][mb] = f32x4{0, 0, 0, 0};
-  float mrow[4], lrow[4];
+    for (int mb = 0; mb < MB; ++mb) oacc[nb][mb] = f32x4{0, 0, 0, 0};
+  float mrow[MB], lrow[MB];
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) { mrow[mb] = -INFINITY; lrow[mb] = 0.f; }
+  for (int mb = 0; mb < MB; ++mb) { mrow[mb] = -INFINITY; lrow[mb] = 0.f; }
 
   if (nsteps > 0) {
     fetch(0);
@@ -200,30 +215,32 @@ __global__ __launch_bounds__(64 * G) void prefill_kernel(PrefillArgs a) {
     const uint16_t* vt = s_v[buf];
 
     // S^T = K . Q^T : sacc[n][mb] holds S^T[key = n*16 + 4g + i][q = mb*16 + r]
-    f32x4 sacc[2][4];
+    f32x4 sacc[4][MB];
 #pragma unroll
-    for (int n = 0; n < 2; ++n)
+    for (int n = 0; n < 4; ++n)
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) sacc[n][mb] = f32x4{0, 0, 0, 0};
+      for (int mb = 0; mb < MB; ++mb) sacc[n][mb] = f32x4{0, 0, 0, 0};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
 #pragma unroll
-      for (int n = 0; n < 2; ++n) {
-        const u32x4 ka = *reinterpret_cast<const u32x4*>(&kt[(n * 16 + r) * kKRow + c * 32 + g * 8]);
+      for (int n = 0; n < 4; ++n) {
+        const u32x4 ka = *reinterpret_cast<const u32x4*>(&kt[(n * 16 + r) * kRow + c * 32 + g * 8]);
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) sacc[n][mb] = Mfma<TT>::mma(ka, qb[mb][c], sacc[n][mb]);
+        for (int mb = 0; mb < MB; ++mb) sacc[n][mb] = Mfma<TT>::mma(ka, qb[mb][c], sacc[n][mb]);
       }
     }
-    // scale, causal mask, online softmax (log2 domain)
+    // scale, causal mask, online softmax (log2 domain); pb[kc][mb] is the
+    // B operand of keys kc*32 .. +32: slots e<4 -> key kc*32 + 4g + e,
+    // e>=4 -> kc*32 + 16 + 4g + e - 4
     const int key0 = step * kKT;
-    const bool diag = key0 + kKT - 1 > pos0;   // some key here is after some query
-    u32x4 pb[4];
+    const bool diag = key0 + kKT - 1 > wpos0;   // some key here is after some row
+    u32x4 pb[2][MB];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      const int qpos = pos0 + mb * 16 + r;
-      float v[8];
+    for (int mb = 0; mb < MB; ++mb) {
+      const int qpos = wpos0 + mb * 16 + r;
+      float v[16];
 #pragma unroll
-      for (int n = 0; n < 2; ++n)
+      for (int n = 0; n < 4; ++n)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           float x = sacc[n][mb][i] * a.scale_log2;
@@ -232,7 +249,7 @@ __global__ __launch_bounds__(64 * G) void prefill_kernel(PrefillArgs a) {
         }
       float mx = v[0];
 #pragma unroll
-      for (int e = 1; e < 8; ++e) mx = fmaxf(mx, v[e]);
+      for (int e = 1; e < 16; ++e) mx = fmaxf(mx, v[e]);
       mx = fmaxf(mx, shfl_xor(mx, 16));
       mx = fmaxf(mx, shfl_xor(mx, 32));
       const float mnew = fmaxf(mrow[mb], mx);
@@ -241,30 +258,39 @@ __global__ __launch_bounds__(64 * G) void prefill_kernel(PrefillArgs a) {
       const float mref = mnew == -INFINITY ? 0.f : mnew;
       const float alpha = __builtin_amdgcn_exp2f(mrow[mb] - mref);
       float ls = 0.f;
-      uint32_t packed[4];
+      uint32_t packed[8];
 #pragma unroll
-      for (int e = 0; e < 8; e += 2) {
+      for (int e = 0; e < 16; e += 2) {
         const float p0 = __builtin_amdgcn_exp2f(v[e] - mref);
         const float p1 = __builtin_amdgcn_exp2f(v[e + 1] - mref);
-        const uint32_t u0 = TT::from_float(p0), u1 = TT::from_float(p1);
-        ls += TT::lo(u0) + TT::lo(u1);
-        packed[e / 2] = u0 | (u1 << 16);
+        const uint32_t u = TT::pack2(p0, p1);
+        ls += TT::lo(u) + TT::hi(u);
+        packed[e / 2] = u;
       }
       lrow[mb] = lrow[mb] * alpha + ls;
       mrow[mb] = mnew;
-      pb[mb] = u32x4{packed[0], packed[1], packed[2], packed[3]};
+      // packed[n*2 + i/2] holds keys n*16 + 4g + i, i in pairs
+      pb[0][mb] = u32x4{packed[0], packed[1], packed[2], packed[3]};
+      pb[1][mb] = u32x4{packed[4], packed[5], packed[6], packed[7]};
+      if (__ballot(alpha != 1.f) != 0) {
 #pragma unroll
-      for (int nb = 0; nb < 8; ++nb) oacc[nb][mb] *= alpha;
+        for (int nb = 0; nb < 8; ++nb) oacc[nb][mb] *= alpha;
+      }
     }
-    // O^T += V^T . P^T ; A = V^T[d = nb*16 + r][keys 4g..4g+3, 16+4g..16+4g+3]
+    // O^T += V^T . P^T ; A = V^T[d = nb*16 + r][keys kc*32 + {4g..4g+3, 16+4g..16+4g+3}]
+    // transposing reads: lane r of group g addresses key (.. + 4g + r/4),
+    // dims nb*16 + 4*(r%4) .. +3, and receives dim nb*16 + r of keys +0..3
+    const uint16_t* vlane = vt + (g * 4 + (r >> 2)) * kRow + 4 * (r & 3);
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) {
-      const uint16_t* vr = &vt[(nb * 16 + r) * kVRow];
-      const u32x2 lo = *reinterpret_cast<const u32x2*>(vr + g * 4);
-      const u32x2 hi = *reinterpret_cast<const u32x2*>(vr + 16 + g * 4);
-      const u32x4 va = u32x4{lo.x, lo.y, hi.x, hi.y};
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) oacc[nb][mb] = Mfma<TT>::mma(va, pb[mb], oacc[nb][mb]);
+      for (int kc = 0; kc < 2; ++kc) {
+        const u32x2 lo = lds_read_tr(vlane + (kc * 32) * kRow + nb * 16);
+        const u32x2 hi = lds_read_tr(vlane + (kc * 32 + 16) * kRow + nb * 16);
+        const u32x4 va = u32x4{lo.x, lo.y, hi.x, hi.y};
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) oacc[nb][mb] = Mfma<TT>::mma(va, pb[kc][mb], oacc[nb][mb]);
+      }
     }
     // buf ^ 1 was last read in the previous step, which every wave finished
     // before that step's barrier
@@ -274,20 +300,20 @@ __global__ __launch_bounds__(64 * G) void prefill_kernel(PrefillArgs a) {
 
   // normalise and store: lane writes d = nb*16 + 4g .. +3 of query row mb*16 + r
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
+  for (int mb = 0; mb < MB; ++mb) {
     float l = lrow[mb];
     l += shfl_xor(l, 16);
     l += shfl_xor(l, 32);
-    const int row = t * kQT + mb * 16 + r;
+    const int row = t * kQT + wrow0 + mb * 16 + r;
     if (row >= qlen) continue;
-    const float inv = (l > 0.f && pos0 + mb * 16 + r >= 0) ? 1.f / l : 0.f;
+    const float inv = (l > 0.f && wpos0 + mb * 16 + r >= 0) ? 1.f / l : 0.f;
     uint16_t* op = a.out + (int64_t)(q0 + row) * a.out_stride_token + (int64_t)h * a.out_stride_head;
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) {
       const f32x4 o = oacc[nb][mb];
       u32x2 w;
-      w.x = TT::from_float(o[0] * inv) | (TT::from_float(o[1] * inv) << 16);
-      w.y = TT::from_float(o[2] * inv) | (TT::from_float(o[3] * inv) << 16);
+      w.x = TT::pack2(o[0] * inv, o[1] * inv);
+      w.y = TT::pack2(o[2] * inv, o[3] * inv);
       *reinterpret_cast<u32x2*>(op + nb * 16 + g * 4) = w;
     }
   }
@@ -296,11 +322,11 @@ __global__ __launch_bounds__(64 * G) void prefill_kernel(PrefillArgs a) {
 template <class TT>
 int launch(int g, const PrefillArgs& a, int64_t grid, hipStream_t st) {
   switch (g) {
-    case 1: hipLaunchKernelGGL((prefill_kernel<TT, 1>), dim3((unsigned)grid), dim3(64), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((prefill_kernel<TT, 2>), dim3((unsigned)grid), dim3(128), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((prefill_kernel<TT, 4>), dim3((unsigned)grid), dim3(256), 0, st, a); break;
-    case 6: hipLaunchKernelGGL((prefill_kernel<TT, 6>), dim3((unsigned)grid), dim3(384), 0, st, a); break;
-    case 8: hipLaunchKernelGGL((prefill_kernel<TT, 8>), dim3((unsigned)grid), dim3(512), 0, st, a); break;
+    case 1: hipLaunchKernelGGL((prefill_kernel<TT, 1>), dim3((unsigned)grid), dim3(128), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((prefill_kernel<TT, 2>), dim3((unsigned)grid), dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((prefill_kernel<TT, 4>), dim3((unsigned)grid), dim3(512), 0, st, a); break;
+    case 6: hipLaunchKernelGGL((prefill_kernel<TT, 6>), dim3((unsigned)grid), dim3(768), 0, st, a); break;
+    case 8: hipLaunchKernelGGL((prefill_kernel<TT, 8>), dim3((unsigned)grid), dim3(1024), 0, st, a); break;
     default: return npd::fail(NPD_E_INVALID, "npd_paged_prefill_attention: group size %d", g);
   }
   return npd::check_launch("npd_paged_prefill_attention");
