@@ -133,7 +133,8 @@ def bench_decode(args, w) -> dict:
         "ms_per_step": ms_step,
         "value": step_bytes / (ms_step * 1e-3) / 1e9,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": _profiled_traffic(f"decode_d128_kernel/{w.name}")},
         "detail": {
             "attention_us_mean": round(attn_avg * 1e3, 2),
             "attention_us_median": round(statistics.median(attn_ms) * 1e3, 2),
@@ -147,6 +148,114 @@ def bench_decode(args, w) -> dict:
             "kernels": "decode_d128_kernel (partitions + fused log-sum-exp merge)",
         },
     }
+
+
+def cpu_baseline_prefill(w, budget_s: float = 15.0) -> dict:
+    """The reference's prefill attention (oracle/torch_ref.py ref_prefill_sdpa,
+    restating nanoPD/engine/model_runner.py:152-168: SDPA over the packed chunks
+    with a block-diagonal causal mask, no paged prefix) on host cores, over
+    the first chunks whose run fits the time budget. Its FLOPs are counted
+    for the work it does (the chunk-causal part only)."""
+    from oracle.torch_ref import ref_prefill_sdpa
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    npf = w.num_prefill_seqs
+    chunks = w.chunk_lens[:npf]
+    H, D = w.num_heads, w.head_dim
+    q, k, v = w.query.cpu(), w.new_k.cpu(), w.new_v.cpu()
+    t0 = time.perf_counter()
+    ref_prefill_sdpa(q[:chunks[0]], k[:chunks[0]], v[:chunks[0]], chunks[:1], w.scale)
+    per_chunk = max(time.perf_counter() - t0, 1e-4)
+    n = max(1, min(npf, int(budget_s / 5 / per_chunk)))
+    t = sum(chunks[:n])
+    reps = []
+    start = time.perf_counter()
+    while len(reps) < 5 or time.perf_counter() - start < budget_s:
+        t0 = time.perf_counter()
+        ref_prefill_sdpa(q[:t], k[:t], v[:t], chunks[:n], w.scale)
+        reps.append(time.perf_counter() - t0)
+    med = statistics.median(reps)
+    flops = 4 * H * D * sum(c * (c + 1) // 2 for c in chunks[:n])
+    return {"value": round(flops / med / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"ref_prefill_sdpa (torch CPU SDPA, fp32, chunk-only causal as the reference "
+                      f"computes it) on {n} of {npf} chunks of {chunks[0]} tokens, median of "
+                      f"{len(reps)} runs = {med * 1e3:.1f} ms; CPU: {_cpu_model()}"}
+
+
+def bench_prefill(args, w) -> dict:
+    """Configuration 3: one step = slot store of every new token, the prefill
+    op over the 4 chunks (paged prefix + chunk), the decode op over the 48
+    decode rows. Roofline: the prefill kernel against the bf16 MFMA peak,
+    counting the useful (unmasked causal) FLOPs."""
+    from nanopd_amd import paged_kernels as pk
+    npf, tp = w.num_prefill_seqs, w.num_prefill_tokens
+    mb = w.block_tables.size(1)
+    bt_p, cu_p, cl_p = (w.block_tables[:npf].contiguous(), w.cu_seqlens_q[:npf + 1].contiguous(),
+                        w.context_lens[:npf].contiguous())
+    bt_d, cl_d = w.block_tables[npf:].contiguous(), w.context_lens[npf:].contiguous()
+    out = torch.empty_like(w.query)
+    max_q = max(w.chunk_lens[:npf])
+
+    def store():
+        pk.paged_kv_store_slots(w.k_cache, w.v_cache, w.new_k, w.new_v, w.slot_mapping)
+
+    def prefill():
+        pk.paged_prefill_attention(out[:tp], w.query[:tp], w.k_cache, w.v_cache, bt_p, cu_p, cl_p,
+                                   w.scale, w.block_size, mb, max_q)
+
+    def decode():
+        pk.paged_attention_forward(out[tp:], w.query[tp:], w.k_cache, w.v_cache, bt_d, cl_d,
+                                   w.scale, w.block_size, mb)
+
+    for _ in range(args.warmup):
+        store()
+        prefill()
+        decode()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for a, b in ev:
+        store()
+        a.record()
+        prefill()
+        b.record()
+        decode()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    pf_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
+    ms_step = wall * 1e3 / args.steps
+    flops = w.prefill_flops()
+    tflops = flops / (pf_ms * 1e-3) / 1e12
+    return {
+        "ms_per_step": ms_step,
+        "value": flops / (ms_step * 1e-3) / 1e12,
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                     "traffic": _profiled_traffic(f"prefill_kernel/{w.name}")},
+        "detail": {
+            "prefill_us_mean": round(pf_ms * 1e3, 2),
+            "store_us_median": round(statistics.median(_events_ms(store, 20)) * 1e3, 2),
+            "decode_us_median": round(statistics.median(_events_ms(decode, 20)) * 1e3, 2),
+            "prefill_flops": flops,
+            "prefill_tokens": tp,
+            "decode_seqs": len(w.chunk_lens) - npf,
+            "kernels": "prefill_kernel (MFMA 16x16x32) + kv_store_kernel + decode_d128_kernel",
+        },
+    }
+
+
+def _profiled_traffic(key: str):
+    """HBM bytes per launch of a kernel, from the committed rocprofv3 counter
+    summary (FETCH_SIZE and WRITE_SIZE runs, scaled by a plain copy's counter
+    reading); None where no profile was taken."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            rec = json.load(f).get(key)
+    except (OSError, ValueError):
+        return None
+    return None if rec is None else rec.get("bytes")
 
 
 def bench_copy(args, dev) -> int:
@@ -174,13 +283,46 @@ def bench_copy(args, dev) -> int:
     return 0
 
 
+def emit_prefill(args, w) -> int:
+    from nanopd_amd import paged_kernels as pk
+    pk.paged_kv_store_slots(w.k_cache, w.v_cache, w.new_k, w.new_v, w.slot_mapping)
+    res = bench_prefill(args, w)
+    line = {
+        "metric": "Chunked-prefill attention TFLOP/s (useful causal FLOPs per mixed step)",
+        "value": round(res["value"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)*0.5 values, shuffled block tables)",
+        "config": {"workload": w.name, "num_heads": w.num_heads, "num_kv_heads": w.num_kv_heads,
+                   "head_dim": w.head_dim, "block_size": w.block_size,
+                   "chunks": w.chunk_lens[:w.num_prefill_seqs],
+                   "prefixes": w.ctx_before[:w.num_prefill_seqs],
+                   "decodes": len(w.chunk_lens) - w.num_prefill_seqs,
+                   "step": "slot store of all new tokens + prefill op + decode op"},
+        "roofline": res["roofline"],
+        "detail": res["detail"],
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline_prefill(w)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=["decode", "long", "copy"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "long", "prefill", "copy"], default="decode",
                     help="decode: config 2 (default); long: config 4 (8 seqs, 8k-32k); "
+                         "prefill: config 3 (4 chunks of 512 on paged prefixes + 48 decodes); "
                          "copy: a plain 256 MiB device copy, the calibration kernel for "
                          "the FETCH_SIZE / WRITE_SIZE counters")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -197,6 +339,8 @@ def main() -> int:
     dev = torch.device("cuda:0")
     if args.workload == "copy":
         return bench_copy(args, dev)
+    if args.workload == "prefill":
+        return emit_prefill(args, workloads.config3(dev))
     if args.workload == "decode":
         w = workloads.config2(dev)
     else:
