@@ -139,8 +139,15 @@ int64_t npd_paged_prefill_workspace_size(int64_t num_seqs, int64_t total_q,
  * [total_q, H, D]; its chunk K/V must already be stored in the pool;
  * context_lens[s] counts prefix + chunk tokens. Query row i of s sits at
  * position p = context_lens[s] - q_len_s + i and attends to keys 0..p.
- * Rows with p < 0 (context shorter than the chunk) get zeros.
- * max_q_len / max_context_len: host-known upper bounds used to size the grid.
+ * Rows with p < 0 (context shorter than the chunk) get zeros. scale must be
+ * positive and finite.
+ * max_q_len: host-known upper bound on the chunk lengths (grid size).
+ * max_context_len: host-known upper bound on context_lens; key ranges longer
+ * than 1024 keys are split over up to 8 workgroups when it allows (<= 0: no
+ * split). It sizes the workspace: npd_paged_prefill_workspace_size(...) bytes,
+ * 256-byte aligned, zero-filled before first use; every call leaves its merge
+ * counters at zero, so calls that share a workspace must be ordered on one
+ * stream.
  */
 int npd_paged_prefill_attention(void* out, const void* query,
                                 const void* key_cache, const void* value_cache,

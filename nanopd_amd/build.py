@@ -20,12 +20,19 @@ LIB_DIR = PKG / "lib"
 LIB_PATH = LIB_DIR / "libnanopd_hip.so"
 ARCH = os.environ.get("NPD_OFFLOAD_ARCH", "gfx950")
 
-# Packed-FP32 VALU ops are kept out of the generated code (see DESIGN.md,
-# "compiler flags"); the host pass warns that it does not know the feature.
+# Packed-FP32 VALU ops (v_pk_fma_f32 and kin) are kept out of the generated
+# code: some of their forms have given wrong results on this hardware pool.
+# The host pass warns that it does not know the feature.
 COMMON_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
+# Per-file additions. prefill_attention: attention scores are finite or -inf
+# (masked keys), so the row maxima need no NaN quieting (v_max_f32 x, x, x
+# before every max).
+FILE_FLAGS = {
+    "prefill_attention.hip": ["-fno-honor-nans"],
+}
 
 
 def _hipcc() -> str:
@@ -41,7 +48,8 @@ def sources() -> list[Path]:
 
 def _compile(hipcc: str, src: Path, verbose: bool) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc, f"--offload-arch={ARCH}", *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc, f"--offload-arch={ARCH}", *COMMON_FLAGS, *FILE_FLAGS.get(src.name, []), "-c",
+           str(src), "-o", str(obj)]
     if src.suffix == ".cpp":
         cmd.insert(1, "-x")
         cmd.insert(2, "hip")

@@ -24,6 +24,7 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 // f32 -> bf16 rounds to nearest even, NaN stays NaN.
 // ---------------------------------------------------------------------------
 struct BF16 {
+  static constexpr uint32_t kOne2 = 0x3f803f80u;   // packed (1.0, 1.0)
   static __device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
   static __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
   static __device__ __forceinline__ uint32_t from_float(float f) {
@@ -46,6 +47,7 @@ struct BF16 {
 };
 
 struct F16 {
+  static constexpr uint32_t kOne2 = 0x3c003c00u;   // packed (1.0, 1.0)
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
   static __device__ __forceinline__ float lo(uint32_t w) {
     return static_cast<float>(__builtin_bit_cast(h2, w).x);
@@ -67,5 +69,21 @@ struct F16 {
     return __builtin_bit_cast(uint32_t, v);
   }
 };
+
+// Agent-scope relaxed atomic accesses: written through to, and read from, the
+// device-coherent level, so partials published by a workgroup on one XCD are
+// seen by a workgroup on another without an L2 writeback or invalidate.
+// 8-byte granularity. A writer waits for its stores to complete
+// (s_waitcnt 0) before it signals, through an atomic counter, that they are there.
+__device__ __forceinline__ void st_coherent2(float* p, float x, float y) {
+  const uint64_t v = (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ld_coherent2(const float* p, float& x, float& y) {
+  const uint64_t v = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+  x = __uint_as_float((uint32_t)v);
+  y = __uint_as_float((uint32_t)(v >> 32));
+}
 
 }  // namespace npd

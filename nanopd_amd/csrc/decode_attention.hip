@@ -433,19 +433,8 @@ __device__ __forceinline__ void bfly_stage(float* v, bool upper) {
   }
 }
 
-// Agent-scope relaxed atomic accesses: written through to, and read from, the
-// device-coherent level, so partials published by one XCD are seen by another
-// without L2 writeback/invalidate. 8-byte granularity.
-__device__ __forceinline__ void st_coherent2(float* p, float x, float y) {
-  const uint64_t v = (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void ld_coherent2(const float* p, float& x, float& y) {
-  const uint64_t v = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-  x = __uint_as_float((uint32_t)v);
-  y = __uint_as_float((uint32_t)(v >> 32));
-}
+using npd::ld_coherent2;
+using npd::st_coherent2;
 
 // Merge of one (sequence, kv-head) by a single wave (fast path, D = 128), the
 // same log-sum-exp merge as merge_unit but latency-bound work done in parallel:

@@ -10,18 +10,23 @@
 // them before attending, model_runner.py:146). For an empty prefix both agree.
 //
 // MI355X design (gfx950, v_mfma_f32_16x16x32_{bf16,f16}, wave64):
-//   workgroup = one (sequence, kv-head, tile of 64 query positions) with 2*G
-//   waves: wave w serves query head kv*G + w/2 and the 32 query rows
-//   (w%2)*32 .. +32 of the tile. Each 64-key K/V tile is gathered from the
-//   pool once into LDS and used by all 2*G waves (GQA reuse); two waves per
-//   SIMD let one wave's softmax (VALU) run under the other's MFMAs.
+//   workgroup = 4 waves = one (sequence, kv-head, head group, query tile, key
+//   split). A wave owns one query head and 64 query rows, so the 64-key K/V
+//   tile that the workgroup gathers from the pool into LDS is read from LDS
+//   once per 64 rows (GQA heads and, for small groups, neighbouring row tiles
+//   share it). HW = gcd(G, 4) heads per workgroup, 4 / HW row tiles of 64.
+//   One wave per SIMD (up to 512 VGPRs, accumulators in AGPRs).
 //   per step of 64 keys, each wave:
 //     S^T = K . Q^T   -- A = K rows from LDS, B = the wave's query rows, kept
 //                        in registers for the whole key loop;
-//     online softmax  -- lane l owns query (mb*16 + l%16) of each 16-row block:
-//                        16 of its 64 scores per step are in-lane, the rest in
-//                        lanes l^16, l^32; the O rescale is skipped when no
-//                        row maximum moved;
+//     softmax          -- lane l holds 16 keys of query (mb*16 + l%16) of each
+//                        16-row block; the rest are in lanes l^16, l^32.
+//                        Scale and max subtraction are one FMA before exp2;
+//                        the row sum is a v_dot2 of the rounded P pair with
+//                        (1, 1). The running max is only moved (and O
+//                        rescaled) when a row's new max exceeds it by more than
+//                        2^kTau: P entries then stay <= 2^kTau, exact in fp32
+//                        accumulation, and the rescale is rare after step 1;
 //     O^T += V^T . P^T -- P^T is the S^T accumulator, already in B-operand
 //                        layout (packed with v_cvt_pk_bf16_f32); V stays
 //                        row-major in LDS like K, and the V^T A operand is two
@@ -34,6 +39,18 @@
 //   K/V tiles are double-buffered in LDS: the next tile's global loads are in
 //   flight while the current one is multiplied. Keys past the visible range
 //   are written as zeros and masked, so no NaN from stale pool memory leaks in.
+//
+// Key splits: a query tile whose key range is longer than kSplitSteps steps is
+// cut into nsp <= splits_max near-equal ranges run by separate workgroups (the
+// tiles of a long prefix would otherwise run many times longer than the rest).
+// Each split publishes its unnormalised O, running max and row sum with
+// device-coherent stores, then takes a ticket from a per-tile counter; the last
+// of the nsp to arrive merges the others into its registers
+//   M = max_j m_j,  L = sum_j l_j 2^(m_j - M),  O = sum_j O_j 2^(m_j - M) / L
+// writes the output and resets the counter to 0. Workgroups are ordered last
+// query tile first, a tile's splits adjacent, so the longest work starts first.
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
@@ -45,15 +62,24 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kD = 128;          // head_dim of this kernel
-constexpr int kQT = 64;          // query positions per workgroup
-constexpr int kQW = 32;          // query rows per wave
+constexpr int kWaves = 8;        // waves per workgroup: 2 per SIMD
+constexpr int kThreads = 64 * kWaves;
+constexpr int kPairs = kWaves / 2;   // (head, 64-row tile) pairs, two 32-row waves each
+constexpr int kWaveRows = 32;    // query rows per wave
 constexpr int kKT = 64;          // keys per step
+constexpr int kDepth = 3;        // K/V tiles in flight per workgroup
 // LDS row of the K and V tiles (elements): 72 dwords, an 8-bank shift per row,
 // so 16 rows of K read at one column and 4 rows x 32 bytes of a transposing
 // V read both hit distinct banks
 constexpr int kRow = kD + 16;
-constexpr int kMaxBlocksLds = 1024;   // block ids of one workgroup's key range kept in LDS
+constexpr int kMaxBlocksLds = 16384;  // block ids of one workgroup's key range kept in LDS (64 KB)
+constexpr int kSplitSteps = 16;       // a key range longer than this many steps is split
+constexpr int kMaxSplits = 8;
+constexpr float kTau = 8.f;           // lazy-rescale threshold, log2 units
 constexpr float kLog2e = 1.4426950408889634f;
+// partial record of one wave (32 rows of one head, one split), floats
+constexpr int kRecO = 16 * 2 * 64 * 2;   // [nb*2 + mb][half][lane][2]
+constexpr int kRecML = 2 * 64 * 2;       // [mb][lane][m, l]
 
 struct PrefillArgs {
   uint16_t* out;
@@ -63,7 +89,11 @@ struct PrefillArgs {
   const int32_t* block_tables;
   const int32_t* cu_seqlens_q;
   const int32_t* context_lens;
-  int num_seqs, num_kv_heads, block_size, num_blocks, max_bps, tiles_max;
+  int* counters;
+  float* part_o;
+  float* part_ml;
+  int num_seqs, num_kv_heads, group, hgroups, block_size, bs_shift, num_blocks, max_bps;
+  int tiles_max, subtiles, splits_max;   // subtiles: 32-row subtiles per sequence
   float scale_log2;
   int64_t q_stride_token, q_stride_head, out_stride_token, out_stride_head;
 };
@@ -96,101 +126,126 @@ __device__ __forceinline__ u32x2 lds_read_tr(const uint16_t* p) {
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p)));
 }
 
-template <class TT, int G>
-__global__ __launch_bounds__(128 * G) void prefill_kernel(PrefillArgs a) {
-  constexpr int NT = 128 * G;                          // threads
-  constexpr int MB = kQW / 16;                         // 16-row query blocks per wave
+template <class TT, int HW>
+__global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
+  constexpr int RT = kPairs / HW;                      // row tiles of 64 per workgroup
+  constexpr int TR = 64 * RT;                          // query rows per workgroup
+  constexpr int MB = kWaveRows / 16;                   // 16-row query blocks per wave
   __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kKT * kRow];
-  __shared__ __attribute__((aligned(16))) uint16_t s_v[2][kKT * kRow];
+  __shared__ __attribute__((aligned(16))) uint16_t s_v[3][kKT * kRow];
   __shared__ int s_blk[kMaxBlocksLds];
+  __shared__ int s_ticket;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, r = lane & 15;
 
-  // item: tiles of a sequence are visited last-tile first (they see the most keys)
-  const int per_seq = a.num_kv_heads * a.tiles_max;
-  const int s = blockIdx.x / per_seq;
-  const int rem = blockIdx.x - s * per_seq;
-  const int kh = rem / a.tiles_max;
-  const int t = a.tiles_max - 1 - (rem - kh * a.tiles_max);
+  // unit = (tile, last first; sequence; kv-head x head group; split)
+  int b = blockIdx.x;
+  const int j = b % a.splits_max;
+  b /= a.splits_max;
+  const int nhg = a.num_kv_heads * a.hgroups;
+  const int khg = b % nhg;
+  b /= nhg;
+  const int s = b % a.num_seqs;
+  const int t = a.tiles_max - 1 - b / a.num_seqs;
+  const int kh = khg / a.hgroups, hg = khg - kh * a.hgroups;
 
-  const int q0 = a.cu_seqlens_q[s], q1 = a.cu_seqlens_q[s + 1];
-  const int qlen = q1 - q0;
-  if (t * kQT >= qlen) return;
+  const int q0 = a.cu_seqlens_q[s];
+  const int qlen = a.cu_seqlens_q[s + 1] - q0;
+  if (t * TR >= qlen) return;
   const int cap = a.max_bps * a.block_size;
   int ctx = a.context_lens[s];
-  ctx = ctx < cap ? ctx : cap;
+  ctx = ctx < 0 ? 0 : (ctx < cap ? ctx : cap);
   const int prefix = ctx - qlen;                       // position of query row 0
-  const int rows = (qlen - t * kQT) < kQT ? (qlen - t * kQT) : kQT;
-  const int pos0 = prefix + t * kQT;                   // position of the tile's first row
+  const int rows = (qlen - t * TR) < TR ? (qlen - t * TR) : TR;
+  const int pos0 = prefix + t * TR;                    // position of the tile's first row
   int nkeys = pos0 + rows;                             // keys 0 .. last row's position
   nkeys = nkeys < 0 ? 0 : nkeys;
-  const int h = kh * G + (wave >> 1);
-  const int wrow0 = (wave & 1) * kQW;                  // this wave's first row in the tile
-  const int wpos0 = pos0 + wrow0;
   const int nsteps = (nkeys + kKT - 1) / kKT;
-  const int bs = a.block_size;
-  const int nblk = (nkeys + bs - 1) / bs;
+  int nsp = (nsteps + kSplitSteps - 1) / kSplitSteps;
+  nsp = nsp < 1 ? 1 : (nsp > a.splits_max ? a.splits_max : nsp);
+  if (j >= nsp) return;
+  const int st0 = (int)((int64_t)nsteps * j / nsp);
+  const int st1 = (int)((int64_t)nsteps * (j + 1) / nsp);
 
-  // block ids of the key range -> LDS (clamped into the pool)
-  for (int e = tid; e < nblk && e < kMaxBlocksLds; e += NT) {
-    int b = a.block_tables[(int64_t)s * a.max_bps + e];
-    s_blk[e] = b < 0 ? 0 : (b >= a.num_blocks ? a.num_blocks - 1 : b);
+  // wave -> (head of the group, row tile, half of the row tile)
+  const int pair = wave >> 1, half = wave & 1;
+  const int wr = pair / HW;
+  const int h = kh * a.group + hg * HW + (pair - wr * HW);
+  const int wsub = (t * RT + wr) * 2 + half;           // 32-row subtile index in the sequence
+  const int wrow0 = wsub * kWaveRows;                  // this wave's first row
+  const int wpos0 = prefix + wrow0;
+  const int bs = a.block_size;
+  const int kbeg = st0 * kKT;
+  const int kend = st1 * kKT < nkeys ? st1 * kKT : nkeys;
+  const int blk0 = kbeg / bs;
+  const int nblk = kend > kbeg ? (kend + bs - 1) / bs - blk0 : 0;
+
+  if (st0 >= st1) {
+    // no key at all (every row of the tile sits before position 0): zero rows
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int row = wrow0 + mb * 16 + r;
+      if (row >= qlen) continue;
+      uint16_t* op = a.out + (int64_t)(q0 + row) * a.out_stride_token + (int64_t)h * a.out_stride_head;
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) *reinterpret_cast<u32x2*>(op + nb * 16 + g * 4) = u32x2{0, 0};
+    }
+    return;
   }
 
-  // the wave's query rows as B operands: qb[mb][c] = Q[row mb*16 + r][c*32 + 8g .. +8]
+  // block ids of the split's key range -> LDS (clamped into the pool); the
+  // host guarantees max_bps <= kMaxBlocksLds, so the whole range fits
+  for (int e = tid; e < nblk; e += kThreads) {
+    int bid = a.block_tables[(int64_t)s * a.max_bps + blk0 + e];
+    s_blk[e] = bid < 0 ? 0 : (bid >= a.num_blocks ? a.num_blocks - 1 : bid);
+  }
+
+  // the wave's query rows as B operands: qb[mb][c] = Q[row mb*16 + r][c*32 + 8g .. +8].
+  // Rows past the chunk read its last row (their outputs are never stored):
+  // unconditional loads keep the compiler's count of loads in flight exact.
   u32x4 qb[MB][4];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
-    const int row = t * kQT + wrow0 + mb * 16 + r;
-    const bool ok = row < qlen;
-    const uint16_t* qp = a.q + (int64_t)(q0 + (ok ? row : 0)) * a.q_stride_token +
+    int row = wrow0 + mb * 16 + r;
+    row = row < qlen ? row : qlen - 1;
+    const uint16_t* qp = a.q + (int64_t)(q0 + row) * a.q_stride_token +
                          (int64_t)h * a.q_stride_head + g * 8;
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-      qb[mb][c] = ok ? *reinterpret_cast<const u32x4*>(qp + c * 32) : u32x4{0, 0, 0, 0};
+    for (int c = 0; c < 4; ++c) qb[mb][c] = *reinterpret_cast<const u32x4*>(qp + c * 32);
   }
   __syncthreads();
 
-  // K/V tile loaders: chunk ch (16 bytes) of the 64 x 256-byte tile
-  constexpr int kChunks = kKT * kD / 8;                // 1024
-  constexpr int kPer = (kChunks + NT - 1) / NT;
-  u32x4 kst[kPer], vst[kPer];
-  auto fetch = [&](int step) {
+  // K/V tile loaders: chunk tid + 512e (16 bytes) of the 64 x 256-byte tile,
+  // i.e. key (tid >> 4) + 32e, column tid & 15. Loads run kDepth steps ahead
+  // through a register ring (slot = step % kDepth): one 32 KB tile in flight
+  // per CU leaves a step waiting on memory latency.
+  constexpr int kPer = kKT * kD / 8 / kThreads;        // 2
+  u32x4 kst[kDepth][kPer], vst[kDepth][kPer];
+  const int col = tid & 15;
+  // Every fetch issues the same loads (tokens clamped into the split's range,
+  // out-of-range ones zeroed when written to LDS), so the compiler's count of
+  // loads in flight stays exact and its waits cover only the slot being used.
+  auto fetch = [&](int step, u32x4* ks, u32x4* vs) {
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
-      const int ch = tid + e * NT;
-      kst[e] = u32x4{0, 0, 0, 0};
-      vst[e] = u32x4{0, 0, 0, 0};
-      if (ch < kChunks) {
-        const int kk = ch >> 4, col = ch & 15;
-        const int tok = step * kKT + kk;
-        if (tok < nkeys) {
-          const int lb = tok / bs;
-          int blk;
-          if (lb < kMaxBlocksLds) {
-            blk = s_blk[lb];
-          } else {
-            blk = a.block_tables[(int64_t)s * a.max_bps + lb];
-            blk = blk < 0 ? 0 : (blk >= a.num_blocks ? a.num_blocks - 1 : blk);
-          }
-          const int64_t idx = (((int64_t)blk * a.num_kv_heads + kh) * bs + (tok - lb * bs)) * 16 + col;
-          kst[e] = a.k_cache[idx];
-          vst[e] = a.v_cache[idx];
-        }
-      }
+      int tok = step * kKT + (tid >> 4) + 32 * e;
+      tok = tok < kend ? tok : kend - 1;
+      const int lb = a.bs_shift >= 0 ? tok >> a.bs_shift : tok / bs;
+      const int blk = s_blk[lb - blk0];
+      const int64_t idx = (((int64_t)blk * a.num_kv_heads + kh) * bs + (tok - lb * bs)) * 16 + col;
+      ks[e] = a.k_cache[idx];
+      vs[e] = a.v_cache[idx];
     }
   };
-  auto stash = [&](int buf) {
+  auto stash = [&](int step, int kbuf, int vbuf, const u32x4* ks, const u32x4* vs) {
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
-      const int ch = tid + e * NT;
-      if (ch < kChunks) {
-        const int kk = ch >> 4, col = ch & 15;
-        *reinterpret_cast<u32x4*>(&s_k[buf][kk * kRow + col * 8]) = kst[e];
-        *reinterpret_cast<u32x4*>(&s_v[buf][kk * kRow + col * 8]) = vst[e];
-      }
+      const int kk = (tid >> 4) + 32 * e;
+      const bool ok = step * kKT + kk < nkeys;
+      *reinterpret_cast<u32x4*>(&s_k[kbuf][kk * kRow + col * 8]) = ok ? ks[e] : u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(&s_v[vbuf][kk * kRow + col * 8]) = ok ? vs[e] : u32x4{0, 0, 0, 0};
     }
   };
 
@@ -199,23 +254,27 @@ __global__ __launch_bounds__(128 * G) void prefill_kernel(PrefillArgs a) {
   for (int nb = 0; nb < 8; ++nb)
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) oacc[nb][mb] = f32x4{0, 0, 0, 0};
-  float mrow[MB], lrow[MB];
+  float mrow[MB], nmref[MB], lrow[MB];   // running max (log2 units), -max or 0, row sum
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) { mrow[mb] = -INFINITY; lrow[mb] = 0.f; }
-
-  if (nsteps > 0) {
-    fetch(0);
-    stash(0);
+  for (int mb = 0; mb < MB; ++mb) {
+    mrow[mb] = -INFINITY;
+    nmref[mb] = 0.f;
+    lrow[mb] = 0.f;
   }
-  __syncthreads();
-  for (int step = 0; step < nsteps; ++step) {
-    const int buf = step & 1;
-    if (step + 1 < nsteps) fetch(step + 1);
-    const uint16_t* kt = s_k[buf];
-    const uint16_t* vt = s_v[buf];
+  const float c2 = a.scale_log2;
 
-    // S^T = K . Q^T : sacc[n][mb] holds S^T[key = n*16 + 4g + i][q = mb*16 + r]
-    f32x4 sacc[4][MB];
+#pragma unroll
+  for (int d = 0; d < kDepth; ++d) fetch(st0 + d, kst[d], vst[d]);
+  stash(st0, 0, 0, kst[0], vst[0]);
+  __syncthreads();
+
+  // Step pieces. qk: S^T of step `step` from K buffer kbuf; softmax: P of
+  // that step into pb (moves the running max and rescales O when needed);
+  // pv: O^T += V^T . P^T from V buffer vbuf.
+  f32x4 sacc[4][MB];   // S^T[key = n*16 + 4g + i][q = mb*16 + r]
+  auto qk = [&](int kbuf) {
+    const uint16_t* kt = s_k[kbuf];
+    // S^T = K . Q^T
 #pragma unroll
     for (int n = 0; n < 4; ++n)
 #pragma unroll
@@ -229,58 +288,65 @@ __global__ __launch_bounds__(128 * G) void prefill_kernel(PrefillArgs a) {
         for (int mb = 0; mb < MB; ++mb) sacc[n][mb] = Mfma<TT>::mma(ka, qb[mb][c], sacc[n][mb]);
       }
     }
-    // scale, causal mask, online softmax (log2 domain); pb[kc][mb] is the
-    // B operand of keys kc*32 .. +32: slots e<4 -> key kc*32 + 4g + e,
-    // e>=4 -> kc*32 + 16 + 4g + e - 4
+  };
+  auto softmax = [&](int step, u32x4 (&pb)[2][MB]) {
     const int key0 = step * kKT;
+    // causal mask, lazy-max softmax; pb[kc][mb] is the B operand of keys
+    // kc*32 .. +32: slots e<4 -> key kc*32 + 4g + e, e>=4 -> kc*32 + 16 + 4g + e - 4
     const bool diag = key0 + kKT - 1 > wpos0;   // some key here is after some row
-    u32x4 pb[2][MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
-      const int qpos = wpos0 + mb * 16 + r;
       float v[16];
 #pragma unroll
       for (int n = 0; n < 4; ++n)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float x = sacc[n][mb][i] * a.scale_log2;
-          if (diag && key0 + n * 16 + g * 4 + i > qpos) x = -INFINITY;
-          v[n * 4 + i] = x;
-        }
-      float mx = v[0];
+        for (int i = 0; i < 4; ++i) v[n * 4 + i] = sacc[n][mb][i];
+      if (diag) {
+        // key n*16 + 4g + i of this step is visible to the row iff n*16 + i <= lim
+        const int lim = wpos0 + mb * 16 + r - key0 - 4 * g;
 #pragma unroll
-      for (int e = 1; e < 16; ++e) mx = fmaxf(mx, v[e]);
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (n * 16 + i > lim) v[n * 4 + i] = -INFINITY;
+      }
+      float mx = fmaxf(v[0], fmaxf(v[1], v[2]));
+#pragma unroll
+      for (int e = 3; e < 15; e += 2) mx = fmaxf(mx, fmaxf(v[e], v[e + 1]));
+      mx = fmaxf(mx, v[15]);
       mx = fmaxf(mx, shfl_xor(mx, 16));
       mx = fmaxf(mx, shfl_xor(mx, 32));
-      const float mnew = fmaxf(mrow[mb], mx);
-      // a row that has seen only masked keys keeps m = -inf: use 0 as the
-      // reference so exp2 gives 0, not NaN
-      const float mref = mnew == -INFINITY ? 0.f : mnew;
-      const float alpha = __builtin_amdgcn_exp2f(mrow[mb] - mref);
-      float ls = 0.f;
+      const float mxs = mx * c2;
+      const bool need = mxs > mrow[mb] + kTau;
+      if (__ballot(need) != 0) {
+        // a row whose max moved past the threshold takes the new max as its
+        // reference; alpha = 0 from the initial -inf (O and l are still 0)
+        const float mnew = need ? mxs : mrow[mb];
+        const float alpha = need ? __builtin_amdgcn_exp2f(mrow[mb] - mnew) : 1.f;
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) oacc[nb][mb] *= alpha;
+        lrow[mb] *= alpha;
+        mrow[mb] = mnew;
+        nmref[mb] = mnew == -INFINITY ? 0.f : -mnew;
+      }
       uint32_t packed[8];
 #pragma unroll
       for (int e = 0; e < 16; e += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(v[e] - mref);
-        const float p1 = __builtin_amdgcn_exp2f(v[e + 1] - mref);
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(v[e], c2, nmref[mb]));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(v[e + 1], c2, nmref[mb]));
         const uint32_t u = TT::pack2(p0, p1);
-        ls += TT::lo(u) + TT::hi(u);
+        lrow[mb] = TT::dot2(u, TT::kOne2, lrow[mb]);
         packed[e / 2] = u;
       }
-      lrow[mb] = lrow[mb] * alpha + ls;
-      mrow[mb] = mnew;
-      // packed[n*2 + i/2] holds keys n*16 + 4g + i, i in pairs
       pb[0][mb] = u32x4{packed[0], packed[1], packed[2], packed[3]};
       pb[1][mb] = u32x4{packed[4], packed[5], packed[6], packed[7]};
-      if (__ballot(alpha != 1.f) != 0) {
-#pragma unroll
-        for (int nb = 0; nb < 8; ++nb) oacc[nb][mb] *= alpha;
-      }
     }
+  };
+  auto pv = [&](int vbuf, const u32x4 (&pb)[2][MB]) {
     // O^T += V^T . P^T ; A = V^T[d = nb*16 + r][keys kc*32 + {4g..4g+3, 16+4g..16+4g+3}]
     // transposing reads: lane r of group g addresses key (.. + 4g + r/4),
     // dims nb*16 + 4*(r%4) .. +3, and receives dim nb*16 + r of keys +0..3
-    const uint16_t* vlane = vt + (g * 4 + (r >> 2)) * kRow + 4 * (r & 3);
+    const uint16_t* vlane = s_v[vbuf] + (g * 4 + (r >> 2)) * kRow + 4 * (r & 3);
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) {
 #pragma unroll
@@ -292,20 +358,130 @@ __global__ __launch_bounds__(128 * G) void prefill_kernel(PrefillArgs a) {
         for (int mb = 0; mb < MB; ++mb) oacc[nb][mb] = Mfma<TT>::mma(va, pb[kc][mb], oacc[nb][mb]);
       }
     }
-    // buf ^ 1 was last read in the previous step, which every wave finished
-    // before that step's barrier
-    if (step + 1 < nsteps) stash(buf ^ 1);
+  };
+
+  // Two waves share each SIMD (waves w and w + 4). Group A (waves 0-3) runs
+  // a step as QK -> softmax -> PV; group B (waves 4-7) runs the PV of the
+  // previous step first, then QK -> softmax, so that one wave's softmax (VALU)
+  // runs while the other's MFMAs do. K tiles use two LDS buffers; V tiles
+  // three, because group B still reads step j - 1's V in step j.
+  // Register ring slot D holds this step's tile (already in LDS); it is
+  // refilled with step + kDepth, and slot D + 1 (the next step's tile) is
+  // copied into LDS at the end of the step.
+  const bool late = wave >= kWaves / 2;
+  u32x4 pb[2][MB];
+  bool pending = false;   // group B: pb holds the P of a step whose PV is due
+  auto step_body = [&](int step, auto slot) {
+    constexpr int D = decltype(slot)::value;
+    constexpr int DN = (D + 1) % kDepth;
+    const int rel = step - st0;
+    fetch(step + kDepth, kst[D], vst[D]);   // past st1: clamped, never used
+    const bool active = step * kKT <= wpos0 + kWaveRows - 1;   // some row sees a key here
+    if (!late) {
+      if (active) {
+        qk(rel & 1);
+        softmax(step, pb);
+        pv(rel % 3, pb);
+      }
+    } else {
+      if (pending) pv((rel + 2) % 3, pb);
+      pending = active;
+      if (active) {
+        qk(rel & 1);
+        softmax(step, pb);
+      }
+    }
+    // K buffer (rel + 1) & 1 and V buffer (rel + 1) % 3 were last read in
+    // step - 1 (group B's PV of step - 2 included), which every wave finished
+    // before that step's barrier. Written even after the last step (nobody
+    // reads it then): an unconditional copy keeps the compiler's load
+    // accounting exact on every path.
+    stash(step + 1, (rel + 1) & 1, (rel + 1) % 3, kst[DN], vst[DN]);
     __syncthreads();
+  };
+  // full rounds of the ring in the loop; the 0-2 remaining steps after it, so
+  // that every path back to the loop head has run all three slots
+  static_assert(kDepth == 3, "the unrolled ring below has three slots");
+  int step = st0;
+  for (; step + kDepth <= st1; step += kDepth) {
+    step_body(step, std::integral_constant<int, 0>{});
+    step_body(step + 1, std::integral_constant<int, 1>{});
+    step_body(step + 2, std::integral_constant<int, 2>{});
+  }
+  if (step < st1) step_body(step, std::integral_constant<int, 0>{});
+  if (step + 1 < st1) step_body(step + 1, std::integral_constant<int, 1>{});
+  if (late && pending) pv((st1 - 1 - st0) % 3, pb);
+
+  // row sums over the 4 lanes of a row
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    lrow[mb] += shfl_xor(lrow[mb], 16);
+    lrow[mb] += shfl_xor(lrow[mb], 32);
+  }
+
+  if (nsp > 1) {
+    // publish this split's partial (register order: every store is 512
+    // contiguous bytes), then the last split of the tile to arrive merges
+    const int H = a.num_kv_heads * a.group;
+    const int64_t rec = (((int64_t)s * a.subtiles + wsub) * H + h) * a.splits_max;
+    {
+      float* po = a.part_o + (rec + j) * kRecO + lane * 2;
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          const int idx = nb * MB + mb;
+          npd::st_coherent2(po + (idx * 2) * 128, oacc[nb][mb][0], oacc[nb][mb][1]);
+          npd::st_coherent2(po + (idx * 2 + 1) * 128, oacc[nb][mb][2], oacc[nb][mb][3]);
+        }
+      float* pm = a.part_ml + (rec + j) * kRecML + lane * 2;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) npd::st_coherent2(pm + mb * 128, mrow[mb], lrow[mb]);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);   // every store of this wave has completed
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    const int64_t cidx = (((int64_t)s * a.tiles_max + t) * a.num_kv_heads + kh) * a.hgroups + hg;
+    if (tid == 0)
+      s_ticket = __hip_atomic_fetch_add(a.counters + cidx, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_ticket != nsp - 1) return;
+    for (int jj = 0; jj < nsp; ++jj) {
+      if (jj == j) continue;
+      const float* pm = a.part_ml + (rec + jj) * kRecML + lane * 2;
+      float wa[MB], wb[MB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        float mp, lp;
+        npd::ld_coherent2(pm + mb * 128, mp, lp);
+        const float mm = fmaxf(mrow[mb], mp);
+        wa[mb] = mrow[mb] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mrow[mb] - mm);
+        wb[mb] = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - mm);
+        lrow[mb] = lrow[mb] * wa[mb] + lp * wb[mb];
+        mrow[mb] = mm;
+      }
+      const float* po = a.part_o + (rec + jj) * kRecO + lane * 2;
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          const int idx = nb * MB + mb;
+          float x0, x1, x2, x3;
+          npd::ld_coherent2(po + (idx * 2) * 128, x0, x1);
+          npd::ld_coherent2(po + (idx * 2 + 1) * 128, x2, x3);
+          oacc[nb][mb] = oacc[nb][mb] * wa[mb] + f32x4{x0, x1, x2, x3} * wb[mb];
+        }
+    }
+    if (tid == 0) __hip_atomic_store(a.counters + cidx, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
   // normalise and store: lane writes d = nb*16 + 4g .. +3 of query row mb*16 + r
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
-    float l = lrow[mb];
-    l += shfl_xor(l, 16);
-    l += shfl_xor(l, 32);
-    const int row = t * kQT + wrow0 + mb * 16 + r;
+    const int row = wrow0 + mb * 16 + r;
     if (row >= qlen) continue;
+    const float l = lrow[mb];
     const float inv = (l > 0.f && wpos0 + mb * 16 + r >= 0) ? 1.f / l : 0.f;
     uint16_t* op = a.out + (int64_t)(q0 + row) * a.out_stride_token + (int64_t)h * a.out_stride_head;
 #pragma unroll
@@ -320,23 +496,52 @@ __global__ __launch_bounds__(128 * G) void prefill_kernel(PrefillArgs a) {
 }
 
 template <class TT>
-int launch(int g, const PrefillArgs& a, int64_t grid, hipStream_t st) {
-  switch (g) {
-    case 1: hipLaunchKernelGGL((prefill_kernel<TT, 1>), dim3((unsigned)grid), dim3(128), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((prefill_kernel<TT, 2>), dim3((unsigned)grid), dim3(256), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((prefill_kernel<TT, 4>), dim3((unsigned)grid), dim3(512), 0, st, a); break;
-    case 6: hipLaunchKernelGGL((prefill_kernel<TT, 6>), dim3((unsigned)grid), dim3(768), 0, st, a); break;
-    case 8: hipLaunchKernelGGL((prefill_kernel<TT, 8>), dim3((unsigned)grid), dim3(1024), 0, st, a); break;
-    default: return npd::fail(NPD_E_INVALID, "npd_paged_prefill_attention: group size %d", g);
+int launch(int hw, const PrefillArgs& a, int64_t grid, hipStream_t st) {
+  switch (hw) {
+    case 1: hipLaunchKernelGGL((prefill_kernel<TT, 1>), dim3((unsigned)grid), dim3(kThreads), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((prefill_kernel<TT, 2>), dim3((unsigned)grid), dim3(kThreads), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((prefill_kernel<TT, 4>), dim3((unsigned)grid), dim3(kThreads), 0, st, a); break;
+    default: return npd::fail(NPD_E_INVALID, "npd_paged_prefill_attention: heads per workgroup %d", hw);
   }
   return npd::check_launch("npd_paged_prefill_attention");
 }
 
+// Workspace: [counters | O partials | (m, l) partials]. Sized for the most
+// records any head group / row tiling of these shapes can address: a sequence
+// has tiles_max * (4 / HW) * 2 <= ceil(max_q_len / 32) + 7 subtiles of 32 rows.
+struct Layout {
+  int splits;
+  int64_t o_off, ml_off, total;
+};
+
+Layout prefill_layout(int64_t num_seqs, int64_t num_heads, int64_t max_q_len, int64_t max_context_len) {
+  Layout L{1, 0, 0, 0};
+  if (max_context_len > 0) {
+    const int64_t steps = (max_context_len + kKT - 1) / kKT;
+    const int64_t sp = (steps + kSplitSteps - 1) / kSplitSteps;
+    L.splits = (int)(sp < 1 ? 1 : (sp > kMaxSplits ? kMaxSplits : sp));
+  }
+  if (L.splits == 1 || num_seqs <= 0 || num_heads <= 0 || max_q_len <= 0) {
+    L.splits = 1;
+    return L;
+  }
+  const int64_t t32 = (max_q_len + kWaveRows - 1) / kWaveRows + 7;
+  const int64_t units = num_seqs * t32 * num_heads;
+  const int64_t nrec = units * L.splits;
+  L.o_off = (units * 4 + 255) / 256 * 256;
+  L.ml_off = L.o_off + nrec * kRecO * 4;
+  L.total = L.ml_off + nrec * kRecML * 4;
+  return L;
+}
+
 }  // namespace
 
-extern "C" int64_t npd_paged_prefill_workspace_size(int64_t, int64_t, int64_t, int64_t, int64_t,
-                                                    int64_t) {
-  return 0;
+extern "C" int64_t npd_paged_prefill_workspace_size(int64_t num_seqs, int64_t total_q,
+                                                    int64_t num_heads, int64_t head_dim,
+                                                    int64_t max_q_len, int64_t max_context_len) {
+  (void)total_q;
+  (void)head_dim;
+  return prefill_layout(num_seqs, num_heads, max_q_len, max_context_len).total;
 }
 
 extern "C" int npd_paged_prefill_attention(
@@ -348,9 +553,6 @@ extern "C" int npd_paged_prefill_attention(
     int64_t out_stride_token, int64_t out_stride_head, void* workspace, int64_t workspace_bytes,
     int32_t dtype, void* stream) {
   using namespace npd;
-  (void)workspace;
-  (void)workspace_bytes;
-  (void)max_context_len;
   const char* name = "npd_paged_prefill_attention";
   if (dtype != NPD_DTYPE_F16 && dtype != NPD_DTYPE_BF16)
     return fail(NPD_E_DTYPE, "%s: unsupported dtype code %d (fp16/bf16 only)", name, dtype);
@@ -364,23 +566,36 @@ extern "C" int npd_paged_prefill_attention(
     return fail(NPD_E_INVALID, "%s: num_heads %lld is not a multiple of num_kv_heads %lld", name,
                 (long long)num_heads, (long long)num_kv_heads);
   const int64_t g = num_heads / num_kv_heads;
-  if (g != 1 && g != 2 && g != 4 && g != 6 && g != 8)
-    return fail(NPD_E_INVALID, "%s: query heads per kv head %lld not in {1, 2, 4, 6, 8}", name,
-                (long long)g);
+  const int hw = (g % 4 == 0) ? 4 : (g % 2 == 0 ? 2 : 1);   // gcd(g, 4)
   if (num_blocks * block_size * num_kv_heads > INT32_MAX || max_blocks_per_seq * block_size > INT32_MAX)
     return fail(NPD_E_INVALID, "%s: pool exceeds int32 row indexing", name);
+  if (max_blocks_per_seq > kMaxBlocksLds)
+    return fail(NPD_E_INVALID, "%s: block tables wider than %d blocks are not supported", name,
+                kMaxBlocksLds);
   if (q_stride_token % 8 || q_stride_head % 8 || out_stride_token % 4 || out_stride_head % 4 ||
       q_stride_token < 0 || q_stride_head < 0 || out_stride_token < 0 || out_stride_head < 0)
     return fail(NPD_E_ALIGN, "%s: query strides must be multiples of 8 elements, out strides of 4",
                 name);
+  if (!(scale > 0.f) || scale == INFINITY)   // the row maxima are taken before scaling
+    return fail(NPD_E_INVALID, "%s: scale must be positive and finite", name);
   if (num_seqs == 0 || total_q == 0 || max_q_len == 0) return NPD_OK;
   if (!out || !query || !key_cache || !value_cache || !block_tables || !cu_seqlens_q || !context_lens)
     return fail(NPD_E_INVALID, "%s: null pointer", name);
   if (!aligned16(query) || !aligned16(key_cache) || !aligned16(value_cache) ||
       (reinterpret_cast<uintptr_t>(out) & 7u) != 0)
     return fail(NPD_E_ALIGN, "%s: query/cache pointers must be 16-byte aligned, out 8-byte", name);
-  const int64_t tiles = (max_q_len + kQT - 1) / kQT;
-  const int64_t grid = num_seqs * num_kv_heads * tiles;
+  const Layout L = prefill_layout(num_seqs, num_heads, max_q_len, max_context_len);
+  if (L.total > 0) {
+    if (!workspace || workspace_bytes < L.total)
+      return fail(NPD_E_WORKSPACE, "%s: workspace of %lld bytes needed, %lld given", name,
+                  (long long)L.total, (long long)workspace_bytes);
+    if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+      return fail(NPD_E_ALIGN, "%s: workspace must be 256-byte aligned", name);
+  }
+  const int rt = kPairs / hw;
+  const int64_t tiles = (max_q_len + 64LL * rt - 1) / (64LL * rt);
+  const int64_t hgroups = g / hw;
+  const int64_t grid = tiles * num_seqs * num_kv_heads * hgroups * L.splits;
   if (grid > INT32_MAX) return fail(NPD_E_INVALID, "%s: too many tiles", name);
 
   PrefillArgs a;
@@ -391,18 +606,27 @@ extern "C" int npd_paged_prefill_attention(
   a.block_tables = block_tables;
   a.cu_seqlens_q = cu_seqlens_q;
   a.context_lens = context_lens;
+  char* ws = static_cast<char*>(workspace);
+  a.counters = L.total > 0 ? reinterpret_cast<int*>(ws) : nullptr;
+  a.part_o = L.total > 0 ? reinterpret_cast<float*>(ws + L.o_off) : nullptr;
+  a.part_ml = L.total > 0 ? reinterpret_cast<float*>(ws + L.ml_off) : nullptr;
   a.num_seqs = (int)num_seqs;
   a.num_kv_heads = (int)num_kv_heads;
+  a.group = (int)g;
+  a.hgroups = (int)hgroups;
   a.block_size = (int)block_size;
+  a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctzll((unsigned long long)block_size) : -1;
   a.num_blocks = (int)num_blocks;
   a.max_bps = (int)max_blocks_per_seq;
   a.tiles_max = (int)tiles;
+  a.subtiles = (int)(tiles * rt * 2);
+  a.splits_max = L.splits;
   a.scale_log2 = scale * kLog2e;
   a.q_stride_token = q_stride_token;
   a.q_stride_head = q_stride_head;
   a.out_stride_token = out_stride_token;
   a.out_stride_head = out_stride_head;
   hipStream_t st = as_stream(stream);
-  if (dtype == NPD_DTYPE_BF16) return launch<BF16>((int)g, a, grid, st);
-  return launch<F16>((int)g, a, grid, st);
+  if (dtype == NPD_DTYPE_BF16) return launch<BF16>(hw, a, grid, st);
+  return launch<F16>(hw, a, grid, st);
 }

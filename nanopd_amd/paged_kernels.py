@@ -29,7 +29,7 @@ from . import _lib
 __all__ = [
     "paged_kv_store", "paged_kv_store_slots", "paged_attention_forward",
     "paged_prefill_attention", "copy_blocks", "pack_metadata", "BatchMetadata",
-    "attention_workspace_bytes",
+    "attention_workspace_bytes", "prefill_workspace_bytes",
 ]
 
 _DTYPES = {torch.float16: _lib.NPD_DTYPE_F16, torch.bfloat16: _lib.NPD_DTYPE_BF16}
@@ -171,8 +171,10 @@ def paged_kv_store_slots(k_cache: torch.Tensor, v_cache: torch.Tensor, k_src: to
 _workspaces: dict = {}
 
 
-def _decode_workspace(dev: torch.device, stream: int, need: int) -> torch.Tensor:
-    key = (dev.index, stream)
+def _decode_workspace(dev: torch.device, stream: int, need: int, kind: str = "decode") -> torch.Tensor:
+    """A zero-filled workspace cached per (device, stream, op): the kernels
+    leave their merge counters at zero, so it is cleared only when allocated."""
+    key = (dev.index, stream, kind)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < need:
         ws = torch.zeros(need, dtype=torch.uint8, device=dev)
@@ -244,11 +246,18 @@ def paged_attention_forward(out: torch.Tensor, query: torch.Tensor, key_cache: t
 # Chunked prefill attention
 # ---------------------------------------------------------------------------
 
+def prefill_workspace_bytes(num_seqs: int, total_q: int, num_heads: int, head_dim: int,
+                            max_q_len: int, max_context_len: int) -> int:
+    return int(_lib.load().npd_paged_prefill_workspace_size(
+        num_seqs, total_q, num_heads, head_dim, max_q_len, max_context_len))
+
+
 def paged_prefill_attention(out: torch.Tensor, query: torch.Tensor, key_cache: torch.Tensor,
                             value_cache: torch.Tensor, block_tables: torch.Tensor,
                             cu_seqlens_q: torch.Tensor, context_lens: torch.Tensor, scale: float,
                             block_size: int, max_num_blocks_per_seq: int, max_q_len: int,
-                            max_context_len: int | None = None) -> None:
+                            max_context_len: int | None = None,
+                            workspace: torch.Tensor | None = None) -> None:
     """Causal varlen attention over the paged prefix plus the new chunk.
 
     Replaces the SDPA prefill of paged_forward (nanoPD/engine/model_runner.py:
@@ -256,7 +265,11 @@ def paged_prefill_attention(out: torch.Tensor, query: torch.Tensor, key_cache: t
     num_heads, head_dim]; sequence s owns rows cu_seqlens_q[s]:cu_seqlens_q[s+1];
     its chunk K/V must already be in the pool; context_lens[s] = prefix + chunk.
     Row i of s sits at position context_lens[s] - q_len + i and sees keys 0..pos.
-    max_q_len / max_context_len are host-side upper bounds (grid sizing).
+    max_q_len / max_context_len are host-side upper bounds (grid sizing; the
+    context bound, default max_num_blocks_per_seq * block_size, sets how long
+    key ranges are split). An optional uint8 ``workspace`` of at least
+    :func:`prefill_workspace_bytes` bytes, zero-filled before its first use,
+    replaces the cached per-stream one; calls sharing one run in stream order.
     """
     _check(isinstance(query, torch.Tensor) and query.is_cuda, "query is must be on CUDA")
     _check(query.dim() == 3, "query must be [total_q, num_heads, head_size]")
@@ -286,14 +299,20 @@ def paged_prefill_attention(out: torch.Tensor, query: torch.Tensor, key_cache: t
     if ns == 0 or tq == 0:
         return
     mctx = int(max_context_len) if max_context_len is not None else mb * bs
-    need = int(_lib.load().npd_paged_prefill_workspace_size(ns, tq, h, d, int(max_q_len), mctx))
-    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev) if need > 0 else None
+    need = prefill_workspace_bytes(ns, tq, h, d, int(max_q_len), mctx)
+    stream = _stream(dev)
+    ws_ptr = 0
+    if need > 0:
+        if workspace is None:
+            workspace = _decode_workspace(dev, stream, need, "prefill")
+        _check(workspace.numel() * workspace.element_size() >= need,
+               f"workspace of {need} bytes needed")
+        ws_ptr = workspace.data_ptr()
     _lib.call("npd_paged_prefill_attention", out.data_ptr(), query.data_ptr(),
               key_cache.data_ptr(), value_cache.data_ptr(), block_tables.data_ptr(),
               cu_seqlens_q.data_ptr(), context_lens.data_ptr(), ns, tq, h, kvh, d, num_blocks, bs,
               mb, int(max_q_len), mctx, float(scale), query.stride(0), query.stride(1),
-              out.stride(0), out.stride(1), ws.data_ptr() if ws is not None else 0, need, code,
-              _stream(dev))
+              out.stride(0), out.stride(1), ws_ptr, need, code, stream)
 
 
 # ---------------------------------------------------------------------------

@@ -108,6 +108,23 @@ def test_workspace_size():
     assert n == 2 * 8 * 4 * (64 + 2) * 4
 
 
+def test_prefill_workspace_size():
+    lib = _lib.load()
+    # key ranges up to 16 steps of 64 keys run whole: no workspace
+    assert lib.npd_paged_prefill_workspace_size(4, 2048, 32, 128, 512, 1024) == 0
+    assert lib.npd_paged_prefill_workspace_size(4, 2048, 32, 128, 512, 0) == 0
+    # longer ranges are split (at most 8 ways): int32 counters per (sequence,
+    # row subtile of 32, head), padded to 256 bytes, then per (..., split) an O
+    # record of 32 rows x 128 fp32 and an (m, l) record of 32 rows x 2 x 4 lanes
+    def split(S, H, max_q, splits):
+        t32 = (max_q + 31) // 32 + 7
+        units = S * t32 * H
+        return (units * 4 + 255) // 256 * 256 + units * splits * (16384 + 1024)
+    assert lib.npd_paged_prefill_workspace_size(4, 2048, 32, 128, 512, 3584) == split(4, 32, 512, 4)
+    assert lib.npd_paged_prefill_workspace_size(1, 100, 32, 128, 100, 1025) == split(1, 32, 100, 2)
+    assert lib.npd_paged_prefill_workspace_size(2, 1024, 32, 128, 512, 32768) == split(2, 32, 512, 8)
+
+
 def test_python_mirror_raises_like_torch_check():
     q = torch.zeros(2, 4, 64, dtype=torch.float16)
     kc = torch.zeros(4, 4, 8, 64, dtype=torch.float16)
