@@ -40,15 +40,16 @@
 //   flight while the current one is multiplied. Keys past the visible range
 //   are written as zeros and masked, so no NaN from stale pool memory leaks in.
 //
-// Key splits: a query tile whose key range is longer than kSplitSteps steps is
-// cut into nsp <= splits_max near-equal ranges run by separate workgroups (the
-// tiles of a long prefix would otherwise run many times longer than the rest).
+// Key splits: a query tile whose key range is longer than ks_steps steps of 64
+// keys is cut at multiples of ks_steps into nsp <= splits_max ranges run by
+// separate workgroups (the tiles of a long prefix would otherwise run many
+// times longer than the rest). Cutting at the same keys for every tile lets the
+// tiles of a sequence share each K/V range through L2.
 // Each split publishes its unnormalised O, running max and row sum with
 // device-coherent stores, then takes a ticket from a per-tile counter; the last
 // of the nsp to arrive merges the others into its registers
 //   M = max_j m_j,  L = sum_j l_j 2^(m_j - M),  O = sum_j O_j 2^(m_j - M) / L
-// writes the output and resets the counter to 0. Workgroups are ordered last
-// query tile first, a tile's splits adjacent, so the longest work starts first.
+// writes the output and resets the counter to 0.
 #include <type_traits>
 
 #include "common.h"
@@ -94,6 +95,7 @@ struct PrefillArgs {
   float* part_ml;
   int num_seqs, num_kv_heads, group, hgroups, block_size, bs_shift, num_blocks, max_bps;
   int tiles_max, subtiles, splits_max;   // subtiles: 32-row subtiles per sequence
+  int ks_steps, num_groups;              // key steps per split; (split, seq, kv-head) groups
   float scale_log2;
   int64_t q_stride_token, q_stride_head, out_stride_token, out_stride_head;
 };
@@ -117,7 +119,22 @@ struct Mfma<npd::F16> {
   }
 };
 
-__device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+// Max / sum over the 4 lanes l, l^16, l^32, l^48 (the 4 key groups of a query
+// row), with the gfx950 row-swap permutes: v_permlane16_swap with both
+// operands x hands every lane {x, x of lane^16} in some order, and
+// v_permlane32_swap {x, x of lane^32}.
+__device__ __forceinline__ float row_max4(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float row_sum4(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 // ds_read_b64_tr_b16 on an LDS address given as a generic pointer to __shared__
@@ -140,16 +157,23 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   const int wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, r = lane & 15;
 
-  // unit = (tile, last first; sequence; kv-head x head group; split)
-  int b = blockIdx.x;
-  const int j = b % a.splits_max;
-  b /= a.splits_max;
-  const int nhg = a.num_kv_heads * a.hgroups;
-  const int khg = b % nhg;
-  b /= nhg;
-  const int s = b % a.num_seqs;
-  const int t = a.tiles_max - 1 - b / a.num_seqs;
-  const int kh = khg / a.hgroups, hg = khg - kh * a.hgroups;
+  // Unit = (split j, sequence, kv-head; tile t, head group). The units of one
+  // (j, s, kv-head) read the same K/V key range: they form a group that runs
+  // on one XCD at the same time (workgroups go to XCDs round-robin by
+  // blockIdx, so the group's blockIdx values are 8 apart and consecutive in
+  // that XCD's order), so K/V tiles come from that XCD's L2 after the first
+  // read. Within a group the last tile (the most keys) comes first.
+  const int gunits = a.tiles_max * a.hgroups;
+  const int xcd = blockIdx.x & 7, p = blockIdx.x >> 3;
+  const int gi = (p / gunits) * 8 + xcd;
+  if (gi >= a.num_groups) return;
+  const int u = p - (p / gunits) * gunits;
+  const int t = a.tiles_max - 1 - u / a.hgroups;
+  const int hg = u - (u / a.hgroups) * a.hgroups;
+  const int kh = gi % a.num_kv_heads;
+  const int js = gi / a.num_kv_heads;
+  const int s = js % a.num_seqs;
+  const int j = js / a.num_seqs;
 
   const int q0 = a.cu_seqlens_q[s];
   const int qlen = a.cu_seqlens_q[s + 1] - q0;
@@ -163,11 +187,13 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   int nkeys = pos0 + rows;                             // keys 0 .. last row's position
   nkeys = nkeys < 0 ? 0 : nkeys;
   const int nsteps = (nkeys + kKT - 1) / kKT;
-  int nsp = (nsteps + kSplitSteps - 1) / kSplitSteps;
+  // split j covers steps [j*ks, (j+1)*ks) -- the same keys for every tile of
+  // the sequence -- the last split runs to the end of the tile's range
+  int nsp = (nsteps + a.ks_steps - 1) / a.ks_steps;
   nsp = nsp < 1 ? 1 : (nsp > a.splits_max ? a.splits_max : nsp);
   if (j >= nsp) return;
-  const int st0 = (int)((int64_t)nsteps * j / nsp);
-  const int st1 = (int)((int64_t)nsteps * (j + 1) / nsp);
+  const int st0 = j * a.ks_steps;
+  const int st1 = j == nsp - 1 ? nsteps : st0 + a.ks_steps;
 
   // wave -> (head of the group, row tile, half of the row tile)
   const int pair = wave >> 1, half = wave & 1;
@@ -291,49 +317,63 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   };
   auto softmax = [&](int step, u32x4 (&pb)[2][MB]) {
     const int key0 = step * kKT;
-    // causal mask, lazy-max softmax; pb[kc][mb] is the B operand of keys
-    // kc*32 .. +32: slots e<4 -> key kc*32 + 4g + e, e>=4 -> kc*32 + 16 + 4g + e - 4
+    // causal mask, lazy-max softmax
     const bool diag = key0 + kKT - 1 > wpos0;   // some key here is after some row
+    float v[MB][16];
+    float mxs[MB];
+    bool need = false;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
-      float v[16];
 #pragma unroll
       for (int n = 0; n < 4; ++n)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[n * 4 + i] = sacc[n][mb][i];
-      if (diag) {
+        for (int i = 0; i < 4; ++i) v[mb][n * 4 + i] = sacc[n][mb][i];
+    }
+    if (diag) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
         // key n*16 + 4g + i of this step is visible to the row iff n*16 + i <= lim
         const int lim = wpos0 + mb * 16 + r - key0 - 4 * g;
 #pragma unroll
         for (int n = 0; n < 4; ++n)
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if (n * 16 + i > lim) v[n * 4 + i] = -INFINITY;
+            if (n * 16 + i > lim) v[mb][n * 4 + i] = -INFINITY;
       }
-      float mx = fmaxf(v[0], fmaxf(v[1], v[2]));
+    }
 #pragma unroll
-      for (int e = 3; e < 15; e += 2) mx = fmaxf(mx, fmaxf(v[e], v[e + 1]));
-      mx = fmaxf(mx, v[15]);
-      mx = fmaxf(mx, shfl_xor(mx, 16));
-      mx = fmaxf(mx, shfl_xor(mx, 32));
-      const float mxs = mx * c2;
-      const bool need = mxs > mrow[mb] + kTau;
-      if (__ballot(need) != 0) {
-        // a row whose max moved past the threshold takes the new max as its
-        // reference; alpha = 0 from the initial -inf (O and l are still 0)
-        const float mnew = need ? mxs : mrow[mb];
-        const float alpha = need ? __builtin_amdgcn_exp2f(mrow[mb] - mnew) : 1.f;
+    for (int mb = 0; mb < MB; ++mb) {
+      float mx = fmaxf(v[mb][0], fmaxf(v[mb][1], v[mb][2]));
+#pragma unroll
+      for (int e = 3; e < 15; e += 2) mx = fmaxf(mx, fmaxf(v[mb][e], v[mb][e + 1]));
+      mx = row_max4(fmaxf(mx, v[mb][15]));
+      mxs[mb] = mx * c2;
+      need = need || (mxs[mb] > mrow[mb] + kTau);
+    }
+    if (__ballot(need) != 0) {
+      // a row whose max moved past the threshold takes the new max as its
+      // reference; alpha = 0 from the initial -inf (O and l are still 0)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const bool nd = mxs[mb] > mrow[mb] + kTau;
+        const float mnew = nd ? mxs[mb] : mrow[mb];
+        const float alpha = nd ? __builtin_amdgcn_exp2f(mrow[mb] - mnew) : 1.f;
 #pragma unroll
         for (int nb = 0; nb < 8; ++nb) oacc[nb][mb] *= alpha;
         lrow[mb] *= alpha;
         mrow[mb] = mnew;
         nmref[mb] = mnew == -INFINITY ? 0.f : -mnew;
       }
+    }
+    // P = 2^(s*c - m), packed; pb[kc][mb] is the B operand of keys kc*32 .. +32:
+    // slots e<4 -> key kc*32 + 4g + e, e>=4 -> kc*32 + 16 + 4g + e - 4
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
       uint32_t packed[8];
 #pragma unroll
       for (int e = 0; e < 16; e += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(v[e], c2, nmref[mb]));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(v[e + 1], c2, nmref[mb]));
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(v[mb][e], c2, nmref[mb]));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(v[mb][e + 1], c2, nmref[mb]));
         const uint32_t u = TT::pack2(p0, p1);
         lrow[mb] = TT::dot2(u, TT::kOne2, lrow[mb]);
         packed[e / 2] = u;
@@ -376,7 +416,8 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     constexpr int DN = (D + 1) % kDepth;
     const int rel = step - st0;
     fetch(step + kDepth, kst[D], vst[D]);   // past st1: clamped, never used
-    const bool active = step * kKT <= wpos0 + kWaveRows - 1;   // some row sees a key here
+    // some row of the wave sees a key here (always so with one row tile)
+    const bool active = RT == 1 || step * kKT <= wpos0 + kWaveRows - 1;
     if (!late) {
       if (active) {
         qk(rel & 1);
@@ -414,10 +455,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 
   // row sums over the 4 lanes of a row
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    lrow[mb] += shfl_xor(lrow[mb], 16);
-    lrow[mb] += shfl_xor(lrow[mb], 32);
-  }
+  for (int mb = 0; mb < MB; ++mb) lrow[mb] = row_sum4(lrow[mb]);
 
   if (nsp > 1) {
     // publish this split's partial (register order: every store is 512
@@ -510,18 +548,21 @@ int launch(int hw, const PrefillArgs& a, int64_t grid, hipStream_t st) {
 // records any head group / row tiling of these shapes can address: a sequence
 // has tiles_max * (4 / HW) * 2 <= ceil(max_q_len / 32) + 7 subtiles of 32 rows.
 struct Layout {
-  int splits;
+  int splits, ks_steps;
   int64_t o_off, ml_off, total;
 };
 
 Layout prefill_layout(int64_t num_seqs, int64_t num_heads, int64_t max_q_len, int64_t max_context_len) {
-  Layout L{1, 0, 0, 0};
+  Layout L{1, kSplitSteps, 0, 0, 0};
   if (max_context_len > 0) {
+    // splits of kSplitSteps steps, longer ones when that would exceed kMaxSplits
     const int64_t steps = (max_context_len + kKT - 1) / kKT;
-    const int64_t sp = (steps + kSplitSteps - 1) / kSplitSteps;
-    L.splits = (int)(sp < 1 ? 1 : (sp > kMaxSplits ? kMaxSplits : sp));
+    int64_t ks = (steps + kMaxSplits - 1) / kMaxSplits;
+    ks = ks < kSplitSteps ? kSplitSteps : ks;
+    L.ks_steps = (int)ks;
+    L.splits = (int)((steps + ks - 1) / ks);
   }
-  if (L.splits == 1 || num_seqs <= 0 || num_heads <= 0 || max_q_len <= 0) {
+  if (L.splits <= 1 || num_seqs <= 0 || num_heads <= 0 || max_q_len <= 0) {
     L.splits = 1;
     return L;
   }
@@ -595,7 +636,8 @@ extern "C" int npd_paged_prefill_attention(
   const int rt = kPairs / hw;
   const int64_t tiles = (max_q_len + 64LL * rt - 1) / (64LL * rt);
   const int64_t hgroups = g / hw;
-  const int64_t grid = tiles * num_seqs * num_kv_heads * hgroups * L.splits;
+  const int64_t groups = (int64_t)L.splits * num_seqs * num_kv_heads;
+  const int64_t grid = (groups + 7) / 8 * 8 * tiles * hgroups;
   if (grid > INT32_MAX) return fail(NPD_E_INVALID, "%s: too many tiles", name);
 
   PrefillArgs a;
@@ -621,6 +663,8 @@ extern "C" int npd_paged_prefill_attention(
   a.tiles_max = (int)tiles;
   a.subtiles = (int)(tiles * rt * 2);
   a.splits_max = L.splits;
+  a.ks_steps = L.ks_steps;
+  a.num_groups = (int)groups;
   a.scale_log2 = scale * kLog2e;
   a.q_stride_token = q_stride_token;
   a.q_stride_head = q_stride_head;
