@@ -10,35 +10,39 @@
 // them before attending, model_runner.py:146). For an empty prefix both agree.
 //
 // MI355X design (gfx950, v_mfma_f32_16x16x32_{bf16,f16}, wave64):
-//   workgroup = 4 waves = one (sequence, kv-head, head group, query tile, key
-//   split). A wave owns one query head and 64 query rows, so the 64-key K/V
-//   tile that the workgroup gathers from the pool into LDS is read from LDS
-//   once per 64 rows (GQA heads and, for small groups, neighbouring row tiles
-//   share it). HW = gcd(G, 4) heads per workgroup, 4 / HW row tiles of 64.
-//   One wave per SIMD (up to 512 VGPRs, accumulators in AGPRs).
+//   workgroup = 8 waves = one (sequence, kv-head, head group, 64-row query
+//   tile, key split); wave w owns one query head and 32 query rows. Two waves
+//   per SIMD, 256 VGPRs each (MFMA operands stay in VGPRs). HW = gcd(G, 4)
+//   heads per workgroup, 4 / HW row tiles of 64 (G = 4: 4 heads x 64 rows).
+//   The 64-key K/V tile the workgroup gathers from the pool into LDS is read
+//   by all 8 waves (GQA and row reuse).
 //   per step of 64 keys, each wave:
 //     S^T = K . Q^T   -- A = K rows from LDS, B = the wave's query rows, kept
 //                        in registers for the whole key loop;
 //     softmax          -- lane l holds 16 keys of query (mb*16 + l%16) of each
-//                        16-row block; the rest are in lanes l^16, l^32.
-//                        Scale and max subtraction are one FMA before exp2;
-//                        the row sum is a v_dot2 of the rounded P pair with
-//                        (1, 1). The running max is only moved (and O
-//                        rescaled) when a row's new max exceeds it by more than
-//                        2^kTau: P entries then stay <= 2^kTau, exact in fp32
-//                        accumulation, and the rescale is rare after step 1;
+//                        16-row block; the rest are in lanes l^16, l^32 (row
+//                        max / sum with v_permlane16/32_swap). Scale and max
+//                        subtraction are one FMA before exp2; the row sum is a
+//                        v_dot2 of the rounded P pair with (1, 1). The running
+//                        max is only moved (and O rescaled) when a row's new
+//                        max exceeds it by more than 2^kTau: P entries then
+//                        stay <= 2^kTau, exact in fp32 accumulation, and the
+//                        rescale is rare after the first step;
 //     O^T += V^T . P^T -- P^T is the S^T accumulator, already in B-operand
 //                        layout (packed with v_cvt_pk_bf16_f32); V stays
 //                        row-major in LDS like K, and the V^T A operand is two
 //                        ds_read_b64_tr_b16 (gfx950 transposing LDS read: in a
 //                        group of 16 lanes, lane j receives element j%4 of the
 //                        8-byte chunks addressed by lanes 4e + j/4, e = 0..3).
+//   The two waves of a SIMD are phase-shifted (one runs PV of the previous
+//   step before QK, the other after softmax), so one's softmax VALU work can
+//   run under the other's MFMAs. K/V loads run three steps ahead through a
+//   register ring, are copied into LDS (2 K, 3 V buffers) one step ahead, and
+//   keys past the visible range are clamped to the last visible key (a real,
+//   finite context row) and masked.
 //   Operand layouts of v_mfma_f32_16x16x32 (checked on the hardware):
 //     A[m = lane%16][k = 8*(lane/16) + e], B[k = 8*(lane/16) + e][n = lane%16],
 //     D[m = 4*(lane/16) + i][n = lane%16].
-//   K/V tiles are double-buffered in LDS: the next tile's global loads are in
-//   flight while the current one is multiplied. Keys past the visible range
-//   are written as zeros and masked, so no NaN from stale pool memory leaks in.
 //
 // Key splits: a query tile whose key range is longer than ks_steps steps of 64
 // keys is cut at multiples of ks_steps into nsp <= splits_max ranges run by
@@ -143,7 +147,9 @@ __device__ __forceinline__ u32x2 lds_read_tr(const uint16_t* p) {
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p)));
 }
 
-template <class TT, int HW>
+// kOff32: every K/V element of the pool lies within 4 GiB of the cache base,
+// so gather offsets are 32-bit
+template <class TT, int HW, bool kOff32>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   constexpr int RT = kPairs / HW;                      // row tiles of 64 per workgroup
   constexpr int TR = 64 * RT;                          // query rows per workgroup
@@ -250,9 +256,11 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   constexpr int kPer = kKT * kD / 8 / kThreads;        // 2
   u32x4 kst[kDepth][kPer], vst[kDepth][kPer];
   const int col = tid & 15;
-  // Every fetch issues the same loads (tokens clamped into the split's range,
-  // out-of-range ones zeroed when written to LDS), so the compiler's count of
-  // loads in flight stays exact and its waits cover only the slot being used.
+  // Every fetch issues the same loads, so the compiler's count of loads in
+  // flight stays exact and its waits cover only the slot being used: tokens
+  // past the split's range are clamped to its last key. Such keys only occur
+  // past the tile's last row (the causal mask removes them) and hold real
+  // context rows, so their V is finite and P = 0 cancels it.
   auto fetch = [&](int step, u32x4* ks, u32x4* vs) {
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
@@ -260,18 +268,24 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
       tok = tok < kend ? tok : kend - 1;
       const int lb = a.bs_shift >= 0 ? tok >> a.bs_shift : tok / bs;
       const int blk = s_blk[lb - blk0];
-      const int64_t idx = (((int64_t)blk * a.num_kv_heads + kh) * bs + (tok - lb * bs)) * 16 + col;
-      ks[e] = a.k_cache[idx];
-      vs[e] = a.v_cache[idx];
+      const int row = (blk * a.num_kv_heads + kh) * bs + (tok - lb * bs);   // < 2^31 (host check)
+      if (kOff32) {
+        const uint32_t off = (uint32_t)row * 256u + (uint32_t)col * 16u;
+        ks[e] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(a.k_cache) + off);
+        vs[e] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(a.v_cache) + off);
+      } else {
+        const int64_t idx = (int64_t)row * 16 + col;
+        ks[e] = a.k_cache[idx];
+        vs[e] = a.v_cache[idx];
+      }
     }
   };
-  auto stash = [&](int step, int kbuf, int vbuf, const u32x4* ks, const u32x4* vs) {
+  auto stash = [&](int kbuf, int vbuf, const u32x4* ks, const u32x4* vs) {
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
       const int kk = (tid >> 4) + 32 * e;
-      const bool ok = step * kKT + kk < nkeys;
-      *reinterpret_cast<u32x4*>(&s_k[kbuf][kk * kRow + col * 8]) = ok ? ks[e] : u32x4{0, 0, 0, 0};
-      *reinterpret_cast<u32x4*>(&s_v[vbuf][kk * kRow + col * 8]) = ok ? vs[e] : u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(&s_k[kbuf][kk * kRow + col * 8]) = ks[e];
+      *reinterpret_cast<u32x4*>(&s_v[vbuf][kk * kRow + col * 8]) = vs[e];
     }
   };
 
@@ -291,7 +305,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 
 #pragma unroll
   for (int d = 0; d < kDepth; ++d) fetch(st0 + d, kst[d], vst[d]);
-  stash(st0, 0, 0, kst[0], vst[0]);
+  stash(0, 0, kst[0], vst[0]);
   __syncthreads();
 
   // Step pieces. qk: S^T of step `step` from K buffer kbuf; softmax: P of
@@ -437,7 +451,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     // before that step's barrier. Written even after the last step (nobody
     // reads it then): an unconditional copy keeps the compiler's load
     // accounting exact on every path.
-    stash(step + 1, (rel + 1) & 1, (rel + 1) % 3, kst[DN], vst[DN]);
+    stash((rel + 1) & 1, (rel + 1) % 3, kst[DN], vst[DN]);
     __syncthreads();
   };
   // full rounds of the ring in the loop; the 0-2 remaining steps after it, so
@@ -533,12 +547,12 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   }
 }
 
-template <class TT>
+template <class TT, bool kOff32>
 int launch(int hw, const PrefillArgs& a, int64_t grid, hipStream_t st) {
   switch (hw) {
-    case 1: hipLaunchKernelGGL((prefill_kernel<TT, 1>), dim3((unsigned)grid), dim3(kThreads), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((prefill_kernel<TT, 2>), dim3((unsigned)grid), dim3(kThreads), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((prefill_kernel<TT, 4>), dim3((unsigned)grid), dim3(kThreads), 0, st, a); break;
+    case 1: hipLaunchKernelGGL((prefill_kernel<TT, 1, kOff32>), dim3((unsigned)grid), dim3(kThreads), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((prefill_kernel<TT, 2, kOff32>), dim3((unsigned)grid), dim3(kThreads), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((prefill_kernel<TT, 4, kOff32>), dim3((unsigned)grid), dim3(kThreads), 0, st, a); break;
     default: return npd::fail(NPD_E_INVALID, "npd_paged_prefill_attention: heads per workgroup %d", hw);
   }
   return npd::check_launch("npd_paged_prefill_attention");
@@ -671,6 +685,8 @@ extern "C" int npd_paged_prefill_attention(
   a.out_stride_token = out_stride_token;
   a.out_stride_head = out_stride_head;
   hipStream_t st = as_stream(stream);
-  if (dtype == NPD_DTYPE_BF16) return launch<BF16>(hw, a, grid, st);
-  return launch<F16>(hw, a, grid, st);
+  const bool off32 = num_blocks * num_kv_heads * block_size * head_dim * 2 <= (int64_t)UINT32_MAX;
+  if (dtype == NPD_DTYPE_BF16)
+    return off32 ? launch<BF16, true>(hw, a, grid, st) : launch<BF16, false>(hw, a, grid, st);
+  return off32 ? launch<F16, true>(hw, a, grid, st) : launch<F16, false>(hw, a, grid, st);
 }

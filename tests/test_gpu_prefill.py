@@ -155,3 +155,42 @@ def test_config3_store_then_prefill_and_decode(device):
     err = max_abs(out, want)
     print(f"cfg3 max-abs {err:.2e}")
     assert err <= ATOL[torch.bfloat16]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_key_splits_match_whole_ranges(device, dtype):
+    """Long prefixes are cut into key splits merged by the last split to
+    arrive; splitting off (max_context_len=0) runs every range whole. Both
+    agree with the oracle and with each other."""
+    args = make_case(device, [3000, 1100, 0, 5000], [200, 64, 130, 33], dtype=dtype, seed=21)
+    q, kc, vc, bt, cu, ctx, mb, mq = args
+    scale = 1 / math.sqrt(128)
+    assert pk.prefill_workspace_bytes(4, int(q.size(0)), 32, 128, mq, mb * 16) > 0
+    split = run(*args, scale)
+    whole = torch.full_like(q, float("nan"))
+    pk.paged_prefill_attention(whole, q, kc, vc, bt, cu, ctx, scale, 16, mb, mq, max_context_len=0)
+    torch.cuda.synchronize()
+    check(split, q, kc, vc, bt, cu, ctx, scale)
+    check(whole, q, kc, vc, bt, cu, ctx, scale)
+    assert max_abs(split, f32(whole).astype(np.float64)) <= ATOL[dtype]
+
+
+def test_workspace_reuse_and_explicit_workspace(device):
+    """The merge counters are left at zero: the same (explicit) workspace
+    serves consecutive calls of different shapes; a short one is refused."""
+    scale = 1 / math.sqrt(128)
+    a1 = make_case(device, [2500, 700], [100, 300], seed=31)
+    a2 = make_case(device, [4000], [64], seed=32)
+    need = max(pk.prefill_workspace_bytes(2, 400, 32, 128, 300, a1[6] * 16),
+               pk.prefill_workspace_bytes(1, 64, 32, 128, 64, a2[6] * 16))
+    ws = torch.zeros(need, dtype=torch.uint8, device=device)
+    for args in (a1, a2, a1):
+        q, kc, vc, bt, cu, ctx, mb, mq = args
+        out = torch.full_like(q, float("nan"))
+        pk.paged_prefill_attention(out, q, kc, vc, bt, cu, ctx, scale, 16, mb, mq, workspace=ws)
+        torch.cuda.synchronize()
+        check(out, q, kc, vc, bt, cu, ctx, scale)
+    q, kc, vc, bt, cu, ctx, mb, mq = a2
+    with pytest.raises(RuntimeError, match="workspace"):
+        pk.paged_prefill_attention(torch.empty_like(q), q, kc, vc, bt, cu, ctx, scale, 16, mb, mq,
+                                   workspace=ws[:64])
