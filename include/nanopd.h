@@ -88,8 +88,9 @@ int npd_paged_kv_store_slots(void* k_cache, void* v_cache,
                              int32_t dtype, void* stream);
 
 /*
- * Bytes of device workspace npd_paged_attention needs for these shapes (split-
- * context partials). 0 means no workspace is needed.
+ * Bytes of device workspace npd_paged_attention needs for these shapes (merge
+ * counter region, work list, split-context partials). 0 means no workspace is
+ * needed.
  */
 int64_t npd_paged_attention_workspace_size(int64_t num_seqs, int64_t num_heads,
                                            int64_t num_kv_heads, int64_t head_dim,
@@ -107,9 +108,11 @@ int64_t npd_paged_attention_workspace_size(int64_t num_seqs, int64_t num_heads,
  * Every output element is written: out need not be zeroed.
  * workspace: at least npd_paged_attention_workspace_size(...) bytes, 256-byte
  * aligned (may be NULL when that size is 0), zero-filled before its first
- * use: it holds split-context partials and, for head_dim 128, per-(sequence,
- * kv-head) merge counters that every call leaves at zero, and a work list.
- * Calls sharing a workspace must be stream-ordered.
+ * use. Layout: a fixed 1 MiB region of merge counters (at most 262144
+ * (sequence, kv-head) units) that every call leaves at zero, then the work
+ * list and split-context partials. Partials never overlap the counter region,
+ * so one workspace (large enough for each call) serves calls of any shape,
+ * and npd_paged_prefill_attention calls too, if they are stream-ordered.
  */
 int npd_paged_attention(void* out, const void* query,
                         const void* key_cache, const void* value_cache,
@@ -145,9 +148,10 @@ int64_t npd_paged_prefill_workspace_size(int64_t num_seqs, int64_t total_q,
  * max_context_len: host-known upper bound on context_lens; key ranges longer
  * than 1024 keys are split over up to 8 workgroups when it allows (<= 0: no
  * split). It sizes the workspace: npd_paged_prefill_workspace_size(...) bytes,
- * 256-byte aligned, zero-filled before first use; every call leaves its merge
- * counters at zero, so calls that share a workspace must be ordered on one
- * stream.
+ * 256-byte aligned, zero-filled before first use, with the same fixed 1 MiB
+ * counter region as npd_paged_attention's (every call leaves its counters at
+ * zero; partials follow the region), so any stream-ordered sequence of calls
+ * of either op may share one workspace that is large enough for each.
  */
 int npd_paged_prefill_attention(void* out, const void* query,
                                 const void* key_cache, const void* value_cache,

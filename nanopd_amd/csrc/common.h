@@ -18,6 +18,13 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Every workspace starts with a fixed region of int32 merge counters that all
+// attention ops share: partial results are only ever written after it, and
+// every call leaves the counters it used at zero. So a zero-filled workspace
+// stays valid across calls of any shape (and across ops), in stream order.
+constexpr int64_t kCounterBytes = 1 << 20;
+constexpr int64_t kMaxCounters = kCounterBytes / 4;
+
 // ---------------------------------------------------------------------------
 // Element conversions. Both storage types are 2 bytes; arithmetic is fp32.
 // bf16 -> f32 is exact (the bf16 bits are the high half of the f32 bits);

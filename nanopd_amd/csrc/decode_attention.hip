@@ -1103,11 +1103,10 @@ extern "C" int64_t npd_paged_attention_workspace_size(int64_t num_seqs, int64_t 
   const int64_t parts = (max_ctx + ps - 1) / ps;
   if (parts <= 1 && !use_fast_path(head_dim, block_size, num_seqs)) return 0;
   const int64_t partials = num_seqs * num_heads * parts * (head_dim + 2) * (int64_t)sizeof(float);
-  if (!use_fast_path(head_dim, block_size, num_seqs)) return partials;
-  // fast path: merge counters, item count (padded to 16 B), work list
+  if (!use_fast_path(head_dim, block_size, num_seqs)) return npd::kCounterBytes + partials;
+  // fast path: counter region, item count (16 B), work list, partials
   const int64_t units = num_seqs * num_kv_heads;
-  const int64_t counters = (units * 4 + 15) / 16 * 16;
-  return partials + counters + 16 + units * parts * 8;
+  return (npd::kCounterBytes + 16 + units * parts * 8 + 255) / 256 * 256 + partials;
 }
 
 extern "C" int npd_paged_attention(void* out, const void* query, const void* key_cache,
@@ -1179,12 +1178,19 @@ extern "C" int npd_paged_attention(void* out, const void* query, const void* key
   a.block_tables = block_tables;
   a.seq_lens = seq_lens;
   const int64_t units = num_seqs * num_kv_heads;
-  float* ws = static_cast<float*>(workspace);
-  a.part_acc = ws;
-  a.part_ml = ws ? ws + units * max_parts * g * head_dim : nullptr;
-  a.counters = ws ? reinterpret_cast<int*>(a.part_ml + units * max_parts * g * 2) : nullptr;
-  a.sched = ws ? a.counters + (units * 4 + 15) / 16 * 4 : nullptr;
-  a.items = ws ? reinterpret_cast<int2*>(a.sched + 4) : nullptr;
+  if (units > kMaxCounters)
+    return fail(NPD_E_INVALID, "%s: %lld (sequence, kv-head) units exceed the %lld merge counters",
+                name, (long long)units, (long long)kMaxCounters);
+  // [counters | item count | work list | partial acc | partial (m, l)]
+  char* wsb = static_cast<char*>(workspace);
+  const bool fast_ws = use_fast_path(head_dim, block_size, num_seqs);
+  const int64_t part_off =
+      fast_ws ? (kCounterBytes + 16 + units * max_parts * 8 + 255) / 256 * 256 : kCounterBytes;
+  a.counters = wsb ? reinterpret_cast<int*>(wsb) : nullptr;
+  a.sched = wsb ? reinterpret_cast<int*>(wsb + kCounterBytes) : nullptr;
+  a.items = wsb ? reinterpret_cast<int2*>(wsb + kCounterBytes + 16) : nullptr;
+  a.part_acc = wsb ? reinterpret_cast<float*>(wsb + part_off) : nullptr;
+  a.part_ml = wsb ? a.part_acc + units * max_parts * g * head_dim : nullptr;
   a.num_kv_heads = (int)num_kv_heads;
   a.num_seqs = (int)num_seqs;
   a.block_size = (int)block_size;

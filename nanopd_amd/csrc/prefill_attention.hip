@@ -558,9 +558,10 @@ int launch(int hw, const PrefillArgs& a, int64_t grid, hipStream_t st) {
   return npd::check_launch("npd_paged_prefill_attention");
 }
 
-// Workspace: [counters | O partials | (m, l) partials]. Sized for the most
-// records any head group / row tiling of these shapes can address: a sequence
-// has tiles_max * (4 / HW) * 2 <= ceil(max_q_len / 32) + 7 subtiles of 32 rows.
+// Workspace: [counter region (kCounterBytes) | O partials | (m, l) partials].
+// Sized for the most records any head group / row tiling of these shapes can
+// address: a sequence has tiles_max * (4 / HW) * 2 <= ceil(max_q_len / 32) + 7
+// subtiles of 32 rows.
 struct Layout {
   int splits, ks_steps;
   int64_t o_off, ml_off, total;
@@ -583,7 +584,7 @@ Layout prefill_layout(int64_t num_seqs, int64_t num_heads, int64_t max_q_len, in
   const int64_t t32 = (max_q_len + kWaveRows - 1) / kWaveRows + 7;
   const int64_t units = num_seqs * t32 * num_heads;
   const int64_t nrec = units * L.splits;
-  L.o_off = (units * 4 + 255) / 256 * 256;
+  L.o_off = npd::kCounterBytes;
   L.ml_off = L.o_off + nrec * kRecO * 4;
   L.total = L.ml_off + nrec * kRecML * 4;
   return L;
@@ -650,6 +651,9 @@ extern "C" int npd_paged_prefill_attention(
   const int rt = kPairs / hw;
   const int64_t tiles = (max_q_len + 64LL * rt - 1) / (64LL * rt);
   const int64_t hgroups = g / hw;
+  if (L.total > 0 && num_seqs * tiles * num_kv_heads * (g / hw) > kMaxCounters)
+    return fail(NPD_E_INVALID, "%s: too many query tiles for the %lld merge counters", name,
+                (long long)kMaxCounters);
   const int64_t groups = (int64_t)L.splits * num_seqs * num_kv_heads;
   const int64_t grid = (groups + 7) / 8 * 8 * tiles * hgroups;
   if (grid > INT32_MAX) return fail(NPD_E_INVALID, "%s: too many tiles", name);

@@ -1,0 +1,181 @@
+"""Qwen3 decoder with random weights whose attention runs on the paged
+kernels: the caller side of the hot path, as ModelRunner.paged_forward
+(nanoPD/engine/model_runner.py:75-213) patches HF Qwen3 attention.
+
+Per layer and per engine step, for a packed ragged batch (prefill chunk
+tokens first, then one token per decode sequence):
+  RMSNorm -> fused QKV projection -> per-head RMSNorm of q and k (Qwen3) ->
+  RoPE at each token's position -> paged_kv_store_slots of the step's K/V
+  (token-major, straight from the projection) -> paged_prefill_attention for
+  the prefill rows and paged_attention_forward for the decode rows ->
+  o_proj + residual -> RMSNorm -> SwiGLU MLP + residual.
+The reference stores K/V first and attends after (model_runner.py:146, :189);
+so does this. Its prefill SDPA sees only the chunk (model_runner.py:152-168);
+here prefill rows attend to the paged prefix as well, the same result for a
+sequence's first chunk and the correct one for later chunks.
+
+GEMMs, norms and activations are PyTorch (rocBLAS / hipBLASLt on the GPU);
+the attention backend is a parameter so that a test can run the same model
+with a PyTorch restatement of the attention and compare.
+Shapes follow Qwen3-8B (config.json of the Qwen3 release): 36 layers, hidden
+4096, 32 query / 8 kv heads of 128, MLP 12288, vocab 151936, RoPE theta 1e6,
+RMSNorm eps 1e-6, untied LM head.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Callable, Optional
+
+import torch
+import torch.nn.functional as F
+
+from . import paged_kernels as pk
+
+
+@dataclass(frozen=True)
+class Qwen3Config:
+    num_layers: int = 36
+    hidden: int = 4096
+    num_heads: int = 32
+    num_kv_heads: int = 8
+    head_dim: int = 128
+    intermediate: int = 12288
+    vocab: int = 151936
+    rope_theta: float = 1.0e6
+    rms_eps: float = 1.0e-6
+    init_std: float = 0.02
+
+    @property
+    def num_params(self) -> int:
+        qkv = self.hidden * (self.num_heads + 2 * self.num_kv_heads) * self.head_dim
+        o = self.num_heads * self.head_dim * self.hidden
+        mlp = 3 * self.hidden * self.intermediate
+        norms = 2 * self.hidden + 2 * self.head_dim
+        return (self.num_layers * (qkv + o + mlp + norms) + 2 * self.vocab * self.hidden
+                + self.hidden)
+
+
+QWEN3_8B = Qwen3Config()
+
+
+@dataclass
+class StepBatch:
+    """One engine step's packed batch, prefill sequences first.
+    meta: pack_metadata output; num_prefill_seqs / num_prefill_tokens: the
+    prefill part; sample_rows: token rows whose logits are wanted."""
+    input_ids: torch.Tensor          # int64 [T]
+    meta: pk.BatchMetadata
+    num_prefill_seqs: int
+    num_prefill_tokens: int
+    sample_rows: torch.Tensor        # int64 [R]
+    max_prefill_q: int = 0           # longest prefill chunk (grid bound)
+
+
+# attention(layer, q [T,H,D], k_cache, v_cache, batch, out [T,H,D]) -> None
+Attention = Callable[[int, torch.Tensor, torch.Tensor, torch.Tensor, StepBatch, torch.Tensor], None]
+
+
+class PagedQwen3:
+    def __init__(self, cfg: Qwen3Config, num_blocks: int, block_size: int = 16,
+                 device: str | torch.device = "cuda", dtype: torch.dtype = torch.bfloat16,
+                 seed: int = 0, attention: Optional[Attention] = None):
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self.dtype = dtype
+        self.block_size = block_size
+        self.num_blocks = num_blocks
+        self.scale = 1.0 / math.sqrt(cfg.head_dim)
+        self.attention = attention or self._paged_attention
+        g = torch.Generator(device=self.device)
+        g.manual_seed(seed)
+
+        def rnd(*shape):
+            w = torch.empty(*shape, dtype=dtype, device=self.device)
+            w.normal_(0.0, cfg.init_std, generator=g)
+            return w
+
+        def ones(n):
+            return torch.ones(n, dtype=dtype, device=self.device)
+
+        H, KV, D, E = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.hidden
+        self.embed = rnd(cfg.vocab, E)
+        self.layers = []
+        for _ in range(cfg.num_layers):
+            self.layers.append({
+                "in_norm": ones(E),
+                "qkv": rnd((H + 2 * KV) * D, E),
+                "q_norm": ones(D),
+                "k_norm": ones(D),
+                "o": rnd(E, H * D),
+                "post_norm": ones(E),
+                "gate_up": rnd(2 * cfg.intermediate, E),
+                "down": rnd(E, cfg.intermediate),
+            })
+        self.final_norm = ones(E)
+        self.lm_head = rnd(cfg.vocab, E)
+        self.inv_freq = 1.0 / (cfg.rope_theta ** (torch.arange(0, D, 2, dtype=torch.float32,
+                                                               device=self.device) / D))
+        shape = (cfg.num_layers, num_blocks, KV, block_size, D)
+        self.k_cache = torch.zeros(shape, dtype=dtype, device=self.device)
+        self.v_cache = torch.zeros(shape, dtype=dtype, device=self.device)
+
+    # -- pieces ------------------------------------------------------------
+    def _rope(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+        """Rotate-half RoPE (HF Qwen3 apply_rotary_pos_emb), in fp32."""
+        half = x.size(-1) // 2
+        xf = x.float()
+        x1, x2 = xf[..., :half], xf[..., half:]
+        return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1).to(x.dtype)
+
+    def _paged_attention(self, layer: int, q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor,
+                         b: StepBatch, out: torch.Tensor) -> None:
+        m, npf, tp = b.meta, b.num_prefill_seqs, b.num_prefill_tokens
+        T = q.size(0)
+        if npf:
+            pk.paged_prefill_attention(out[:tp], q[:tp], kc, vc, m.block_tables[:npf],
+                                       m.cu_seqlens_q[:npf + 1], m.seq_lens[:npf], self.scale,
+                                       self.block_size, m.max_blocks_per_seq,
+                                       max(1, b.max_prefill_q), m.max_seq_len)
+        if T > tp:
+            pk.paged_attention_forward(out[tp:], q[tp:], kc, vc, m.block_tables[npf:],
+                                       m.seq_lens[npf:], self.scale, self.block_size,
+                                       m.max_blocks_per_seq)
+
+    # -- forward -------------------------------------------------------------
+    @torch.no_grad()
+    def forward(self, b: StepBatch) -> torch.Tensor:
+        """Runs one packed step; returns fp32 logits [R, vocab] of b.sample_rows."""
+        cfg = self.cfg
+        H, KV, D, E = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.hidden
+        T = b.input_ids.numel()
+        pos = b.meta.positions.float()
+        freqs = pos[:, None] * self.inv_freq[None, :]
+        cos, sin = freqs.cos()[:, None, :], freqs.sin()[:, None, :]
+        x = F.embedding(b.input_ids, self.embed)
+        attn = torch.empty(T, H, D, dtype=self.dtype, device=self.device)
+        for li, w in enumerate(self.layers):
+            h = F.rms_norm(x, (E,), w["in_norm"], cfg.rms_eps)
+            qkv = h @ w["qkv"].t()
+            q = qkv[:, : H * D].view(T, H, D)
+            k = qkv[:, H * D:(H + KV) * D].view(T, KV, D)
+            v = qkv[:, (H + KV) * D:].view(T, KV, D)
+            q = self._rope(F.rms_norm(q, (D,), w["q_norm"], cfg.rms_eps), cos, sin)
+            k = self._rope(F.rms_norm(k, (D,), w["k_norm"], cfg.rms_eps), cos, sin)
+            kc, vc = self.k_cache[li], self.v_cache[li]
+            pk.paged_kv_store_slots(kc, vc, k, v, b.meta.slot_mapping)
+            self.attention(li, q, kc, vc, b, attn)
+            x = x + attn.view(T, H * D) @ w["o"].t()
+            h = F.rms_norm(x, (E,), w["post_norm"], cfg.rms_eps)
+            gu = h @ w["gate_up"].t()
+            x = x + (F.silu(gu[:, : cfg.intermediate]) * gu[:, cfg.intermediate:]) @ w["down"].t()
+        xs = F.rms_norm(x.index_select(0, b.sample_rows), (E,), self.final_norm, cfg.rms_eps)
+        return (xs @ self.lm_head.t()).float()
+
+    def copy_blocks(self, pairs) -> None:
+        """Copy-on-write copies (old, new) in every layer's cache."""
+        if not pairs:
+            return
+        t = torch.tensor(pairs, dtype=torch.int32).to(self.device)
+        for li in range(self.cfg.num_layers):
+            pk.copy_blocks(self.k_cache[li], self.v_cache[li], t)

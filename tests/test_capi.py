@@ -88,13 +88,13 @@ def test_c_validation_paths_need_no_gpu():
 
 def test_workspace_size():
     lib = _lib.load()
-    # fast path (head_dim 128): fp32 partials (G*D + 2G floats per partition),
-    # one int32 merge counter per (sequence, kv head) padded to 16 bytes, a
-    # 16-byte item count, and an 8-byte (unit, partition) work-list entry per
-    # possible partition.
+    # fast path (head_dim 128): the fixed 1 MiB counter region every workspace
+    # starts with, a 16-byte item count, an 8-byte (unit, partition) work-list
+    # entry per possible partition (padded to 256 bytes), then fp32 partials
+    # (G*D + 2G floats per partition).
     def fast(S, H, kvh, P):
         units = S * kvh
-        return S * H * P * 130 * 4 + (units * 4 + 15) // 16 * 16 + 16 + units * P * 8
+        return (2**20 + 16 + units * P * 8 + 255) // 256 * 256 + S * H * P * 130 * 4
     # 1024 seqs x 8 kv heads x 256 tokens: one partition of 256 each
     assert lib.npd_paged_attention_workspace_size(1024, 32, 8, 128, 16, 16) == fast(1024, 32, 8, 1)
     # 64 seqs x 8 kv heads x 256 tokens: 512 waves -> partitions of 64 (4 each)
@@ -105,7 +105,7 @@ def test_workspace_size():
     assert lib.npd_paged_attention_workspace_size(1, 32, 8, 128, 16, 256) == fast(1, 32, 8, 64)
     # generic path (head_dim 64): partitions of 256 below 4096 waves
     n = lib.npd_paged_attention_workspace_size(2, 8, 8, 64, 16, 64)
-    assert n == 2 * 8 * 4 * (64 + 2) * 4
+    assert n == 2**20 + 2 * 8 * 4 * (64 + 2) * 4
 
 
 def test_prefill_workspace_size():
@@ -113,13 +113,13 @@ def test_prefill_workspace_size():
     # key ranges up to 16 steps of 64 keys run whole: no workspace
     assert lib.npd_paged_prefill_workspace_size(4, 2048, 32, 128, 512, 1024) == 0
     assert lib.npd_paged_prefill_workspace_size(4, 2048, 32, 128, 512, 0) == 0
-    # longer ranges are split (at most 8 ways): int32 counters per (sequence,
-    # row subtile of 32, head), padded to 256 bytes, then per (..., split) an O
-    # record of 32 rows x 128 fp32 and an (m, l) record of 32 rows x 2 x 4 lanes
+    # longer ranges are split (at most 8 ways): the 1 MiB counter region, then
+    # per (sequence, row subtile of 32, head, split) an O record of 32 rows x
+    # 128 fp32 and an (m, l) record of 32 rows x 2 x 4 lanes
     def split(S, H, max_q, splits):
         t32 = (max_q + 31) // 32 + 7
         units = S * t32 * H
-        return (units * 4 + 255) // 256 * 256 + units * splits * (16384 + 1024)
+        return 2**20 + units * splits * (16384 + 1024)
     assert lib.npd_paged_prefill_workspace_size(4, 2048, 32, 128, 512, 3584) == split(4, 32, 512, 4)
     assert lib.npd_paged_prefill_workspace_size(1, 100, 32, 128, 100, 1025) == split(1, 32, 100, 2)
     assert lib.npd_paged_prefill_workspace_size(2, 1024, 32, 128, 512, 32768) == split(2, 32, 512, 8)

@@ -221,3 +221,37 @@ def test_workspace_reuse_across_calls(device, num_seqs):
         pk.paged_attention_forward(out, q, kc, vc, bt, sl, scale, 16, mb, workspace=ws)
         torch.cuda.synchronize()
         check(out, q, kc, vc, bt, sl, scale)
+
+
+def test_workspace_shared_across_shapes_and_ops(device):
+    """One zero-filled workspace serves decode calls whose layouts differ
+    (sequence count, table width -> partition count, work-list and partial
+    offsets) and a chunked-prefill call in between: the merge counters sit in a
+    fixed region that partial results never overwrite, and each call leaves
+    its counters at zero. (A serving engine calls with a new shape every step.)"""
+    from tests.test_gpu_prefill import make_case, oracle as prefill_oracle
+    shapes = [(70, 1500, 94), (6, 4000, 250), (33, 700, 44), (70, 1500, 94), (64, 2500, 157)]
+    need = max(pk.attention_workspace_bytes(n, 32, 8, 128, 16, mb) for n, _, mb in shapes)
+    pq, pkc, pvc, pbt, pcu, pctx, pmb, pmq = make_case(device, [2500, 900], [200, 64], seed=41)
+    need = max(need, pk.prefill_workspace_bytes(2, int(pq.size(0)), 32, 128, pmq, pmb * 16))
+    ws = torch.zeros(need, dtype=torch.uint8, device=device)
+    for i, (n, top, mb) in enumerate(shapes):
+        g = torch.Generator().manual_seed(100 + i)
+        lens = torch.randint(1, top + 1, (n,), generator=g).tolist()
+        lens[0] = top
+        q, kc, vc, bt, sl, scale, mbi = make_inputs(n, 32, 8, 128, lens, 16, torch.bfloat16,
+                                                    device, seed=50 + i)
+        assert mbi <= mb
+        btw = torch.zeros(n, mb, dtype=torch.int32, device=device)
+        btw[:, :mbi] = bt
+        out = torch.full_like(q, float("nan"))
+        pk.paged_attention_forward(out, q, kc, vc, btw, sl, scale, 16, mb, workspace=ws)
+        torch.cuda.synchronize()
+        check(out, q, kc, vc, btw, sl, scale)
+        if i == 1:
+            pout = torch.full_like(pq, float("nan"))
+            pk.paged_prefill_attention(pout, pq, pkc, pvc, pbt, pcu, pctx, 1 / math.sqrt(128), 16,
+                                       pmb, pmq, workspace=ws)
+            torch.cuda.synchronize()
+            want = prefill_oracle(pq, pkc, pvc, pbt, pcu, pctx, 1 / math.sqrt(128))
+            assert max_abs(pout, want) <= ATOL[torch.bfloat16]
