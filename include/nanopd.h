@@ -182,6 +182,36 @@ int npd_copy_blocks(void* k_cache, void* v_cache, const int32_t* pairs,
                     int64_t block_elems, int32_t dtype, void* stream);
 
 /*
+ * Fused attention prologue of a Qwen3-style layer (replaces the per-layer
+ * q_norm / k_norm, rotary embedding, K/V transpose copies and paged_kv_store
+ * calls of nanoPD/engine/model_runner.py:97-115, :142-146, :189-192).
+ * qkv: [num_tokens, (num_heads + 2 num_kv_heads) * head_dim] token rows
+ * (q heads, then k heads, then v heads) with token stride qkv_stride_token
+ * elements -- the fused QKV projection output as it is.
+ * For each token t, at position positions[t]:
+ *   q_out[t, h, :]        = rope(rmsnorm(q[t, h, :], q_norm_weight))
+ *   k_cache[slot, kh, :]  = rope(rmsnorm(k[t, kh, :], k_norm_weight))
+ *   v_cache[slot, kh, :]  = v[t, kh, :]
+ * with slot = slot_mapping[t] (block * block_size + offset, pool layout
+ * [num_blocks, num_kv_heads, block_size, head_dim]); tokens whose slot is
+ * negative or outside the pool are not stored (q_out is still written).
+ * rmsnorm(x, w) = half(half(x * rsqrt(mean(x^2) + eps)) * w) as HF
+ * Qwen3RMSNorm; rope is rotate-half with angle positions[t] * inv_freq[i]
+ * (inv_freq: fp32 [head_dim / 2]), computed in fp32 and rounded once.
+ * q_out token stride is q_stride_token elements (heads contiguous).
+ * head_dim 128 only; dtype fp16 or bf16 for every 2-byte tensor.
+ */
+int npd_qk_norm_rope_store(void* q_out, void* k_cache, void* v_cache,
+                           const void* qkv, const int32_t* slot_mapping,
+                           const int32_t* positions, const float* inv_freq,
+                           const void* q_norm_weight, const void* k_norm_weight,
+                           int64_t num_tokens, int64_t num_heads,
+                           int64_t num_kv_heads, int64_t head_dim,
+                           int64_t num_blocks, int64_t block_size,
+                           int64_t qkv_stride_token, int64_t q_stride_token,
+                           float eps, int32_t dtype, void* stream);
+
+/*
  * Ragged-batch metadata packing on the GPU (no reference counterpart: the
  * reference re-tensorises its context dict per layer with host loops,
  * nanoPD/engine/model_runner.py:129-187, from nanoPD/engine/engine.py:45-90).

@@ -1,0 +1,156 @@
+// Fused attention prologue for Qwen3-style layers: per-head RMSNorm of q and k
+// (q_norm / k_norm), rotate-half RoPE at each token's position, and the paged
+// KV store of the rotated k and of v by slot -- one launch per layer, reading
+// the fused QKV projection output as it is.
+//
+// Reference: per layer, paged_forward runs HF Qwen3Attention's q_norm / k_norm
+// and apply_rotary_pos_emb (nanoPD/engine/model_runner.py:97-115), transposes
+// and copies k / v (.contiguous(), :142-143, :191-192) and calls
+// paged_kv_store (:146, :189): about a dozen elementwise launches plus the
+// copies. Here one wave handles one (token, head) row of the QKV output:
+//   rows [0, H)           q heads: normalise, rotate, write q_out
+//   rows [H, H + KV)      k heads: normalise, rotate, store to k_cache[slot]
+//   rows [H + KV, H + 2KV) v heads: store to v_cache[slot]
+// Lane l holds elements l and l + 64 of the 128-wide row: exactly a
+// rotate-half pair, so RoPE needs no data exchange.
+// RMSNorm rounds as HF Qwen3RMSNorm does (transformers modeling_qwen3):
+// n = half(half(x * rsqrt(mean(x^2) + eps)) * w), with the mean in fp32.
+// RoPE then rotates n in fp32 with cos / sin of pos * inv_freq[l] (inv_freq
+// from the caller, fp32) and rounds once. The reference's HF
+// apply_rotary_pos_emb rounds cos / sin and each product to the model dtype
+// first; the fp32 rotation here is the more accurate of the two and differs
+// from it by a few half-precision ulps at most.
+#include "common.h"
+
+namespace {
+
+constexpr int kThreads = 256;   // 4 rows per workgroup
+constexpr int kD = 128;
+
+struct RopeArgs {
+  uint16_t* q_out;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  const uint16_t* qkv;
+  const int32_t* slots;
+  const int32_t* positions;
+  const float* inv_freq;
+  const uint16_t* q_w;
+  const uint16_t* k_w;
+  int64_t rows;               // tokens * (H + 2 KV)
+  int heads, kv_heads, block_size, num_blocks;
+  int64_t qkv_stride, q_stride;
+  float eps;
+};
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
+  return x;
+}
+
+template <class TT>
+__device__ __forceinline__ float ld(const uint16_t* p) {
+  return TT::lo((uint32_t)*p);
+}
+
+template <class TT>
+__global__ __launch_bounds__(kThreads) void qk_norm_rope_store_kernel(RopeArgs a) {
+  const int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  const int l = threadIdx.x & 63;
+  const int per = a.heads + 2 * a.kv_heads;
+  const int64_t t = row / per;
+  const int hh = (int)(row - t * per);
+  const uint16_t* src = a.qkv + t * a.qkv_stride + (int64_t)hh * kD;
+  const float x0 = ld<TT>(src + l), x1 = ld<TT>(src + l + 64);
+
+  const int slot = a.slots[t];
+  const bool store = slot >= 0 && slot < a.num_blocks * a.block_size;
+  const int64_t blk = store ? slot / a.block_size : 0;
+  const int off = store ? slot - (int)blk * a.block_size : 0;
+
+  if (hh >= a.heads + a.kv_heads) {   // v: plain store
+    if (!store) return;
+    uint16_t* dst = a.v_cache + ((blk * a.kv_heads + (hh - a.heads - a.kv_heads)) * a.block_size + off) * kD;
+    dst[l] = src[l];
+    dst[l + 64] = src[l + 64];
+    return;
+  }
+  const bool is_q = hh < a.heads;
+  const uint16_t* w = is_q ? a.q_w : a.k_w;
+  const float r = rsqrtf(wave_sum(x0 * x0 + x1 * x1) * (1.f / kD) + a.eps);
+  const float n0 = TT::lo(TT::from_float(TT::lo(TT::from_float(x0 * r)) * ld<TT>(w + l)));
+  const float n1 = TT::lo(TT::from_float(TT::lo(TT::from_float(x1 * r)) * ld<TT>(w + l + 64)));
+  float s, c;
+  sincosf((float)a.positions[t] * a.inv_freq[l], &s, &c);
+  const uint16_t y0 = (uint16_t)TT::from_float(n0 * c - n1 * s);
+  const uint16_t y1 = (uint16_t)TT::from_float(n1 * c + n0 * s);
+  uint16_t* dst;
+  if (is_q) {
+    dst = a.q_out + t * a.q_stride + (int64_t)hh * kD;
+  } else {
+    if (!store) return;
+    dst = a.k_cache + ((blk * a.kv_heads + (hh - a.heads)) * a.block_size + off) * kD;
+  }
+  dst[l] = y0;
+  dst[l + 64] = y1;
+}
+
+}  // namespace
+
+extern "C" int npd_qk_norm_rope_store(void* q_out, void* k_cache, void* v_cache, const void* qkv,
+                                      const int32_t* slot_mapping, const int32_t* positions,
+                                      const float* inv_freq, const void* q_norm_weight,
+                                      const void* k_norm_weight, int64_t num_tokens,
+                                      int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                                      int64_t num_blocks, int64_t block_size,
+                                      int64_t qkv_stride_token, int64_t q_stride_token, float eps,
+                                      int32_t dtype, void* stream) {
+  using namespace npd;
+  const char* name = "npd_qk_norm_rope_store";
+  if (dtype != NPD_DTYPE_F16 && dtype != NPD_DTYPE_BF16)
+    return fail(NPD_E_DTYPE, "%s: unsupported dtype code %d (fp16/bf16 only)", name, dtype);
+  if (head_dim != kD)
+    return fail(NPD_E_INVALID, "%s: head_dim %lld not supported (128 only)", name,
+                (long long)head_dim);
+  if (num_tokens < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_blocks <= 0 || block_size <= 0)
+    return fail(NPD_E_INVALID, "%s: bad sizes", name);
+  if (num_blocks * block_size > INT32_MAX)
+    return fail(NPD_E_INVALID, "%s: pool exceeds int32 slot indexing", name);
+  if (qkv_stride_token < (num_heads + 2 * num_kv_heads) * head_dim || q_stride_token < num_heads * head_dim)
+    return fail(NPD_E_INVALID, "%s: token strides shorter than a token's heads", name);
+  if (!(eps >= 0.f))
+    return fail(NPD_E_INVALID, "%s: eps must be non-negative", name);
+  if (num_tokens == 0) return NPD_OK;
+  if (!q_out || !k_cache || !v_cache || !qkv || !slot_mapping || !positions || !inv_freq ||
+      !q_norm_weight || !k_norm_weight)
+    return fail(NPD_E_INVALID, "%s: null pointer", name);
+  const int64_t rows = num_tokens * (num_heads + 2 * num_kv_heads);
+  const int64_t grid = (rows + 3) / 4;
+  if (grid > INT32_MAX) return fail(NPD_E_INVALID, "%s: too many rows", name);
+  RopeArgs a;
+  a.q_out = static_cast<uint16_t*>(q_out);
+  a.k_cache = static_cast<uint16_t*>(k_cache);
+  a.v_cache = static_cast<uint16_t*>(v_cache);
+  a.qkv = static_cast<const uint16_t*>(qkv);
+  a.slots = slot_mapping;
+  a.positions = positions;
+  a.inv_freq = inv_freq;
+  a.q_w = static_cast<const uint16_t*>(q_norm_weight);
+  a.k_w = static_cast<const uint16_t*>(k_norm_weight);
+  a.rows = rows;
+  a.heads = (int)num_heads;
+  a.kv_heads = (int)num_kv_heads;
+  a.block_size = (int)block_size;
+  a.num_blocks = (int)num_blocks;
+  a.qkv_stride = qkv_stride_token;
+  a.q_stride = q_stride_token;
+  a.eps = eps;
+  hipStream_t st = as_stream(stream);
+  if (dtype == NPD_DTYPE_BF16)
+    hipLaunchKernelGGL(qk_norm_rope_store_kernel<BF16>, dim3((unsigned)grid), dim3(kThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL(qk_norm_rope_store_kernel<F16>, dim3((unsigned)grid), dim3(kThreads), 0, st, a);
+  return check_launch(name);
+}

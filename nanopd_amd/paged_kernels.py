@@ -11,6 +11,7 @@ plus the ops the MI355X path adds:
 * :func:`paged_kv_store_slots` -- store by flat slot mapping, strided sources
 * :func:`paged_prefill_attention` -- varlen chunked prefill over the paged prefix
 * :func:`copy_blocks` -- copy-on-write block copy
+* :func:`qk_norm_rope_store` -- Qwen3 q/k RMSNorm + RoPE + paged K/V store, fused
 * :func:`pack_metadata` -- ragged-batch metadata built on the GPU
 
 Every op validates its arguments here (``RuntimeError``, as ``TORCH_CHECK``
@@ -29,7 +30,7 @@ from . import _lib
 __all__ = [
     "paged_kv_store", "paged_kv_store_slots", "paged_attention_forward",
     "paged_prefill_attention", "copy_blocks", "pack_metadata", "BatchMetadata",
-    "attention_workspace_bytes", "prefill_workspace_bytes",
+    "attention_workspace_bytes", "prefill_workspace_bytes", "qk_norm_rope_store",
 ]
 
 _DTYPES = {torch.float16: _lib.NPD_DTYPE_F16, torch.bfloat16: _lib.NPD_DTYPE_BF16}
@@ -342,6 +343,54 @@ def copy_blocks(k_cache: torch.Tensor, v_cache: torch.Tensor, block_pairs) -> No
     per_block = k_cache[0].numel()
     _lib.call("npd_copy_blocks", k_cache.data_ptr(), v_cache.data_ptr(), block_pairs.data_ptr(), n,
               k_cache.size(0), per_block, code, _stream(dev))
+
+
+def qk_norm_rope_store(q_out: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                       qkv: torch.Tensor, slot_mapping: torch.Tensor, positions: torch.Tensor,
+                       inv_freq: torch.Tensor, q_norm_weight: torch.Tensor,
+                       k_norm_weight: torch.Tensor, eps: float) -> None:
+    """Qwen3 attention prologue in one launch (replaces q_norm / k_norm,
+    rotary embedding, the K/V copies and paged_kv_store of
+    nanoPD/engine/model_runner.py:97-115, :142-146, :189-192).
+
+    qkv: [T, (H + 2 KV) * D] rows of the fused projection (q, k, v heads;
+    token stride free, elements contiguous); q_out: [T, H, D], heads
+    contiguous; slot_mapping / positions: int32 [T]; inv_freq: fp32 [D / 2];
+    norm weights: [D] in the cache dtype. Writes normalised + rotated q to
+    q_out, normalised + rotated k and raw v to the caches at slot_mapping
+    (negative slots are not stored). D = 128.
+    """
+    _cache_checks(k_cache, v_cache)
+    dev = qkv.device
+    _check(qkv.is_cuda, "qkv must be on CUDA")
+    _same_device(dev, q_out, k_cache, v_cache, slot_mapping, positions, inv_freq, q_norm_weight,
+                 k_norm_weight)
+    _int32(slot_mapping, "slot_mapping")
+    _int32(positions, "positions")
+    num_blocks, kvh, bs, d = k_cache.shape
+    _check(q_out.dim() == 3 and q_out.size(2) == d, "q_out must be [num_tokens, num_heads, head_dim]")
+    t, h = q_out.size(0), q_out.size(1)
+    _check(qkv.dim() == 2 and qkv.size(0) == t and qkv.size(1) == (h + 2 * kvh) * d,
+           "qkv must be [num_tokens, (num_heads + 2 * num_kv_heads) * head_dim]")
+    _check(qkv.stride(1) == 1, "qkv rows must be contiguous")
+    _check(q_out.stride(2) == 1 and q_out.stride(1) == d, "q_out heads must be contiguous")
+    for x in (q_out, qkv, q_norm_weight, k_norm_weight):
+        _check(x.dtype == k_cache.dtype, "qkv / q_out / norm weights must have the cache dtype")
+    _check(q_norm_weight.numel() == d and k_norm_weight.numel() == d
+           and q_norm_weight.is_contiguous() and k_norm_weight.is_contiguous(),
+           "norm weights must be contiguous [head_dim]")
+    _check(inv_freq.dtype == torch.float32 and inv_freq.numel() == d // 2
+           and inv_freq.is_contiguous(), "inv_freq must be contiguous float32 [head_dim / 2]")
+    for x, nm in ((slot_mapping, "slot_mapping"), (positions, "positions")):
+        _check(x.dim() == 1 and x.numel() >= t and x.is_contiguous(),
+               f"{nm} must be a contiguous [num_tokens] tensor")
+    code = _dtype_code(k_cache, "qk_norm_rope_store")
+    if t == 0:
+        return
+    _lib.call("npd_qk_norm_rope_store", q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+              qkv.data_ptr(), slot_mapping.data_ptr(), positions.data_ptr(), inv_freq.data_ptr(),
+              q_norm_weight.data_ptr(), k_norm_weight.data_ptr(), t, h, kvh, d, num_blocks, bs,
+              qkv.stride(0), q_out.stride(0), float(eps), code, _stream(dev))
 
 
 class BatchMetadata(NamedTuple):

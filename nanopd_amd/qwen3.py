@@ -4,11 +4,13 @@ kernels: the caller side of the hot path, as ModelRunner.paged_forward
 
 Per layer and per engine step, for a packed ragged batch (prefill chunk
 tokens first, then one token per decode sequence):
-  RMSNorm -> fused QKV projection -> per-head RMSNorm of q and k (Qwen3) ->
-  RoPE at each token's position -> paged_kv_store_slots of the step's K/V
-  (token-major, straight from the projection) -> paged_prefill_attention for
-  the prefill rows and paged_attention_forward for the decode rows ->
-  o_proj + residual -> RMSNorm -> SwiGLU MLP + residual.
+  RMSNorm -> fused QKV projection -> qk_norm_rope_store (per-head RMSNorm of
+  q and k, RoPE at each token's position, K/V into the paged pool by slot,
+  one launch) -> paged_prefill_attention for the prefill rows and
+  paged_attention_forward for the decode rows -> o_proj + residual ->
+  RMSNorm -> SwiGLU MLP + residual.
+With fused_prologue=False the prologue runs as PyTorch ops (HF Qwen3RMSNorm
+rounding, fp32 rotate-half RoPE) followed by paged_kv_store_slots.
 The reference stores K/V first and attends after (model_runner.py:146, :189);
 so does this. Its prefill SDPA sees only the chunk (model_runner.py:152-168);
 here prefill rows attend to the paged prefix as well, the same result for a
@@ -79,7 +81,8 @@ Attention = Callable[[int, torch.Tensor, torch.Tensor, torch.Tensor, StepBatch, 
 class PagedQwen3:
     def __init__(self, cfg: Qwen3Config, num_blocks: int, block_size: int = 16,
                  device: str | torch.device = "cuda", dtype: torch.dtype = torch.bfloat16,
-                 seed: int = 0, attention: Optional[Attention] = None):
+                 seed: int = 0, attention: Optional[Attention] = None,
+                 fused_prologue: bool = True):
         self.cfg = cfg
         self.device = torch.device(device)
         self.dtype = dtype
@@ -87,6 +90,7 @@ class PagedQwen3:
         self.num_blocks = num_blocks
         self.scale = 1.0 / math.sqrt(cfg.head_dim)
         self.attention = attention or self._paged_attention
+        self.fused_prologue = fused_prologue
         g = torch.Generator(device=self.device)
         g.manual_seed(seed)
 
@@ -128,6 +132,31 @@ class PagedQwen3:
         x1, x2 = xf[..., :half], xf[..., half:]
         return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1).to(x.dtype)
 
+    def _rms_norm_heads(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        """HF Qwen3RMSNorm over head_dim: fp32 statistics, round, times w."""
+        xf = x.float()
+        r = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.cfg.rms_eps)
+        return w * (xf * r).to(x.dtype)
+
+    def _prologue(self, li: int, w: dict, qkv: torch.Tensor, q: torch.Tensor, b: StepBatch,
+                  rope) -> None:
+        """q/k norm + RoPE into q, K/V of the step into layer li's pool."""
+        cfg = self.cfg
+        H, KV, D = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
+        kc, vc = self.k_cache[li], self.v_cache[li]
+        if self.fused_prologue:
+            pk.qk_norm_rope_store(q, kc, vc, qkv, b.meta.slot_mapping, b.meta.positions,
+                                  self.inv_freq, w["q_norm"], w["k_norm"], cfg.rms_eps)
+            return
+        T = qkv.size(0)
+        cos, sin = rope
+        qh = qkv[:, : H * D].view(T, H, D)
+        k = qkv[:, H * D:(H + KV) * D].view(T, KV, D)
+        v = qkv[:, (H + KV) * D:].view(T, KV, D)
+        q.copy_(self._rope(self._rms_norm_heads(qh, w["q_norm"]), cos, sin))
+        k = self._rope(self._rms_norm_heads(k, w["k_norm"]), cos, sin)
+        pk.paged_kv_store_slots(kc, vc, k, v, b.meta.slot_mapping)
+
     def _paged_attention(self, layer: int, q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor,
                          b: StepBatch, out: torch.Tensor) -> None:
         m, npf, tp = b.meta, b.num_prefill_seqs, b.num_prefill_tokens
@@ -149,21 +178,18 @@ class PagedQwen3:
         cfg = self.cfg
         H, KV, D, E = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.hidden
         T = b.input_ids.numel()
-        pos = b.meta.positions.float()
-        freqs = pos[:, None] * self.inv_freq[None, :]
-        cos, sin = freqs.cos()[:, None, :], freqs.sin()[:, None, :]
+        rope = None
+        if not self.fused_prologue:
+            freqs = b.meta.positions.float()[:, None] * self.inv_freq[None, :]
+            rope = (freqs.cos()[:, None, :], freqs.sin()[:, None, :])
         x = F.embedding(b.input_ids, self.embed)
+        q = torch.empty(T, H, D, dtype=self.dtype, device=self.device)
         attn = torch.empty(T, H, D, dtype=self.dtype, device=self.device)
         for li, w in enumerate(self.layers):
             h = F.rms_norm(x, (E,), w["in_norm"], cfg.rms_eps)
             qkv = h @ w["qkv"].t()
-            q = qkv[:, : H * D].view(T, H, D)
-            k = qkv[:, H * D:(H + KV) * D].view(T, KV, D)
-            v = qkv[:, (H + KV) * D:].view(T, KV, D)
-            q = self._rope(F.rms_norm(q, (D,), w["q_norm"], cfg.rms_eps), cos, sin)
-            k = self._rope(F.rms_norm(k, (D,), w["k_norm"], cfg.rms_eps), cos, sin)
+            self._prologue(li, w, qkv, q, b, rope)
             kc, vc = self.k_cache[li], self.v_cache[li]
-            pk.paged_kv_store_slots(kc, vc, k, v, b.meta.slot_mapping)
             self.attention(li, q, kc, vc, b, attn)
             x = x + attn.view(T, H * D) @ w["o"].t()
             h = F.rms_norm(x, (E,), w["post_norm"], cfg.rms_eps)

@@ -84,6 +84,14 @@ def test_c_validation_paths_need_no_gpu():
     assert _rc("npd_copy_blocks", fake, fake, fake, 3, 10, 1004, 1, None) == -3
     assert _rc("npd_pack_metadata", fake, fake, 5000, 1, 1, 4, 16, fake, fake, fake, fake, fake,
                fake, None) == -1
+    # fused q/k norm + rope + store: head_dim, short token stride, dtype, no-op
+    rope = lambda d, stride, code, t=4: _rc(  # noqa: E731
+        "npd_qk_norm_rope_store", fake, fake, fake, fake, fake, fake, fake, fake, fake, t, 32, 8, d,
+        64, 16, stride, 32 * d, ctypes.c_float(1e-6), code, None)
+    assert rope(64, 48 * 64, 1) == -1 and b"head_dim" in lib.npd_last_error()
+    assert rope(128, 40 * 128, 1) == -1 and b"stride" in lib.npd_last_error()
+    assert rope(128, 48 * 128, 5) == -2
+    assert rope(128, 48 * 128, 1, t=0) == 0
 
 
 def test_workspace_size():

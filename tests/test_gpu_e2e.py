@@ -47,9 +47,9 @@ def torch_attention(layer, q, kc, vc, b: StepBatch, out):
         out[a:e] = torch.matmul(torch.softmax(sc, dim=-1), V).transpose(0, 1).to(out.dtype)
 
 
-def _model(device, attention=None):
+def _model(device, attention=None, fused_prologue=True):
     return PagedQwen3(SMALL, num_blocks=512, block_size=16, device=device, seed=3,
-                      attention=attention)
+                      attention=attention, fused_prologue=fused_prologue)
 
 
 def _mixed_batch(model, device):
@@ -94,6 +94,26 @@ def test_mixed_step_logits_match_torch_attention(device):
     assert (lh.argmax(-1) == lr.argmax(-1)).float().mean().item() >= 5 / 6
     # layer 0's K/V come from identical inputs: the stores wrote identical caches
     assert torch.equal(hip.k_cache[0], ref.k_cache[0]) and torch.equal(hip.v_cache[0], ref.v_cache[0])
+
+
+def test_fused_prologue_matches_pytorch_prologue(device):
+    """qk_norm_rope_store against the PyTorch prologue (HF q/k norm, fp32
+    RoPE, paged_kv_store_slots) inside the model: same step, same caches."""
+    fused = _model(device)
+    comp = _model(device, fused_prologue=False)
+    b = _mixed_batch(fused, device)
+    lf, lc = fused.forward(b), comp.forward(b)
+    torch.cuda.synchronize()
+    # layer 0 sees identical inputs: its K/V rows agree up to a rare
+    # last-place rounding difference, V exactly
+    assert torch.equal(fused.v_cache[0], comp.v_cache[0])
+    d = (fused.k_cache[0].float() - comp.k_cache[0].float()).abs()
+    assert (d == 0).float().mean().item() > 0.999 and d.max().item() <= 0.05
+    err = (lf - lc).abs().max().item()
+    spread = lc.abs().max().item()
+    print(f"fused vs PyTorch prologue: logits max-abs {err:.3e} (|logits| max {spread:.2f})")
+    assert err <= 1e-2 * max(1.0, spread)
+    assert (lf.argmax(-1) == lc.argmax(-1)).float().mean().item() >= 5 / 6
 
 
 def test_teacher_forced_steps_agree_with_torch_attention(device):
