@@ -38,6 +38,9 @@ constexpr int kStep = 16;            // tokens per step
 #ifndef NPD_DECODE_NT
 #define NPD_DECODE_NT 1
 #endif
+#ifndef NPD_DECODE_PRIO
+#define NPD_DECODE_PRIO 1
+#endif
 #ifndef NPD_DECODE_PV_DOT2
 #define NPD_DECODE_PV_DOT2 1
 #endif
@@ -655,14 +658,25 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
     u32x4 kb[NBUF][4];
 #pragma unroll
     for (int b = 0; b < NBUF; ++b) load_k(kb[b], b);
-    int st0 = 0;
-    for (; st0 + NBUF < nsteps; st0 += NBUF) {
+    auto round = [&](int st0) {
 #pragma unroll
       for (int b = 0; b < NBUF; ++b) {
         score_step(kb[b], st0 + b);
         load_k(kb[b], st0 + NBUF + b);
       }
-    }
+    };
+    int st0 = 0;
+#if NPD_DECODE_PRIO
+    // Issue priority falls as the wave advances (3, 2 in pass 1; 1, 0 in
+    // pass 3): a SIMD's arbiter otherwise favours its oldest wave, so the
+    // youngest waves lag and the call ends with a few of them alone, each with
+    // only its own loads in flight.
+    __builtin_amdgcn_s_setprio(3);
+    const int half = (nsteps / (2 * NBUF)) * NBUF;
+    for (; st0 < half; st0 += NBUF) round(st0);
+    __builtin_amdgcn_s_setprio(2);
+#endif
+    for (; st0 + NBUF < nsteps; st0 += NBUF) round(st0);
 #pragma unroll
     for (int b = 0; b < NBUF; ++b) score_step(kb[b], st0 + b);
   }
@@ -787,14 +801,21 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
 #endif
   };
   {
-    int st0 = 0;
-    for (; st0 + NBUF < nsteps; st0 += NBUF) {
+    auto round = [&](int st0) {
 #pragma unroll
       for (int b = 0; b < NBUF; ++b) {
         pv_step(vb[b], st0 + b);
         load_v(vb[b], st0 + NBUF + b);
       }
-    }
+    };
+    int st0 = 0;
+#if NPD_DECODE_PRIO
+    __builtin_amdgcn_s_setprio(1);
+    const int half = (nsteps / (2 * NBUF)) * NBUF;
+    for (; st0 < half; st0 += NBUF) round(st0);
+    __builtin_amdgcn_s_setprio(0);
+#endif
+    for (; st0 + NBUF < nsteps; st0 += NBUF) round(st0);
 #pragma unroll
     for (int b = 0; b < NBUF; ++b) pv_step(vb[b], st0 + b);
   }
