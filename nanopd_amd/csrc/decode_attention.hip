@@ -441,20 +441,30 @@ using npd::st_coherent2;
 
 // Merge of one (sequence, kv-head) by a single wave (fast path, D = 128), the
 // same log-sum-exp merge as merge_unit but latency-bound work done in parallel:
-//   A: lanes take partitions, load (m, l) per head, and wave-reduce M and L;
-//   B: per chunk of 64 partitions, the weights 2^(m_p - M) go to LDS and each
-//      lane accumulates its (head, 8-dim chunk) with 4 partitions of loads in
-//      flight at a time.
+//   A: lane p loads (m, l) of partition p for every head; a wave reduction
+//      gives M (partitions past 64 are read in a second loop);
+//   B: per chunk of 64 partitions, the weights 2^(m_p - M) go to LDS (0 past
+//      the last partition) and each lane accumulates its (head, 8-dim chunk)
+//      with kMergeFlight partitions of loads in flight. The loads are
+//      unconditional (clamped to the chunk's last partition, weight 0), so
+//      each wait covers exactly one batch.
+constexpr int kMergeFlight = 4;
 template <class TT, int G>
 __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int unit, int s, int kh,
                                                 int nparts, int lane, float* s_w) {
   constexpr int D = 128, GP = pow2ceil(G), CH = D / 8;
   constexpr int OWN = (G * CH + 63) / 64;   // (head, chunk) pairs per lane
   const int64_t base = (int64_t)unit * a.max_parts;
-  float M[G], L[G];
+  float M[G], L[G], m0[G], l0[G];   // m0, l0: partition `lane`
 #pragma unroll
-  for (int h = 0; h < G; ++h) { M[h] = -INFINITY; L[h] = 0.f; }
-  for (int p = lane; p < nparts; p += 64) {
+  for (int h = 0; h < G; ++h) { m0[h] = -INFINITY; l0[h] = 0.f; }
+  if (lane < nparts) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) ld_coherent2(a.part_ml + ((base + lane) * G + h) * 2, m0[h], l0[h]);
+  }
+#pragma unroll
+  for (int h = 0; h < G; ++h) { M[h] = m0[h]; L[h] = 0.f; }
+  for (int p = lane + 64; p < nparts; p += 64) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
       float mp, lp;
@@ -477,8 +487,8 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int unit, i
     for (int h = 0; h < G; ++h) {
       float w = 0.f;
       if (p < nparts) {
-        float mp, lp;
-        ld_coherent2(a.part_ml + ((base + p) * G + h) * 2, mp, lp);
+        float mp = m0[h], lp = l0[h];
+        if (p0 > 0) ld_coherent2(a.part_ml + ((base + p) * G + h) * 2, mp, lp);
         w = __builtin_amdgcn_exp2f(mp - M[h]);
         L[h] = fmaf(lp, w, L[h]);
       }
@@ -491,23 +501,20 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int unit, i
       const int idx = lane + 64 * k;
       if (idx < G * CH) {
         const int h = idx / CH, c = idx % CH;
-        for (int q0 = 0; q0 < n; q0 += 4) {
-          float x[4][8];
+        for (int q0 = 0; q0 < n; q0 += kMergeFlight) {
+          float x[kMergeFlight][8];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            if (q0 + q < n) {
-              const float* src = a.part_acc + ((base + p0 + q0 + q) * G + h) * D + c * 2;
+          for (int q = 0; q < kMergeFlight; ++q) {
+            const int pq = p0 + (q0 + q < n ? q0 + q : n - 1);
+            const float* src = a.part_acc + ((base + pq) * G + h) * D + c * 2;
 #pragma unroll
-              for (int k = 0; k < 4; ++k) ld_coherent2(src + k * 32, x[q][2 * k], x[q][2 * k + 1]);
-            }
+            for (int k2 = 0; k2 < 4; ++k2) ld_coherent2(src + k2 * 32, x[q][2 * k2], x[q][2 * k2 + 1]);
           }
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            if (q0 + q < n) {
-              const float w = s_w[(q0 + q) * GP + h];
+          for (int q = 0; q < kMergeFlight; ++q) {
+            const float w = s_w[(q0 + q) * GP + h];   // 0 past the chunk's last partition
 #pragma unroll
-              for (int d = 0; d < 8; ++d) o[k][d] = fmaf(x[q][d], w, o[k][d]);
-            }
+            for (int d = 0; d < 8; ++d) o[k][d] = fmaf(x[q][d], w, o[k][d]);
           }
         }
       }
@@ -895,33 +902,62 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
 #endif
   int unit, part;
   if (a.num_seqs <= kInlineSchedMax) {
-    // Small batch: every workgroup derives the work list itself. Lane i holds
-    // sequence i's partition count; its rank (more partitions first, then
-    // index) and the item offset come from one pass over the lanes.
+    // Small batch: every workgroup derives its item from seq_lens alone, in
+    // longest-processing-time order, with scalar loops over ballots:
+    //   A. the full partitions (PS tokens) of every sequence but its last,
+    //      level by level (partition 0 of every unit, then partition 1, ...);
+    //   B. the last partition of every sequence (PS tokens or fewer; an empty
+    //      context has one item that writes zeros), longest first, in 16-token
+    //      buckets.
+    // Items past the resident capacity of the GPU start as earlier ones end,
+    // so the ones dispatched last are the shortest.
     const int lane = threadIdx.x;
     const int cap = a.max_bps * a.block_size;
-    int np = 0;
-    if (lane < a.num_seqs) {
+    const int kvh = a.num_kv_heads;
+    const bool valid = lane < a.num_seqs;
+    int full = 0, bucket = 0;   // full partitions before the last; last one's length in 16s
+    if (valid) {
       int c = a.seq_lens[lane];
       c = c < cap ? c : cap;
-      np = c <= 0 ? 1 : (c + a.partition - 1) / a.partition;
+      if (c > 0) {
+        full = (c - 1) / a.partition;
+        bucket = (c - full * a.partition + 15) >> 4;
+      }
     }
-    int off = 0;
-    for (int jj = 0; jj < a.num_seqs; ++jj) {
-      const int nj = __builtin_amdgcn_readlane(np, jj);
-      if (nj > np || (nj == np && jj < lane)) off += nj;
+    // sequence = the k-th set bit of m
+    auto nth = [&](uint64_t m, int k) -> int {
+      const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+      return __builtin_ctzll(__ballot(((m >> lane) & 1) && rank == k));
+    };
+    int id = blockIdx.x, seq = -1;
+    part = 0;
+    for (int p = 0;; ++p) {
+      const uint64_t m = __ballot(full > p);
+      if (m == 0) break;
+      const int c = __popcll(m) * kvh;
+      if (id < c) {
+        seq = nth(m, id / kvh);
+        unit = seq * kvh + id % kvh;
+        part = p;
+        break;
+      }
+      id -= c;
     }
-    off *= a.num_kv_heads;
-    const int id = blockIdx.x;
-    const bool mine = lane < a.num_seqs && id >= off && id < off + a.num_kv_heads * np;
-    const uint64_t ballot = __ballot(mine);
-    if (ballot == 0) return;   // past the last item
-    const int owner = __builtin_ctzll(ballot);
-    const int o = __builtin_amdgcn_readlane(off, owner);
-    const int n = __builtin_amdgcn_readlane(np, owner);
-    const int kh = (id - o) / n;
-    unit = owner * a.num_kv_heads + kh;
-    part = id - o - kh * n;
+    if (seq < 0) {
+      for (int b = a.partition >> 4; b >= 0; --b) {
+        const uint64_t m = __ballot(valid && bucket == b);
+        const int c = __popcll(m) * kvh;
+        if (id < c) {
+          seq = nth(m, id / kvh);
+          unit = seq * kvh + id % kvh;
+          part = __builtin_amdgcn_readlane(full, seq);
+          break;
+        }
+        id -= c;
+      }
+      if (seq < 0) return;   // past the last item
+    }
   } else {
     if ((int)blockIdx.x >= a.sched[1]) return;
     const int2 it = a.items[blockIdx.x];
