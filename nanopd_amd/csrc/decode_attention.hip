@@ -38,9 +38,6 @@ constexpr int kStep = 16;            // tokens per step
 #ifndef NPD_DECODE_NT
 #define NPD_DECODE_NT 1
 #endif
-#ifndef NPD_DECODE_PRIO
-#define NPD_DECODE_PRIO 1
-#endif
 #ifndef NPD_DECODE_PV_DOT2
 #define NPD_DECODE_PV_DOT2 1
 #endif
@@ -442,7 +439,8 @@ using npd::st_coherent2;
 // Merge of one (sequence, kv-head) by a single wave (fast path, D = 128), the
 // same log-sum-exp merge as merge_unit but latency-bound work done in parallel:
 //   A: lane p loads (m, l) of partition p for every head; a wave reduction
-//      gives M (partitions past 64 are read in a second loop);
+//      gives M (partitions past 64 are read in a second loop). The first
+//      batch of partial rows is requested at the same time;
 //   B: per chunk of 64 partitions, the weights 2^(m_p - M) go to LDS (0 past
 //      the last partition) and each lane accumulates its (head, 8-dim chunk)
 //      with kMergeFlight partitions of loads in flight. The loads are
@@ -455,6 +453,22 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int unit, i
   constexpr int D = 128, GP = pow2ceil(G), CH = D / 8;
   constexpr int OWN = (G * CH + 63) / 64;   // (head, chunk) pairs per lane
   const int64_t base = (int64_t)unit * a.max_parts;
+  // the first batch of partial rows of the lane's first (head, chunk) pair is
+  // requested together with the (m, l) values: it does not depend on them
+  const int n0 = nparts < 64 ? nparts : 64;
+  const bool pair0 = lane < G * CH;
+  const int h0 = pair0 ? lane / CH : 0, c0 = lane % CH;
+  float x[kMergeFlight][8];
+  auto load_batch = [&](int p0, int n, int q0, int h, int c) {
+#pragma unroll
+    for (int q = 0; q < kMergeFlight; ++q) {
+      const int pq = p0 + (q0 + q < n ? q0 + q : n - 1);
+      const float* src = a.part_acc + ((base + pq) * G + h) * D + c * 2;
+#pragma unroll
+      for (int k2 = 0; k2 < 4; ++k2) ld_coherent2(src + k2 * 32, x[q][2 * k2], x[q][2 * k2 + 1]);
+    }
+  };
+  load_batch(0, n0, 0, h0, c0);
   float M[G], L[G], m0[G], l0[G];   // m0, l0: partition `lane`
 #pragma unroll
   for (int h = 0; h < G; ++h) { m0[h] = -INFINITY; l0[h] = 0.f; }
@@ -502,14 +516,7 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int unit, i
       if (idx < G * CH) {
         const int h = idx / CH, c = idx % CH;
         for (int q0 = 0; q0 < n; q0 += kMergeFlight) {
-          float x[kMergeFlight][8];
-#pragma unroll
-          for (int q = 0; q < kMergeFlight; ++q) {
-            const int pq = p0 + (q0 + q < n ? q0 + q : n - 1);
-            const float* src = a.part_acc + ((base + pq) * G + h) * D + c * 2;
-#pragma unroll
-            for (int k2 = 0; k2 < 4; ++k2) ld_coherent2(src + k2 * 32, x[q][2 * k2], x[q][2 * k2 + 1]);
-          }
+          if (p0 > 0 || k > 0 || q0 > 0) load_batch(p0, n, q0, h, c);
 #pragma unroll
           for (int q = 0; q < kMergeFlight; ++q) {
             const float w = s_w[(q0 + q) * GP + h];   // 0 past the chunk's last partition
@@ -673,16 +680,6 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
       }
     };
     int st0 = 0;
-#if NPD_DECODE_PRIO
-    // Issue priority falls as the wave advances (3, 2 in pass 1; 1, 0 in
-    // pass 3): a SIMD's arbiter otherwise favours its oldest wave, so the
-    // youngest waves lag and the call ends with a few of them alone, each with
-    // only its own loads in flight.
-    __builtin_amdgcn_s_setprio(3);
-    const int half = (nsteps / (2 * NBUF)) * NBUF;
-    for (; st0 < half; st0 += NBUF) round(st0);
-    __builtin_amdgcn_s_setprio(2);
-#endif
     for (; st0 + NBUF < nsteps; st0 += NBUF) round(st0);
 #pragma unroll
     for (int b = 0; b < NBUF; ++b) score_step(kb[b], st0 + b);
@@ -816,12 +813,6 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
       }
     };
     int st0 = 0;
-#if NPD_DECODE_PRIO
-    __builtin_amdgcn_s_setprio(1);
-    const int half = (nsteps / (2 * NBUF)) * NBUF;
-    for (; st0 < half; st0 += NBUF) round(st0);
-    __builtin_amdgcn_s_setprio(0);
-#endif
     for (; st0 + NBUF < nsteps; st0 += NBUF) round(st0);
 #pragma unroll
     for (int b = 0; b < NBUF; ++b) pv_step(vb[b], st0 + b);
