@@ -14,6 +14,10 @@ int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 // Maps a failed HIP call (or a failed launch) to NPD_E_LAUNCH.
 int check_launch(const char* what);
 
+// Compute units of the calling thread's current device (queried once per
+// device, 256 if the query fails).
+int device_cus();
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }

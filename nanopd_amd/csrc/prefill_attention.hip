@@ -100,6 +100,7 @@ struct PrefillArgs {
   int num_seqs, num_kv_heads, group, hgroups, block_size, bs_shift, num_blocks, max_bps;
   int tiles_max, subtiles, splits_max;   // subtiles: 32-row subtiles per sequence
   int ks_steps, num_groups;              // key steps per split; (split, seq, kv-head) groups
+  int num_cus;                           // compute units of the device (work-list sizing)
   float scale_log2;
   int64_t q_stride_token, q_stride_head, out_stride_token, out_stride_head;
 };
@@ -163,23 +164,111 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   const int wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, r = lane & 15;
 
-  // Unit = (split j, sequence, kv-head; tile t, head group). The units of one
-  // (j, s, kv-head) read the same K/V key range: they form a group that runs
-  // on one XCD at the same time (workgroups go to XCDs round-robin by
-  // blockIdx, so the group's blockIdx values are 8 apart and consecutive in
-  // that XCD's order), so K/V tiles come from that XCD's L2 after the first
-  // read. Within a group the last tile (the most keys) comes first.
-  const int gunits = a.tiles_max * a.hgroups;
-  const int xcd = blockIdx.x & 7, p = blockIdx.x >> 3;
-  const int gi = (p / gunits) * 8 + xcd;
-  if (gi >= a.num_groups) return;
-  const int u = p - (p / gunits) * gunits;
-  const int t = a.tiles_max - 1 - u / a.hgroups;
-  const int hg = u - (u / a.hgroups) * a.hgroups;
-  const int kh = gi % a.num_kv_heads;
-  const int js = gi / a.num_kv_heads;
-  const int s = js % a.num_seqs;
-  const int j = js / a.num_seqs;
+  int s, t, j, kh, hg, ks = a.ks_steps;
+  if (a.num_seqs * a.tiles_max <= 64) {
+    // Work list in longest-processing-time order, derived by every wave from
+    // the sequence lengths. Lane i stands for (sequence i / tiles_max, tile
+    // i % tiles_max) with n_i key steps. The split length ks is chosen so that
+    // the longest key range falls into equal parts no shorter than the
+    // average work per compute unit (and no shorter than the host's split,
+    // which sized the workspace). Items: first every full split (ks steps),
+    // level by level, then the last split of every tile, longest first. The
+    // kv-head is the fastest-varying index and every count is a multiple of
+    // the kv-head count, so with 8 kv-heads each XCD (workgroups go to XCDs
+    // round-robin by blockIdx) serves one kv-head and its K/V stays in that
+    // XCD's L2.
+    const int ls = lane / a.tiles_max, lt = lane - ls * a.tiles_max;
+    bool valid = ls < a.num_seqs;
+    int n = 0;
+    if (valid) {
+      const int c0 = a.cu_seqlens_q[ls];
+      const int ql = a.cu_seqlens_q[ls + 1] - c0;
+      valid = lt * TR < ql;
+      if (valid) {
+        const int cp = a.max_bps * a.block_size;
+        int cx = a.context_lens[ls];
+        cx = cx < 0 ? 0 : (cx < cp ? cx : cp);
+        const int rw = (ql - lt * TR) < TR ? (ql - lt * TR) : TR;
+        int nk = cx - ql + lt * TR + rw;
+        nk = nk < 0 ? 0 : nk;
+        n = (nk + kKT - 1) / kKT;
+      }
+    }
+    const int per_item = a.num_kv_heads * a.hgroups;   // workgroups per (sequence, tile, split)
+    int tot = n, nmax = n;
+#pragma unroll
+    for (int x = 1; x < 64; x <<= 1) {
+      tot += __shfl_xor(tot, x, 64);
+      nmax = max(nmax, __shfl_xor(nmax, x, 64));
+    }
+    const int avg = (int)(((int64_t)tot * per_item + a.num_cus - 1) / a.num_cus);
+    int parts = avg > 0 ? nmax / avg : 1;
+    parts = parts < 1 ? 1 : parts;
+    const int ksd = __builtin_amdgcn_readfirstlane((nmax + parts - 1) / parts);
+    ks = ksd > ks ? ksd : ks;
+    int nsp = (n + ks - 1) / ks;
+    nsp = nsp < 1 ? 1 : (nsp > a.splits_max ? a.splits_max : nsp);
+    const int full = valid ? nsp - 1 : 0;
+    // steps of the last split, in buckets 0 .. ks (a split count capped at
+    // splits_max leaves a longer last split: it goes in the top bucket)
+    int last = valid ? n - (nsp - 1) * ks : -1;
+    last = last > ks ? ks : last;
+    auto nth = [&](uint64_t m, int k) -> int {   // lane of the k-th set bit of m
+      const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+      return __builtin_ctzll(__ballot(((m >> lane) & 1) && rank == k));
+    };
+    int id = blockIdx.x, sel = -1;
+    j = 0;
+    for (int lvl = 0;; ++lvl) {
+      const uint64_t m = __ballot(full > lvl);
+      if (m == 0) break;
+      const int c = __popcll(m) * per_item;
+      if (id < c) {
+        sel = nth(m, id / per_item);
+        j = lvl;
+        break;
+      }
+      id -= c;
+    }
+    if (sel < 0) {
+      for (int b = ks; b >= 0; --b) {
+        const uint64_t m = __ballot(last == b);
+        const int c = __popcll(m) * per_item;
+        if (id < c) {
+          sel = nth(m, id / per_item);
+          j = __builtin_amdgcn_readlane(full, sel);
+          break;
+        }
+        id -= c;
+      }
+      if (sel < 0) return;   // past the last item
+    }
+    const int rem = id % per_item;
+    kh = rem % a.num_kv_heads;
+    hg = rem / a.num_kv_heads;
+    s = __builtin_amdgcn_readfirstlane(sel / a.tiles_max);
+    t = __builtin_amdgcn_readfirstlane(sel - s * a.tiles_max);
+    j = __builtin_amdgcn_readfirstlane(j);
+  } else {
+    // Unit = (split j, sequence, kv-head; tile t, head group). The units of
+    // one (j, s, kv-head) read the same K/V key range: they form a group that
+    // runs on one XCD at the same time (workgroups go to XCDs round-robin by
+    // blockIdx, so the group's blockIdx values are 8 apart and consecutive in
+    // that XCD's order), so K/V tiles come from that XCD's L2 after the first
+    // read. Within a group the last tile (the most keys) comes first.
+    const int gunits = a.tiles_max * a.hgroups;
+    const int xcd = blockIdx.x & 7, p = blockIdx.x >> 3;
+    const int gi = (p / gunits) * 8 + xcd;
+    if (gi >= a.num_groups) return;
+    const int u = p - (p / gunits) * gunits;
+    t = a.tiles_max - 1 - u / a.hgroups;
+    hg = u - (u / a.hgroups) * a.hgroups;
+    kh = gi % a.num_kv_heads;
+    const int js = gi / a.num_kv_heads;
+    s = js % a.num_seqs;
+    j = js / a.num_seqs;
+  }
 
   const int q0 = a.cu_seqlens_q[s];
   const int qlen = a.cu_seqlens_q[s + 1] - q0;
@@ -195,11 +284,11 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   const int nsteps = (nkeys + kKT - 1) / kKT;
   // split j covers steps [j*ks, (j+1)*ks) -- the same keys for every tile of
   // the sequence -- the last split runs to the end of the tile's range
-  int nsp = (nsteps + a.ks_steps - 1) / a.ks_steps;
+  int nsp = (nsteps + ks - 1) / ks;
   nsp = nsp < 1 ? 1 : (nsp > a.splits_max ? a.splits_max : nsp);
   if (j >= nsp) return;
-  const int st0 = j * a.ks_steps;
-  const int st1 = j == nsp - 1 ? nsteps : st0 + a.ks_steps;
+  const int st0 = j * ks;
+  const int st1 = j == nsp - 1 ? nsteps : st0 + ks;
 
   // wave -> (head of the group, row tile, half of the row tile)
   const int pair = wave >> 1, half = wave & 1;
@@ -683,6 +772,7 @@ extern "C" int npd_paged_prefill_attention(
   a.splits_max = L.splits;
   a.ks_steps = L.ks_steps;
   a.num_groups = (int)groups;
+  a.num_cus = device_cus();
   a.scale_log2 = scale * kLog2e;
   a.q_stride_token = q_stride_token;
   a.q_stride_head = q_stride_head;
