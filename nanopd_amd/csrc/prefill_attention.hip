@@ -165,6 +165,8 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   const int g = lane >> 4, r = lane & 15;
 
   int s, t, j, kh, hg, ks = a.ks_steps;
+  int q0, qlen, ctx;   // the sequence's first query row, chunk length, context
+  const int cap = a.max_bps * a.block_size;
   if (a.num_seqs * a.tiles_max <= 64) {
     // Work list in longest-processing-time order, derived by every wave from
     // the sequence lengths. Lane i stands for (sequence i / tiles_max, tile
@@ -179,15 +181,14 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     // XCD's L2.
     const int ls = lane / a.tiles_max, lt = lane - ls * a.tiles_max;
     bool valid = ls < a.num_seqs;
-    int n = 0;
+    int n = 0, c0 = 0, ql = 0, cx = 0;
     if (valid) {
-      const int c0 = a.cu_seqlens_q[ls];
-      const int ql = a.cu_seqlens_q[ls + 1] - c0;
+      c0 = a.cu_seqlens_q[ls];
+      ql = a.cu_seqlens_q[ls + 1] - c0;
       valid = lt * TR < ql;
       if (valid) {
-        const int cp = a.max_bps * a.block_size;
-        int cx = a.context_lens[ls];
-        cx = cx < 0 ? 0 : (cx < cp ? cx : cp);
+        cx = a.context_lens[ls];
+        cx = cx < 0 ? 0 : (cx < cap ? cx : cap);
         const int rw = (ql - lt * TR) < TR ? (ql - lt * TR) : TR;
         int nk = cx - ql + lt * TR + rw;
         nk = nk < 0 ? 0 : nk;
@@ -250,6 +251,9 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     s = __builtin_amdgcn_readfirstlane(sel / a.tiles_max);
     t = __builtin_amdgcn_readfirstlane(sel - s * a.tiles_max);
     j = __builtin_amdgcn_readfirstlane(j);
+    q0 = __builtin_amdgcn_readlane(c0, sel);
+    qlen = __builtin_amdgcn_readlane(ql, sel);
+    ctx = __builtin_amdgcn_readlane(cx, sel);
   } else {
     // Unit = (split j, sequence, kv-head; tile t, head group). The units of
     // one (j, s, kv-head) read the same K/V key range: they form a group that
@@ -268,14 +272,13 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     const int js = gi / a.num_kv_heads;
     s = js % a.num_seqs;
     j = js / a.num_seqs;
+    q0 = a.cu_seqlens_q[s];
+    qlen = a.cu_seqlens_q[s + 1] - q0;
+    if (t * TR >= qlen) return;
+    ctx = a.context_lens[s];
+    ctx = ctx < 0 ? 0 : (ctx < cap ? ctx : cap);
   }
 
-  const int q0 = a.cu_seqlens_q[s];
-  const int qlen = a.cu_seqlens_q[s + 1] - q0;
-  if (t * TR >= qlen) return;
-  const int cap = a.max_bps * a.block_size;
-  int ctx = a.context_lens[s];
-  ctx = ctx < 0 ? 0 : (ctx < cap ? ctx : cap);
   const int prefix = ctx - qlen;                       // position of query row 0
   const int rows = (qlen - t * TR) < TR ? (qlen - t * TR) : TR;
   const int pos0 = prefix + t * TR;                    // position of the tile's first row
