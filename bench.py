@@ -286,6 +286,7 @@ def bench_e2e(args, dev) -> int:
     lognormal prompt/output lengths (median 512 / 128, sigma 1, clipped to
     [32, 8192] / [8, 1024]) arriving as a Poisson process at 8 req/s."""
     from nanopd_amd.engine import Engine, Request, make_requests, serve
+    from nanopd_amd.graphs import DecodeGraphs
     from nanopd_amd.qwen3 import QWEN3_8B, PagedQwen3
     t0 = time.perf_counter()
     model = PagedQwen3(QWEN3_8B, num_blocks=args.kv_blocks, block_size=16, device=dev, seed=0)
@@ -297,7 +298,16 @@ def bench_e2e(args, dev) -> int:
         warm.add(Request(r.rid, r.prompt, r.max_new_tokens))
     warm.drain()
     torch.cuda.synchronize()
-    eng = Engine(model, max_batch_size=16, budget=1024, chunk=512)
+    graphs, t_graphs = None, 0.0
+    if not args.no_graphs:
+        # decode-only steps replay HIP graphs; every (batch, table width)
+        # bucket is captured before the timed run
+        t0 = time.perf_counter()
+        graphs = DecodeGraphs(model, max_width=(8192 + 1024 + 15) // 16)
+        graphs.capture_all()
+        torch.cuda.synchronize()
+        t_graphs = time.perf_counter() - t0
+    eng = Engine(model, max_batch_size=16, budget=1024, chunk=512, graphs=graphs)
     reqs = make_requests(args.requests, seed=5)
     res = serve(eng, reqs)
     print(json.dumps({
@@ -315,9 +325,10 @@ def bench_e2e(args, dev) -> int:
         "data": "synthetic (random-init weights N(0, 0.02), random prompt token ids)",
         "config": {"workload": "cfg5_qwen3_8b_collocated", "requests": args.requests,
                    "arrival_rate": 8.0, "chunk": 512, "max_running": 16, "block_size": 16,
-                   "kv_blocks": args.kv_blocks, "params": QWEN3_8B.num_params},
+                   "kv_blocks": args.kv_blocks, "params": QWEN3_8B.num_params,
+                   "decode_steps": "hip graphs" if graphs is not None else "eager"},
         "detail": {**{k: (round(v, 4) if isinstance(v, float) else v) for k, v in res.items()},
-                   "init_s": round(t_init, 1)},
+                   "init_s": round(t_init, 1), "graph_capture_s": round(t_graphs, 1)},
     }), flush=True)
     return 0
 
@@ -394,6 +405,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--requests", type=int, default=256, help="e2e: number of requests")
     ap.add_argument("--kv-blocks", type=int, default=12288, help="e2e: KV pool blocks of 16")
+    ap.add_argument("--no-graphs", action="store_true",
+                    help="e2e: launch decode-only steps kernel by kernel instead of from HIP graphs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "

@@ -17,7 +17,9 @@ Scheduling rules kept from the reference:
 Differences, on purpose:
 - the step's metadata (cu_seqlens, slot_mapping, block tables, positions) is
   packed once per step on the GPU (pack_metadata), not rebuilt per layer;
-- copy-on-write pairs from append_slot are copied on the GPU.
+- copy-on-write pairs from append_slot are copied on the GPU;
+- with `graphs`, decode-only steps replay a captured HIP graph of the whole
+  model step (nanopd_amd/graphs.py) instead of launching it kernel by kernel.
 """
 from __future__ import annotations
 
@@ -31,6 +33,7 @@ import torch
 
 from . import paged_kernels as pk
 from .block_manager import BlockSpaceManager
+from .graphs import DecodeGraphs
 from .qwen3 import PagedQwen3, StepBatch
 
 
@@ -121,8 +124,9 @@ class Scheduler:
 
 class Engine:
     def __init__(self, model: PagedQwen3, max_batch_size: int = 16, budget: int = 1024,
-                 chunk: int = 512, clock=None):
+                 chunk: int = 512, clock=None, graphs: Optional[DecodeGraphs] = None):
         self.model = model
+        self.graphs = graphs
         self.blocks = BlockSpaceManager(model.block_size, model.num_blocks)
         self.sched = Scheduler(self.blocks, max_batch_size, budget, chunk)
         self.device = model.device
@@ -140,6 +144,12 @@ class Engine:
         plan = self.sched.schedule(now)
         if plan.prefill is None and not plan.decodes:
             return None
+        return plan, self._pack(*self._rows(plan))
+
+    def _rows(self, plan: StepPlan):
+        """The step's sequences (q_len, ctx_before, block table), token ids and
+        sample rows; makes room for every decode token (append_slot) and runs
+        the copy-on-write copies."""
         seqs, ids, sample_rows = [], [], []
         tp = 0
         if plan.prefill is not None:
@@ -160,6 +170,9 @@ class Engine:
             ids.append(s.output[-1])
             sample_rows.append(tp + i)
         self.model.copy_blocks(cow)
+        return plan, seqs, ids, sample_rows, tp
+
+    def _pack(self, plan: StepPlan, seqs: list, ids: list, sample_rows: list, tp: int) -> StepBatch:
         mb = max(len(t) for _, _, t in seqs)
         meta = pk.pack_metadata(seqs, self.model.block_size, self.device, max_blocks_per_seq=mb)
         batch = StepBatch(
@@ -168,7 +181,7 @@ class Engine:
             num_prefill_tokens=tp,
             sample_rows=torch.tensor(sample_rows, dtype=torch.int64).to(self.device, non_blocking=True),
             max_prefill_q=tp)
-        return plan, batch
+        return batch
 
     def commit(self, plan: StepPlan, tokens: list, now: float = 0.0) -> None:
         """Applies a step's sampled tokens (one per sample row, in order)."""
@@ -194,10 +207,17 @@ class Engine:
 
     def step(self, now: float = 0.0) -> int:
         """One scheduled step, greedy sampling; returns the tokens sampled."""
-        prep = self.prepare(now)
-        if prep is None:
+        plan = self.sched.schedule(now)
+        if plan.prefill is None and not plan.decodes:
             return 0
-        plan, batch = prep
+        rows = self._rows(plan)
+        if self.graphs is not None and plan.prefill is None:
+            _, seqs, ids, _, _ = rows
+            tokens = self.graphs.decode([c for _, c, _ in seqs], [t for _, _, t in seqs], ids)
+            if tokens is not None:
+                self.commit(plan, tokens, now)
+                return len(tokens)
+        batch = self._pack(*rows)
         tokens = []
         if batch.sample_rows.numel():
             tokens = self.model.forward(batch).argmax(dim=-1).tolist()

@@ -70,8 +70,9 @@ class StepBatch:
     meta: pk.BatchMetadata
     num_prefill_seqs: int
     num_prefill_tokens: int
-    sample_rows: torch.Tensor        # int64 [R]
+    sample_rows: Optional[torch.Tensor]   # int64 [R]; None: every row
     max_prefill_q: int = 0           # longest prefill chunk (grid bound)
+    decode_workspace: Optional[torch.Tensor] = None   # explicit decode-attention workspace
 
 
 # attention(layer, q [T,H,D], k_cache, v_cache, batch, out [T,H,D]) -> None
@@ -169,12 +170,13 @@ class PagedQwen3:
         if T > tp:
             pk.paged_attention_forward(out[tp:], q[tp:], kc, vc, m.block_tables[npf:],
                                        m.seq_lens[npf:], self.scale, self.block_size,
-                                       m.max_blocks_per_seq)
+                                       m.max_blocks_per_seq, workspace=b.decode_workspace)
 
     # -- forward -------------------------------------------------------------
     @torch.no_grad()
     def forward(self, b: StepBatch) -> torch.Tensor:
-        """Runs one packed step; returns fp32 logits [R, vocab] of b.sample_rows."""
+        """Runs one packed step; returns fp32 logits [R, vocab] of b.sample_rows
+        (of every row when it is None)."""
         cfg = self.cfg
         H, KV, D, E = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.hidden
         T = b.input_ids.numel()
@@ -195,7 +197,9 @@ class PagedQwen3:
             h = F.rms_norm(x, (E,), w["post_norm"], cfg.rms_eps)
             gu = h @ w["gate_up"].t()
             x = x + (F.silu(gu[:, : cfg.intermediate]) * gu[:, cfg.intermediate:]) @ w["down"].t()
-        xs = F.rms_norm(x.index_select(0, b.sample_rows), (E,), self.final_norm, cfg.rms_eps)
+        if b.sample_rows is not None:
+            x = x.index_select(0, b.sample_rows)
+        xs = F.rms_norm(x, (E,), self.final_norm, cfg.rms_eps)
         return (xs @ self.lm_head.t()).float()
 
     def copy_blocks(self, pairs) -> None:
