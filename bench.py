@@ -358,6 +358,59 @@ def bench_copy(args, dev) -> int:
     return 0
 
 
+def bench_transfer(args, dev) -> int:
+    """KV transfer pack / unpack at configuration 5's shape: one 4096-token
+    sequence (256 blocks of 16) of random-init Qwen3-8B (36 layers, 8 kv heads
+    of 128, bf16), gathered from a shuffled pool into the transfer layout and
+    scattered back into another pool at another block list. Roofline: HBM,
+    every byte read once and written once."""
+    from nanopd_amd import paged_kernels as pk
+    L, N, kvh, bs, D, n = 36, 1024, 8, 16, 128, 256
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    k = torch.randn((L, N, kvh, bs, D), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn((L, N, kvh, bs, D), generator=g, device=dev).to(torch.bfloat16)
+    k2, v2 = torch.empty_like(k), torch.empty_like(v)
+    src = torch.randperm(N, generator=torch.Generator().manual_seed(1))[:n].to(torch.int32).to(dev)
+    dst = torch.randperm(N, generator=torch.Generator().manual_seed(2))[:n].to(torch.int32).to(dev)
+    wk = torch.empty((L, n, kvh, bs, D), dtype=torch.bfloat16, device=dev)
+    wv = torch.empty_like(wk)
+
+    def step():
+        pk.extract_kv(k, v, src, wk, wv)
+        pk.load_kv(k2, v2, dst, wk, wv)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    gather_ms = _launch_avg_ms(lambda: pk.extract_kv(k, v, src, wk, wv), args.steps)
+    scatter_ms = _launch_avg_ms(lambda: pk.load_kv(k2, v2, dst, wk, wv), args.steps)
+    per_op = 2 * 2 * L * n * kvh * bs * D * 2      # K + V, read + write
+    gbs = per_op / (gather_ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "KV transfer pack + unpack HBM GB/s (read + write)",
+        "value": round(2 * per_op / (ms * 1e-3) / 1e9, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) pool, shuffled block lists)",
+        "config": {"workload": "transfer_qwen3_8b_4096_tokens", "layers": L, "blocks": n,
+                   "num_kv_heads": kvh, "block_size": bs, "head_dim": D,
+                   "step": "extract_kv (gather into the wire layout) + load_kv (scatter)"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": _profiled_traffic("kv_blocks_kernel/transfer_qwen3_8b_4096_tokens")},
+        "detail": {"gather_us": round(gather_ms * 1e3, 2), "scatter_us": round(scatter_ms * 1e3, 2),
+                   "bytes_per_op": per_op,
+                   "scatter_gbs": round(per_op / (scatter_ms * 1e-3) / 1e9, 1)},
+    }), flush=True)
+    return 0
+
+
 def emit_prefill(args, w) -> int:
     from nanopd_amd import paged_kernels as pk
     pk.paged_kv_store_slots(w.k_cache, w.v_cache, w.new_k, w.new_v, w.slot_mapping)
@@ -395,11 +448,12 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=["decode", "long", "prefill", "copy", "e2e"],
+    ap.add_argument("--workload", choices=["decode", "long", "prefill", "copy", "e2e", "transfer"],
                     default="decode",
                     help="decode: config 2 (default); long: config 4 (8 seqs, 8k-32k); "
                          "prefill: config 3 (4 chunks of 512 on paged prefixes + 48 decodes); "
                          "e2e: config 5 (Qwen3-8B collocated serving, tok/s); "
+                         "transfer: KV transfer pack + unpack of a 4096-token Qwen3-8B sequence; "
                          "copy: a plain 256 MiB device copy, the calibration kernel for "
                          "the FETCH_SIZE / WRITE_SIZE counters")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -422,6 +476,8 @@ def main() -> int:
         return bench_copy(args, dev)
     if args.workload == "e2e":
         return bench_e2e(args, dev)
+    if args.workload == "transfer":
+        return bench_transfer(args, dev)
     if args.workload == "prefill":
         return emit_prefill(args, workloads.config3(dev))
     if args.workload == "decode":

@@ -182,6 +182,33 @@ int npd_copy_blocks(void* k_cache, void* v_cache, const int32_t* pairs,
                     int64_t block_elems, int32_t dtype, void* stream);
 
 /*
+ * Block-list pack of a multi-layer KV pool into the transfer ("wire") layout,
+ * replacing the per-block copies of extract_kv_to_pinned
+ * (nanoPD/workers/kv_transfer.py:45-53):
+ *   wire_k[l, i, :] = k_cache[l, block_ids[i], :]   (same for v)
+ * for l < num_layers, i < num_ids. Pool: [num_layers, num_blocks,
+ * block_bytes] bytes per tensor (a block is num_kv_heads * block_size *
+ * head_dim elements of any type); wire: [num_layers, num_ids, block_bytes].
+ * An id outside [0, num_blocks) gives zero bytes in the wire.
+ * block_bytes a multiple of 16, 16-byte aligned pointers.
+ */
+int npd_kv_gather_blocks(const void* k_cache, const void* v_cache, int64_t num_layers,
+                         int64_t num_blocks, int64_t block_bytes,
+                         const int32_t* block_ids, int64_t num_ids,
+                         void* wire_k, void* wire_v, void* stream);
+
+/*
+ * The inverse, replacing load_kv_from_pinned (kv_transfer.py:56-69):
+ *   k_cache[l, block_ids[i], :] = wire_k[l, i, :]   (same for v).
+ * Ids outside [0, num_blocks) are skipped. Same layouts and limits as
+ * npd_kv_gather_blocks.
+ */
+int npd_kv_scatter_blocks(void* k_cache, void* v_cache, int64_t num_layers,
+                          int64_t num_blocks, int64_t block_bytes,
+                          const int32_t* block_ids, int64_t num_ids,
+                          const void* wire_k, const void* wire_v, void* stream);
+
+/*
  * Fused attention prologue of a Qwen3-style layer (replaces the per-layer
  * q_norm / k_norm, rotary embedding, K/V transpose copies and paged_kv_store
  * calls of nanoPD/engine/model_runner.py:97-115, :142-146, :189-192).

@@ -36,6 +36,8 @@ SIGNATURES = {
                                                    _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F,
                                                    _I64, _I64, _I64, _I64, _P, _I64, _I32, _P]),
     "npd_copy_blocks": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _I64, _I32, _P]),
+    "npd_kv_gather_blocks": (ctypes.c_int, [_P, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P]),
+    "npd_kv_scatter_blocks": (ctypes.c_int, [_P, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P]),
     "npd_qk_norm_rope_store": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
                                               _I64, _I64, _I64, _I64, _I64, _I64, _F, _I32, _P]),
     "npd_pack_metadata": (ctypes.c_int, [_P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P,

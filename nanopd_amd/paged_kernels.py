@@ -345,6 +345,71 @@ def copy_blocks(k_cache: torch.Tensor, v_cache: torch.Tensor, block_pairs) -> No
               k_cache.size(0), per_block, code, _stream(dev))
 
 
+def _block_list(block_table, dev: torch.device) -> torch.Tensor:
+    if isinstance(block_table, torch.Tensor):
+        _int32(block_table, "block_table")
+        _check(block_table.dim() == 1 and block_table.is_contiguous(),
+               "block_table must be a contiguous 1-D int32 tensor")
+        _same_device(dev, block_table)
+        return block_table
+    return torch.tensor(list(block_table), dtype=torch.int32).to(dev)
+
+
+def _pool_checks(k_cache: torch.Tensor, v_cache: torch.Tensor, what: str) -> None:
+    _check(k_cache.is_cuda, f"{what}: caches must be on CUDA")
+    _check(k_cache.dim() == 5 and v_cache.shape == k_cache.shape,
+           f"{what}: caches must be [num_layers, num_blocks, num_kv_heads, block_size, head_dim]")
+    _check(k_cache.dtype == v_cache.dtype, f"{what}: k_cache and v_cache dtypes differ")
+    _check(k_cache.is_contiguous() and v_cache.is_contiguous(), f"{what}: caches must be contiguous")
+
+
+def extract_kv(k_cache: torch.Tensor, v_cache: torch.Tensor, block_table,
+               out_k: torch.Tensor | None = None, out_v: torch.Tensor | None = None):
+    """Gathers the blocks of ``block_table`` from every layer of the pool into
+    the transfer layout ``[num_layers, len(block_table), num_kv_heads,
+    block_size, head_dim]``, one launch (reference: extract_kv_to_pinned,
+    nanoPD/workers/kv_transfer.py:45-53, one copy per block). Caches are the
+    multi-layer pool ``[num_layers, num_blocks, kvh, bs, D]``. Returns
+    ``(wire_k, wire_v)``, allocated unless given; an id outside the pool gives
+    a zero block."""
+    _pool_checks(k_cache, v_cache, "extract_kv")
+    dev = k_cache.device
+    ids = _block_list(block_table, dev)
+    L, nb = k_cache.shape[:2]
+    shape = (L, ids.numel()) + tuple(k_cache.shape[2:])
+    if out_k is None:
+        out_k = torch.empty(shape, dtype=k_cache.dtype, device=dev)
+    if out_v is None:
+        out_v = torch.empty(shape, dtype=k_cache.dtype, device=dev)
+    for o in (out_k, out_v):
+        _check(tuple(o.shape) == shape and o.dtype == k_cache.dtype and o.is_contiguous(),
+               f"extract_kv: wire buffers must be contiguous {list(shape)} of the cache dtype")
+        _same_device(dev, o)
+    block_bytes = k_cache[0, 0].numel() * k_cache.element_size()
+    _lib.call("npd_kv_gather_blocks", k_cache.data_ptr(), v_cache.data_ptr(), L, nb, block_bytes,
+              ids.data_ptr(), ids.numel(), out_k.data_ptr(), out_v.data_ptr(), _stream(dev))
+    return out_k, out_v
+
+
+def load_kv(k_cache: torch.Tensor, v_cache: torch.Tensor, block_table, wire_k: torch.Tensor,
+            wire_v: torch.Tensor) -> None:
+    """Scatters a transfer buffer (see :func:`extract_kv`) into the pool at
+    ``block_table`` (reference: load_kv_from_pinned, kv_transfer.py:56-69).
+    Ids outside the pool are skipped."""
+    _pool_checks(k_cache, v_cache, "load_kv")
+    dev = k_cache.device
+    ids = _block_list(block_table, dev)
+    L, nb = k_cache.shape[:2]
+    shape = (L, ids.numel()) + tuple(k_cache.shape[2:])
+    for w in (wire_k, wire_v):
+        _check(tuple(w.shape) == shape and w.dtype == k_cache.dtype and w.is_contiguous(),
+               f"load_kv: wire buffers must be contiguous {list(shape)} of the cache dtype")
+        _same_device(dev, w)
+    block_bytes = k_cache[0, 0].numel() * k_cache.element_size()
+    _lib.call("npd_kv_scatter_blocks", k_cache.data_ptr(), v_cache.data_ptr(), L, nb, block_bytes,
+              ids.data_ptr(), ids.numel(), wire_k.data_ptr(), wire_v.data_ptr(), _stream(dev))
+
+
 def qk_norm_rope_store(q_out: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                        qkv: torch.Tensor, slot_mapping: torch.Tensor, positions: torch.Tensor,
                        inv_freq: torch.Tensor, q_norm_weight: torch.Tensor,

@@ -100,6 +100,31 @@ def copy_blocks(k_cache: np.ndarray, v_cache: np.ndarray, pairs: Sequence[tuple[
             v_cache[dst] = v_cache[src]
 
 
+def extract_kv(k_pool: np.ndarray, v_pool: np.ndarray, ids: Sequence[int]):
+    """Transfer layout of a block list (nanoPD/workers/kv_transfer.py:45-53:
+    buf[:, i] = cache[:, bid]): pools [L, N, ...] -> wire [L, len(ids), ...].
+    An id outside the pool gives a zero block (the kernel's rule)."""
+    n = k_pool.shape[1]
+    out_k = np.zeros((k_pool.shape[0], len(ids)) + k_pool.shape[2:], dtype=k_pool.dtype)
+    out_v = np.zeros_like(out_k)
+    for i, b in enumerate(ids):
+        if 0 <= b < n:
+            out_k[:, i] = k_pool[:, b]
+            out_v[:, i] = v_pool[:, b]
+    return out_k, out_v
+
+
+def load_kv(k_pool: np.ndarray, v_pool: np.ndarray, ids: Sequence[int], wire_k: np.ndarray,
+            wire_v: np.ndarray) -> None:
+    """Inverse of extract_kv (kv_transfer.py:56-69: cache[:, bid] = buf[:, i]);
+    ids outside the pool are skipped."""
+    n = k_pool.shape[1]
+    for i, b in enumerate(ids):
+        if 0 <= b < n:
+            k_pool[:, b] = wire_k[:, i]
+            v_pool[:, b] = wire_v[:, i]
+
+
 # ---------------------------------------------------------------------------
 # Attention
 # ---------------------------------------------------------------------------

@@ -11,6 +11,9 @@ reference's Python is never imported or shipped; these are restatements:
   causal mask over the packed chunks, repeat_interleave, SDPA; chunk only).
 * ref_kv_store_loop -- the Python scatter loop of
   nanoPD/docs/en/03-cuda_kernels_en.md:69-78.
+* ref_extract_kv / ref_load_kv -- the per-block copies of extract_kv_to_pinned
+  and load_kv_from_pinned (nanoPD/workers/kv_transfer.py:45-69), into and out
+  of an ordinary (not pinned) buffer.
 """
 from __future__ import annotations
 
@@ -67,3 +70,22 @@ def ref_kv_store_loop(k_cache: torch.Tensor, v_cache: torch.Tensor, k_src: torch
         phys = int(block_tables[i, position // block_size])
         k_cache[phys, :, position % block_size, :] = k_src[:, i, :]
         v_cache[phys, :, position % block_size, :] = v_src[:, i, :]
+
+
+def ref_extract_kv(k_cache: torch.Tensor, v_cache: torch.Tensor, block_table) -> tuple:
+    """kv_transfer.py:45-53: buf.k[:, i].copy_(k_cache[:, bid]) per block."""
+    shape = (k_cache.size(0), len(block_table)) + tuple(k_cache.shape[2:])
+    bk = torch.empty(shape, dtype=k_cache.dtype)
+    bv = torch.empty(shape, dtype=v_cache.dtype)
+    for i, bid in enumerate(block_table):
+        bk[:, i].copy_(k_cache[:, bid])
+        bv[:, i].copy_(v_cache[:, bid])
+    return bk, bv
+
+
+def ref_load_kv(k_cache: torch.Tensor, v_cache: torch.Tensor, block_table, bk: torch.Tensor,
+                bv: torch.Tensor) -> None:
+    """kv_transfer.py:56-69: k_cache[:, bid].copy_(buf.k[:, i]) per block."""
+    for i, bid in enumerate(block_table):
+        k_cache[:, bid].copy_(bk[:, i])
+        v_cache[:, bid].copy_(bv[:, i])

@@ -82,6 +82,12 @@ def test_c_validation_paths_need_no_gpu():
                ctypes.c_float(0.1), 4096, 128, 4096, 128, None, 0, 1, None) == 0
     assert _rc("npd_copy_blocks", fake, fake, fake, 0, 10, 1024, 1, None) == 0
     assert _rc("npd_copy_blocks", fake, fake, fake, 3, 10, 1004, 1, None) == -3
+    # block-list gather / scatter: no-op, unaligned block size, null ids, too many layers
+    for fn in ("npd_kv_gather_blocks", "npd_kv_scatter_blocks"):
+        assert _rc(fn, fake, fake, 36, 100, 32768, fake, 0, fake, fake, None) == 0
+        assert _rc(fn, fake, fake, 36, 100, 32760, fake, 4, fake, fake, None) == -3
+        assert _rc(fn, fake, fake, 36, 100, 32768, None, 4, fake, fake, None) == -1
+        assert _rc(fn, fake, fake, 70000, 100, 32768, fake, 4, fake, fake, None) == -1
     assert _rc("npd_pack_metadata", fake, fake, 5000, 1, 1, 4, 16, fake, fake, fake, fake, fake,
                fake, None) == -1
     # fused q/k norm + rope + store: head_dim, short token stride, dtype, no-op

@@ -24,6 +24,10 @@ function is therefore checked against something that does not share its code:
 * partition_partials + lse_merge -- merged partials equal the unsplit softmax
   for several partition sizes (a dropped rescale term fails it).
 * copy_blocks                -- bytes of dst equal src; others untouched.
+* extract_kv / load_kv       -- the reference's per-block copy loops
+  (kv_transfer.py:45-69) restated in torch (oracle/torch_ref.py); a round trip
+  into a second pool at another block list reproduces the blocks and leaves
+  every other block's poison.
 * pack_metadata              -- hand-written expected tensors for a small batch.
 * BlockAllocator / append_slot -- the reference block-manager test facts
   (LIFO order, CoW pair on a shared last block).
@@ -140,6 +144,32 @@ def test_copy_blocks():
     assert np.array_equal(kc[7], k0[3]) and np.array_equal(vc[2], v0[1])
     keep = [i for i in range(10) if i not in (7, 2)]
     assert np.array_equal(kc[keep], k0[keep]) and np.array_equal(vc[keep], v0[keep])
+
+
+def test_extract_and_load_kv():
+    rng = np.random.default_rng(2)
+    kp = _rand_bits(rng, (3, 12, 2, 4, 16), "bf16")
+    vp = _rand_bits(rng, (3, 12, 2, 4, 16), "bf16")
+    ids = [7, 0, 11, 3]
+    wk, wv = O.extract_kv(kp, vp, ids)
+    rk, rv = R.ref_extract_kv(torch.from_numpy(kp.view(np.int16)),
+                              torch.from_numpy(vp.view(np.int16)), ids)
+    assert np.array_equal(wk, rk.numpy().view(np.uint16))
+    assert np.array_equal(wv, rv.numpy().view(np.uint16))
+    zk, _ = O.extract_kv(kp, vp, [5, 99])             # out of the pool -> zero block
+    assert np.array_equal(zk[:, 0], kp[:, 5]) and not zk[:, 1].any()
+    dk = np.full((3, 20, 2, 4, 16), 0x7fc1, np.uint16)
+    dv = dk.copy()
+    dst = [19, 2, 8, 13]
+    O.load_kv(dk, dv, dst, wk, wv)
+    tk = torch.from_numpy(np.full((3, 20, 2, 4, 16), 0x7fc1, np.uint16).view(np.int16))
+    tv = tk.clone()
+    R.ref_load_kv(tk, tv, dst, torch.from_numpy(wk.view(np.int16)), torch.from_numpy(wv.view(np.int16)))
+    assert np.array_equal(dk, tk.numpy().view(np.uint16)) and np.array_equal(dv, tv.numpy().view(np.uint16))
+    for s_, d_ in zip(ids, dst):
+        assert np.array_equal(dk[:, d_], kp[:, s_]) and np.array_equal(dv[:, d_], vp[:, s_])
+    rest = [b for b in range(20) if b not in dst]
+    assert (dk[:, rest] == 0x7fc1).all() and (dv[:, rest] == 0x7fc1).all()
 
 
 # ---------------------------------------------------------------------------
