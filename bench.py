@@ -358,6 +358,74 @@ def bench_copy(args, dev) -> int:
     return 0
 
 
+def bench_decode_fp8(args, w) -> int:
+    """Configuration 2 over an FP8 (e4m3) pool: the same sequences, tables and
+    queries, the bf16 pool's values quantised with per-kv-head scales
+    (amax / 448). One step = the fp8 store of one new token per sequence + fp8
+    decode attention. Algorithmic bytes count 1 byte per K/V element."""
+    from nanopd_amd import paged_kernels as pk
+    dev = w.k_cache.device
+    kvh = w.num_kv_heads
+    ks = (w.k_cache.float().abs().amax(dim=(0, 2, 3)) / 448).clamp_min(1e-8).contiguous()
+    vs = (w.v_cache.float().abs().amax(dim=(0, 2, 3)) / 448).clamp_min(1e-8).contiguous()
+    k8 = (w.k_cache.float() / ks[None, :, None, None]).to(torch.float8_e4m3fn)
+    v8 = (w.v_cache.float() / vs[None, :, None, None]).to(torch.float8_e4m3fn)
+    out = torch.empty_like(w.query)
+    ws = torch.zeros(max(1, pk.attention_workspace_bytes(
+        w.num_seqs, w.num_heads, kvh, w.head_dim, w.block_size, w.max_blocks_per_seq)),
+        dtype=torch.uint8, device=dev)
+    bt = w.block_tables.cpu()
+    pos = [n - 1 for n in w.seq_lens_list]
+    slots = torch.tensor([int(bt[i, p // w.block_size]) * w.block_size + p % w.block_size
+                          for i, p in enumerate(pos)], dtype=torch.int32, device=dev)
+    sk = w.store_k.transpose(0, 1)            # [T, kvh, D] views of the stored tokens
+    sv = w.store_v.transpose(0, 1)
+
+    def store():
+        pk.paged_kv_store_slots_fp8(k8, v8, sk, sv, slots, ks, vs)
+
+    def attend():
+        pk.paged_attention_forward_fp8(out, w.query, k8, v8, w.block_tables, w.seq_lens, w.scale,
+                                       w.block_size, w.max_blocks_per_seq, ks, vs, workspace=ws)
+
+    for _ in range(args.warmup):
+        store()
+        attend()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        store()
+        attend()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    attn_ms = _launch_avg_ms(attend, args.steps)
+    elt = 2
+    ctx = sum(w.seq_lens_list)
+    attn_bytes = (ctx * kvh * w.head_dim * 2 + 2 * w.num_seqs * w.num_heads * w.head_dim * elt
+                  + w.num_seqs * w.max_blocks_per_seq * 4 + w.num_seqs * 4)
+    t = len(pos)
+    store_bytes = 2 * t * kvh * w.head_dim * (elt + 1) + 4 * t
+    achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "Decode paged-attn achieved HBM GB/s (% peak), FP8 e4m3 KV pool",
+        "value": round((attn_bytes + store_bytes) / (ms * 1e-3) / 1e9, 1), "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp8e4m3/bf16",
+        "data": "synthetic (configuration 2's seeded pool quantised per kv head)",
+        "config": {"workload": "cfg2_qwen3_8b_decode_b64_fp8", "num_seqs": w.num_seqs,
+                   "num_heads": w.num_heads, "num_kv_heads": kvh, "head_dim": w.head_dim,
+                   "block_size": w.block_size, "context_tokens": ctx,
+                   "step": "fp8 kv store (1 token/seq) + fp8 paged decode attention"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": _profiled_traffic(f"decode_d128_kernel/{w.name}_fp8")},
+        "detail": {"attention_us_mean": round(attn_ms * 1e3, 2), "attention_bytes": attn_bytes,
+                   "context_tokens_per_s": round(ctx / (attn_ms * 1e-3), 1),
+                   "kernels": "decode_d128_kernel<.., fp8> (e4m3 -> bf16 in registers)"},
+    }), flush=True)
+    return 0
+
+
 def bench_transfer(args, dev) -> int:
     """KV transfer pack / unpack at configuration 5's shape: one 4096-token
     sequence (256 blocks of 16) of random-init Qwen3-8B (36 layers, 8 kv heads
@@ -448,11 +516,13 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=["decode", "long", "prefill", "copy", "e2e", "transfer"],
+    ap.add_argument("--workload", choices=["decode", "decode-fp8", "long", "prefill", "copy", "e2e",
+                                           "transfer"],
                     default="decode",
                     help="decode: config 2 (default); long: config 4 (8 seqs, 8k-32k); "
                          "prefill: config 3 (4 chunks of 512 on paged prefixes + 48 decodes); "
                          "e2e: config 5 (Qwen3-8B collocated serving, tok/s); "
+                         "decode-fp8: config 2 over an FP8 (e4m3) pool; "
                          "transfer: KV transfer pack + unpack of a 4096-token Qwen3-8B sequence; "
                          "copy: a plain 256 MiB device copy, the calibration kernel for "
                          "the FETCH_SIZE / WRITE_SIZE counters")
@@ -478,6 +548,8 @@ def main() -> int:
         return bench_e2e(args, dev)
     if args.workload == "transfer":
         return bench_transfer(args, dev)
+    if args.workload == "decode-fp8":
+        return bench_decode_fp8(args, workloads.config2(dev))
     if args.workload == "prefill":
         return emit_prefill(args, workloads.config3(dev))
     if args.workload == "decode":

@@ -88,6 +88,25 @@ int npd_paged_kv_store_slots(void* k_cache, void* v_cache,
                              int32_t dtype, void* stream);
 
 /*
+ * FP8 (OCP e4m3) pool variant of npd_paged_kv_store_slots (no reference
+ * counterpart: the reference's caches are fp16, nanoPD/engine/model_runner.py:
+ * 24-31). Caches hold one e4m3 byte per element, same [num_blocks, kvh,
+ * block_size, head_dim] layout; k_scale / v_scale: fp32 [num_kv_heads].
+ *   byte = e4m3_rne(clamp(x / scale[h], -448, 448))   (IEEE fp32 division;
+ *   NaN stays NaN), so that element = e4m3(byte) * scale[h].
+ * Sources are fp16 or bf16 (src_dtype), as in npd_paged_kv_store_slots.
+ * Caches 8-byte aligned, sources 16-byte aligned.
+ */
+int npd_paged_kv_store_slots_fp8(void* k_cache, void* v_cache,
+                                 const void* k_src, const void* v_src,
+                                 const int32_t* slot_mapping,
+                                 const float* k_scale, const float* v_scale,
+                                 int64_t num_tokens, int64_t num_kv_heads, int64_t head_dim,
+                                 int64_t num_blocks, int64_t block_size,
+                                 int64_t src_stride_head, int64_t src_stride_token,
+                                 int32_t src_dtype, void* stream);
+
+/*
  * Bytes of device workspace npd_paged_attention needs for these shapes (merge
  * counter region, work list, split-context partials). 0 means no workspace is
  * needed.
@@ -168,6 +187,26 @@ int npd_paged_prefill_attention(void* out, const void* query,
                                 int64_t out_stride_token, int64_t out_stride_head,
                                 void* workspace, int64_t workspace_bytes,
                                 int32_t dtype, void* stream);
+
+/*
+ * npd_paged_attention over an FP8 (e4m3) pool written by
+ * npd_paged_kv_store_slots_fp8 (no reference counterpart). K and V elements
+ * are e4m3(byte) * k_scale[kv head] (v_scale for V); query/out are fp16 or
+ * bf16 (dtype), arithmetic as in npd_paged_attention. head_dim 128, block_size
+ * 16 or 32, at most 4096 sequences; caches 8-byte aligned. The workspace is
+ * sized by npd_paged_attention_workspace_size with the same arguments.
+ */
+int npd_paged_attention_fp8(void* out, const void* query,
+                            const void* key_cache, const void* value_cache,
+                            const int32_t* block_tables, const int32_t* seq_lens,
+                            const float* k_scale, const float* v_scale,
+                            int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads,
+                            int64_t head_dim, int64_t num_blocks, int64_t block_size,
+                            int64_t max_blocks_per_seq, float scale,
+                            int64_t q_stride_seq, int64_t q_stride_head,
+                            int64_t out_stride_seq, int64_t out_stride_head,
+                            void* workspace, int64_t workspace_bytes,
+                            int32_t dtype, void* stream);
 
 /*
  * Copy-on-write block copy (no reference counterpart: the reference returns

@@ -27,10 +27,15 @@ SIGNATURES = {
                                           _I64, _I64, _I64, _I32, _P]),
     "npd_paged_kv_store_slots": (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
                                                 _I64, _I64, _I32, _P]),
+    "npd_paged_kv_store_slots_fp8": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64,
+                                                    _I64, _I64, _I64, _I64, _I32, _P]),
     "npd_paged_attention_workspace_size": (_I64, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "npd_paged_attention": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
                                            _I64, _I64, _F, _I64, _I64, _I64, _I64, _P, _I64, _I32,
                                            _P]),
+    "npd_paged_attention_fp8": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64,
+                                               _I64, _I64, _I64, _I64, _F, _I64, _I64, _I64, _I64,
+                                               _P, _I64, _I32, _P]),
     "npd_paged_prefill_workspace_size": (_I64, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "npd_paged_prefill_attention": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64,
                                                    _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F,

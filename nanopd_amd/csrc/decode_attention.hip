@@ -23,11 +23,14 @@
 // ones write fp32 partials (acc, max, sum) and merge_partitions_kernel
 // combines them (log-sum-exp merge). No MFMA: at one query row per sequence
 // the op is HBM-bound.
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMaxPartition = 512;   // tokens per partition, upper bound (LDS sizing)
@@ -79,6 +82,8 @@ struct DecodeArgs {
   float* part_ml;    // [S*kvh, max_parts, G, 2]
   int* counters;     // [S*kvh] arrival counters of the fused merge
   int* sched;        // fast path, more than 64 sequences: [1] number of work items
+  const float* k_scale;   // fp8 pool: per-kv-head scales (element = e4m3 byte * scale)
+  const float* v_scale;
   int num_seqs;
   int2* items;       // fast path: (unit, partition) work list
   int num_kv_heads;
@@ -449,7 +454,7 @@ using npd::st_coherent2;
 constexpr int kMergeFlight = 4;
 template <class TT, int G>
 __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int unit, int s, int kh,
-                                                int nparts, int lane, float* s_w) {
+                                                int nparts, int lane, float* s_w, float oscale) {
   constexpr int D = 128, GP = pow2ceil(G), CH = D / 8;
   constexpr int OWN = (G * CH + 63) / 64;   // (head, chunk) pairs per lane
   const int64_t base = (int64_t)unit * a.max_parts;
@@ -538,14 +543,48 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int unit, i
     if (idx < G * CH) {
       const int h = idx / CH, c = idx % CH;
       store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + c * 8,
-                     o[k], 1.f / L[h]);
+                     o[k], oscale / L[h]);
     }
   }
 }
 
-template <class TT, int G, int SPB>
+// Element source of the fast path. 2-byte pools: a lane's 8 elements are one
+// 16-byte load, used as 4 packed pairs. FP8 pools (kF8): 8 e4m3 bytes, one
+// 8-byte load (the same index arithmetic in 8-byte units, a head row being 128
+// bytes), converted exactly to 4 pairs of TT by v_cvt_scalef32_pk_*_fp8 with
+// scale 1 (the per-head scales are applied in fp32: to the scores and to the
+// output).
+template <class TT, bool kF8>
+struct KvSrc {
+  typedef u32x4 raw;
+  static __device__ __forceinline__ raw load(const void* base, int64_t idx) {
+    return ld_stream(static_cast<const u32x4*>(base) + idx);
+  }
+  static __device__ __forceinline__ u32x4 pairs(raw w) { return w; }
+};
+template <class TT>
+struct KvSrc<TT, true> {
+  typedef u32x2 raw;
+  static __device__ __forceinline__ raw load(const void* base, int64_t idx) {
+    return __builtin_nontemporal_load(static_cast<const u32x2*>(base) + idx);
+  }
+  template <bool kHi>
+  static __device__ __forceinline__ uint32_t cvt(uint32_t w) {
+    if constexpr (std::is_same<TT, npd::BF16>::value)
+      return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, kHi));
+    else
+      return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.f, kHi));
+  }
+  static __device__ __forceinline__ u32x4 pairs(raw w) {
+    return u32x4{cvt<false>(w.x), cvt<true>(w.x), cvt<false>(w.y), cvt<true>(w.y)};
+  }
+};
+
+template <class TT, int G, int SPB, bool kF8 = false>
 __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, int part,
                                                  float* s_p, uint32_t* s_pp) {
+  typedef KvSrc<TT, kF8> Src;
+  typedef typename Src::raw raw_t;
   constexpr int D = 128;
   constexpr int GP = pow2ceil(G);
   constexpr int LGP = ilog2(GP);
@@ -612,38 +651,42 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
       myblk = b < 0 ? 0 : (b >= a.num_blocks ? a.num_blocks - 1 : b);
     }
   }
-  const int voff = (r * 16) + j;   // 16-byte offset of the lane's chunk: slot i is token i*4 + r
+  const int voff = (r * 16) + j;   // offset (in lane chunks) of the lane's chunk: slot i is token i*4 + r
+  // scores in log2 units (times the K scale of an fp8 pool); output scale
+  const float score_scale = kF8 ? a.scale_log2 * a.k_scale[kh] : a.scale_log2;
+  const float out_scale = kF8 ? a.v_scale[kh] : 1.f;
 
   const int64_t head_rows = (int64_t)kh * BS;            // rows of head kh in a block
   const int64_t blk_rows = (int64_t)a.num_kv_heads * BS; // rows per block
-  auto step_base = [&](int st) -> int64_t {              // 16-byte index of the step's first row
+  auto step_base = [&](int st) -> int64_t {              // chunk index of the step's first row
     const int blk = __builtin_amdgcn_readlane(myblk, (st / SPB) & 63);
     return ((int64_t)blk * blk_rows + head_rows + (st % SPB) * 16) * 16;
   };
   // K/V rows are read once per call: nontemporal loads keep them from
   // displacing reusable lines in L2
-  auto load_k = [&](u32x4* buf, int st) {
-    const u32x4* p = a.k_cache + step_base(st);
+  auto load_k = [&](raw_t* buf, int st) {
+    const int64_t b = step_base(st) + voff;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) buf[i] = ld_stream(p + voff + i * 64);
+    for (int i = 0; i < 4; ++i) buf[i] = Src::load(a.k_cache, b + i * 64);
   };
-  auto load_v = [&](u32x4* buf, int st) {
-    const u32x4* p = a.v_cache + step_base(st);
+  auto load_v = [&](raw_t* buf, int st) {
+    const int64_t b = step_base(st) + voff;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) buf[i] = ld_stream(p + voff + i * 64);
+    for (int i = 0; i < 4; ++i) buf[i] = Src::load(a.v_cache, b + i * 64);
   };
 
   // ---------------- pass 1: scores ----------------
-  auto score_step = [&](const u32x4* kb, int st) {
+  auto score_step = [&](const raw_t* kraw, int st) {
     float v[NV];   // v[h * 4 + i]: q slot h . token slot i
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      const u32x4 kbi = Src::pairs(kraw[i]);
 #pragma unroll
       for (int h = 0; h < GP; ++h) {
-        float d = TT::dot2(kb[i].x, qv[h].x, 0.f);
-        d = TT::dot2(kb[i].y, qv[h].y, d);
-        d = TT::dot2(kb[i].z, qv[h].z, d);
-        d = TT::dot2(kb[i].w, qv[h].w, d);
+        float d = TT::dot2(kbi.x, qv[h].x, 0.f);
+        d = TT::dot2(kbi.y, qv[h].y, d);
+        d = TT::dot2(kbi.z, qv[h].z, d);
+        d = TT::dot2(kbi.w, qv[h].w, d);
         v[h * 4 + i] = d;
       }
     }
@@ -663,13 +706,13 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
       const int h = headmask;
       const int ti = (tup1 ? 2 : 0) + (HELD == 2 ? e : (tup0 ? 1 : 0));
       const int tl = st * 16 + ti * 4 + r;
-      if (h < G) s_p[tl * GP + h] = (tl < ntok) ? v[e] * a.scale_log2 : -INFINITY;
+      if (h < G) s_p[tl * GP + h] = (tl < ntok) ? v[e] * score_scale : -INFINITY;
     }
   };
   {
     // ring of NBUF steps in flight; the last round is peeled so the steady
     // loop has no branches and each wait leaves the newer loads pending
-    u32x4 kb[NBUF][4];
+    raw_t kb[NBUF][4];
 #pragma unroll
     for (int b = 0; b < NBUF; ++b) load_k(kb[b], b);
     auto round = [&](int st0) {
@@ -685,7 +728,7 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
     for (int b = 0; b < NBUF; ++b) score_step(kb[b], st0 + b);
   }
 
-  u32x4 vb[NBUF][4];
+  raw_t vb[NBUF][4];
 #pragma unroll
   for (int b = 0; b < NBUF; ++b) load_v(vb[b], b);
   __syncthreads();
@@ -739,7 +782,10 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
   for (int h = 0; h < G; ++h)
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[h][d] = 0.f;
-  auto pv_step = [&](u32x4* vbuf, int st) {
+  auto pv_step = [&](const raw_t* vraw, int st) {
+    u32x4 vbuf[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vbuf[i] = Src::pairs(vraw[i]);
     if (st * 16 + 16 > ntok) {   // tail step: rows past the context may hold anything
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -829,7 +875,7 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
 #pragma unroll
       for (int h = 0; h < G; ++h)
         store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + j * 8,
-                       acc[h], 1.f / l[h]);
+                       acc[h], out_scale / l[h]);
     }
     return;
   }
@@ -871,7 +917,7 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
     ticket = __hip_atomic_fetch_add(a.counters + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   ticket = __shfl(ticket, 0, 64);
   if (ticket != nparts - 1) return;
-  merge_unit_fast<TT, G>(a, unit, s, kh, nparts, lane, s_p);
+  merge_unit_fast<TT, G>(a, unit, s, kh, nparts, lane, s_p, out_scale);
   if (lane == 0) __hip_atomic_store(a.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -881,7 +927,7 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
 // consecutive -- so long units start together, finish and merge early, and the
 // short ones fill the tail. The grid is sized for the most items possible;
 // workgroups past the list (all at the end of the grid) exit at once.
-template <class TT, int G, int SPB>
+template <class TT, int G, int SPB, bool kF8>
 __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
   constexpr int GP = pow2ceil(G);
   constexpr int MAXT = kFastMaxPartition + 16 * kRing;
@@ -955,7 +1001,7 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
     unit = it.x;
     part = it.y;
   }
-  decode_d128_item<TT, G, SPB>(a, unit, part, s_p, s_pp);
+  decode_d128_item<TT, G, SPB, kF8>(a, unit, part, s_p, s_pp);
 }
 
 // Builds the work list of decode_d128_kernel (one workgroup):
@@ -1075,11 +1121,12 @@ int choose_partition(int64_t num_seqs, int64_t num_kv_heads, int64_t head_dim, i
   return units * ((max_ctx + 511) / 512) >= 4096 ? 512 : 256;
 }
 
-template <class TT, int G, int SPB>
+template <class TT, int G, int SPB, bool kF8 = false>
 int launch_fast_bs(const DecodeArgs& a, int num_seqs, int64_t max_items, hipStream_t st) {
   if (num_seqs > kInlineSchedMax)
     hipLaunchKernelGGL(decode_schedule_kernel, dim3(1), dim3(kSchedThreads), 0, st, a, num_seqs);
-  hipLaunchKernelGGL((decode_d128_kernel<TT, G, SPB>), dim3((unsigned)max_items), dim3(64), 0, st, a);
+  hipLaunchKernelGGL((decode_d128_kernel<TT, G, SPB, kF8>), dim3((unsigned)max_items), dim3(64), 0,
+                     st, a);
   return NPD_OK;
 }
 
@@ -1092,6 +1139,30 @@ int launch_fast(const DecodeArgs& a, int num_seqs, int64_t max_items, hipStream_
     case 128: return launch_fast_bs<TT, G, 8>(a, num_seqs, max_items, st);
     default: return launch_fast_bs<TT, G, 16>(a, num_seqs, max_items, st);
   }
+}
+
+// FP8 pools: the fast path only, block sizes 16 and 32
+template <class TT, int G>
+int launch_fast_fp8(const DecodeArgs& a, int num_seqs, int64_t max_items, hipStream_t st) {
+  if (a.block_size == 16) return launch_fast_bs<TT, G, 1, true>(a, num_seqs, max_items, st);
+  return launch_fast_bs<TT, G, 2, true>(a, num_seqs, max_items, st);
+}
+
+template <class TT>
+int dispatch_fp8(int g, const DecodeArgs& a, int64_t units, hipStream_t st) {
+  const int ns = (int)(units / a.num_kv_heads);
+  const int64_t mi = units * a.max_parts;
+  switch (g) {
+    case 1: launch_fast_fp8<TT, 1>(a, ns, mi, st); break;
+    case 2: launch_fast_fp8<TT, 2>(a, ns, mi, st); break;
+    case 3: launch_fast_fp8<TT, 3>(a, ns, mi, st); break;
+    case 4: launch_fast_fp8<TT, 4>(a, ns, mi, st); break;
+    case 5: launch_fast_fp8<TT, 5>(a, ns, mi, st); break;
+    case 6: launch_fast_fp8<TT, 6>(a, ns, mi, st); break;
+    case 7: launch_fast_fp8<TT, 7>(a, ns, mi, st); break;
+    default: launch_fast_fp8<TT, 8>(a, ns, mi, st); break;
+  }
+  return npd::check_launch("npd_paged_attention_fp8");
 }
 
 template <class TT, int D, int G>
@@ -1157,17 +1228,19 @@ extern "C" int64_t npd_paged_attention_workspace_size(int64_t num_seqs, int64_t 
   return (npd::kCounterBytes + 16 + units * parts * 8 + 255) / 256 * 256 + partials;
 }
 
-extern "C" int npd_paged_attention(void* out, const void* query, const void* key_cache,
-                                   const void* value_cache, const int32_t* block_tables,
-                                   const int32_t* seq_lens, int64_t num_seqs, int64_t num_heads,
-                                   int64_t num_kv_heads, int64_t head_dim, int64_t num_blocks,
-                                   int64_t block_size, int64_t max_blocks_per_seq, float scale,
-                                   int64_t q_stride_seq, int64_t q_stride_head,
-                                   int64_t out_stride_seq, int64_t out_stride_head,
-                                   void* workspace, int64_t workspace_bytes, int32_t dtype,
-                                   void* stream) {
+namespace {
+
+// Shared by the 2-byte and the fp8 entry points: k_scale / v_scale are null
+// for 2-byte pools.
+int attention_impl(void* out, const void* query, const void* key_cache, const void* value_cache,
+                   const int32_t* block_tables, const int32_t* seq_lens, int64_t num_seqs,
+                   int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t num_blocks,
+                   int64_t block_size, int64_t max_blocks_per_seq, float scale,
+                   int64_t q_stride_seq, int64_t q_stride_head, int64_t out_stride_seq,
+                   int64_t out_stride_head, const float* k_scale, const float* v_scale,
+                   void* workspace, int64_t workspace_bytes, int32_t dtype, void* stream,
+                   bool fp8, const char* name) {
   using namespace npd;
-  const char* name = "npd_paged_attention";
   if (dtype != NPD_DTYPE_F16 && dtype != NPD_DTYPE_BF16)
     return fail(NPD_E_DTYPE, "%s: unsupported dtype code %d (fp16/bf16 only)", name, dtype);
   if (num_seqs < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_blocks <= 0 ||
@@ -1194,11 +1267,20 @@ extern "C" int npd_paged_attention(void* out, const void* query, const void* key
       q_stride_seq < 0 || q_stride_head < 0 || out_stride_seq < 0 || out_stride_head < 0)
     return fail(NPD_E_ALIGN, "%s: query/out strides must be non-negative multiples of 8 elements",
                 name);
+  if (fp8 && (head_dim != 128 || (block_size != 16 && block_size != 32) ||
+              !use_fast_path(head_dim, block_size, num_seqs)))
+    return fail(NPD_E_INVALID, "%s: fp8 pools need head_dim 128, block_size 16 or 32 and at most "
+                "%d sequences", name, kSchedMaxSeqs);
   if (num_seqs == 0) return NPD_OK;
-  if (!out || !query || !key_cache || !value_cache || !block_tables || !seq_lens)
+  if (!out || !query || !key_cache || !value_cache || !block_tables || !seq_lens ||
+      (fp8 && (!k_scale || !v_scale)))
     return fail(NPD_E_INVALID, "%s: null pointer", name);
-  if (!aligned16(out) || !aligned16(query) || !aligned16(key_cache) || !aligned16(value_cache))
-    return fail(NPD_E_ALIGN, "%s: out/query/cache pointers must be 16-byte aligned", name);
+  const uintptr_t cache_align = fp8 ? 7u : 15u;
+  if (!aligned16(out) || !aligned16(query) ||
+      (reinterpret_cast<uintptr_t>(key_cache) & cache_align) ||
+      (reinterpret_cast<uintptr_t>(value_cache) & cache_align))
+    return fail(NPD_E_ALIGN, "%s: out/query pointers must be 16-byte aligned, caches %d-byte", name,
+                fp8 ? 8 : 16);
 
   const int64_t max_ctx = block_size * max_blocks_per_seq;
   const int partition = choose_partition(num_seqs, num_kv_heads, head_dim, block_size, max_ctx);
@@ -1251,7 +1333,49 @@ extern "C" int npd_paged_attention(void* out, const void* query, const void* key
   a.q_stride_head = q_stride_head;
   a.out_stride_seq = out_stride_seq;
   a.out_stride_head = out_stride_head;
+  a.k_scale = k_scale;
+  a.v_scale = v_scale;
   hipStream_t st = as_stream(stream);
+  if (fp8) {
+    if (dtype == NPD_DTYPE_BF16) return dispatch_fp8<BF16>((int)g, a, units, st);
+    return dispatch_fp8<F16>((int)g, a, units, st);
+  }
   if (dtype == NPD_DTYPE_BF16) return dispatch_d<BF16>(head_dim, (int)g, a, units, st);
   return dispatch_d<F16>(head_dim, (int)g, a, units, st);
+}
+
+}  // namespace
+
+extern "C" int npd_paged_attention(void* out, const void* query, const void* key_cache,
+                                   const void* value_cache, const int32_t* block_tables,
+                                   const int32_t* seq_lens, int64_t num_seqs, int64_t num_heads,
+                                   int64_t num_kv_heads, int64_t head_dim, int64_t num_blocks,
+                                   int64_t block_size, int64_t max_blocks_per_seq, float scale,
+                                   int64_t q_stride_seq, int64_t q_stride_head,
+                                   int64_t out_stride_seq, int64_t out_stride_head,
+                                   void* workspace, int64_t workspace_bytes, int32_t dtype,
+                                   void* stream) {
+  return attention_impl(out, query, key_cache, value_cache, block_tables, seq_lens, num_seqs,
+                        num_heads, num_kv_heads, head_dim, num_blocks, block_size,
+                        max_blocks_per_seq, scale, q_stride_seq, q_stride_head, out_stride_seq,
+                        out_stride_head, nullptr, nullptr, workspace, workspace_bytes, dtype,
+                        stream, false, "npd_paged_attention");
+}
+
+extern "C" int npd_paged_attention_fp8(void* out, const void* query, const void* key_cache,
+                                       const void* value_cache, const int32_t* block_tables,
+                                       const int32_t* seq_lens, const float* k_scale,
+                                       const float* v_scale, int64_t num_seqs,
+                                       int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                                       int64_t num_blocks, int64_t block_size,
+                                       int64_t max_blocks_per_seq, float scale,
+                                       int64_t q_stride_seq, int64_t q_stride_head,
+                                       int64_t out_stride_seq, int64_t out_stride_head,
+                                       void* workspace, int64_t workspace_bytes, int32_t dtype,
+                                       void* stream) {
+  return attention_impl(out, query, key_cache, value_cache, block_tables, seq_lens, num_seqs,
+                        num_heads, num_kv_heads, head_dim, num_blocks, block_size,
+                        max_blocks_per_seq, scale, q_stride_seq, q_stride_head, out_stride_seq,
+                        out_stride_head, k_scale, v_scale, workspace, workspace_bytes, dtype,
+                        stream, true, "npd_paged_attention_fp8");
 }

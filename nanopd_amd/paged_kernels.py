@@ -161,6 +161,53 @@ def paged_kv_store_slots(k_cache: torch.Tensor, v_cache: torch.Tensor, k_src: to
               k_src.stride(1), k_src.stride(0), code, _stream(dev))
 
 
+FP8_DTYPES = (torch.uint8, torch.float8_e4m3fn)
+
+
+def _fp8_cache_checks(k_cache: torch.Tensor, v_cache: torch.Tensor, k_scale: torch.Tensor,
+                      v_scale: torch.Tensor) -> None:
+    _check(k_cache.dim() == 4 and v_cache.dim() == 4 and k_cache.shape == v_cache.shape,
+           "fp8 caches must be [num_blocks, num_kv_heads, block_size, head_dim]")
+    _check(k_cache.dtype in FP8_DTYPES and v_cache.dtype == k_cache.dtype,
+           "fp8 caches must be torch.float8_e4m3fn (or uint8 holding e4m3 bytes)")
+    _check(k_cache.is_contiguous() and v_cache.is_contiguous(), "caches must be contiguous")
+    kvh = k_cache.size(1)
+    for sc, nm in ((k_scale, "k_scale"), (v_scale, "v_scale")):
+        _check(isinstance(sc, torch.Tensor) and sc.dtype == torch.float32 and sc.dim() == 1
+               and sc.numel() == kvh and sc.is_contiguous(),
+               f"{nm} must be a contiguous float32 [num_kv_heads] tensor")
+
+
+def paged_kv_store_slots_fp8(k_cache: torch.Tensor, v_cache: torch.Tensor, k_src: torch.Tensor,
+                             v_src: torch.Tensor, slot_mapping: torch.Tensor,
+                             k_scale: torch.Tensor, v_scale: torch.Tensor) -> None:
+    """:func:`paged_kv_store_slots` into an FP8 (OCP e4m3) pool with
+    per-kv-head scales (no reference counterpart; its caches are fp16):
+    byte = e4m3(clamp(x / scale[h], -448, 448)), round to nearest even."""
+    _check(isinstance(k_src, torch.Tensor) and k_src.is_cuda, "k src is must be on CUDA")
+    _check(k_src.dim() == 3 and v_src.shape == k_src.shape,
+           "k_src / v_src must be [num_tokens, num_kv_heads, head_dim]")
+    _fp8_cache_checks(k_cache, v_cache, k_scale, v_scale)
+    _int32(slot_mapping, "slot_mapping")
+    dev = k_src.device
+    _same_device(dev, v_src, k_cache, v_cache, slot_mapping, k_scale, v_scale)
+    n, kvh, d = k_src.shape
+    num_blocks, ckvh, bs, cd = k_cache.shape
+    _check(ckvh == kvh and cd == d, "source does not match cache shape")
+    _check(v_src.dtype == k_src.dtype, "k_src / v_src dtypes differ")
+    code = _dtype_code(k_src, "paged_kv_store_slots_fp8")
+    _check(slot_mapping.dim() == 1 and slot_mapping.numel() >= n and slot_mapping.is_contiguous(),
+           "slot_mapping must be a contiguous [num_tokens] tensor")
+    if n == 0:
+        return
+    if k_src.stride(2) != 1 or v_src.stride() != k_src.stride():
+        k_src, v_src = k_src.contiguous(), v_src.contiguous()
+    _lib.call("npd_paged_kv_store_slots_fp8", k_cache.data_ptr(), v_cache.data_ptr(),
+              k_src.data_ptr(), v_src.data_ptr(), slot_mapping.data_ptr(), k_scale.data_ptr(),
+              v_scale.data_ptr(), n, kvh, d, num_blocks, bs, k_src.stride(1), k_src.stride(0), code,
+              _stream(dev))
+
+
 # ---------------------------------------------------------------------------
 # Decode attention
 # ---------------------------------------------------------------------------
@@ -241,6 +288,54 @@ def paged_attention_forward(out: torch.Tensor, query: torch.Tensor, key_cache: t
               value_cache.data_ptr(), block_tables.data_ptr(), seq_lens.data_ptr(), s, h, kvh, d,
               num_blocks, bs, mb, float(scale), query.stride(0), query.stride(1), out.stride(0),
               out.stride(1), ws_ptr, need, code, stream)
+
+
+def paged_attention_forward_fp8(out: torch.Tensor, query: torch.Tensor, key_cache: torch.Tensor,
+                                value_cache: torch.Tensor, block_tables: torch.Tensor,
+                                seq_lens: torch.Tensor, scale: float, block_size: int,
+                                max_num_blocks_per_seq: int, k_scale: torch.Tensor,
+                                v_scale: torch.Tensor,
+                                workspace: torch.Tensor | None = None) -> None:
+    """:func:`paged_attention_forward` over an FP8 pool written by
+    :func:`paged_kv_store_slots_fp8`: K = e4m3(byte) * k_scale[kv head], V
+    likewise. query/out fp16 or bf16; head_dim 128; block_size 16 or 32."""
+    _check(isinstance(query, torch.Tensor) and query.is_cuda, "query is must be on CUDA")
+    _check(query.dim() == 3, "query must be [num seqs, num_heads, head_size]")
+    _fp8_cache_checks(key_cache, value_cache, k_scale, v_scale)
+    _int32(block_tables, "block_tables")
+    _int32(seq_lens, "seq_lens")
+    dev = query.device
+    _same_device(dev, out, key_cache, value_cache, block_tables, seq_lens, k_scale, v_scale)
+    s, h, d = query.shape
+    num_blocks, kvh, bs, cd = key_cache.shape
+    _check(cd == d, f"head_dim {d} does not match cache head_dim {cd}")
+    _check(int(block_size) == bs, f"block_size {block_size} does not match cache block size {bs}")
+    _check(h % kvh == 0, f"num_heads {h} is not a multiple of num_kv_heads {kvh}")
+    _check(out.shape == query.shape and out.dtype == query.dtype, "out must match query")
+    code = _dtype_code(query, "paged_attention_forward_fp8")
+    mb = int(max_num_blocks_per_seq)
+    _check(block_tables.dim() == 2 and block_tables.size(0) >= s and block_tables.size(1) == mb,
+           "block_tables must be [num_seqs, max_num_blocks_per_seq]")
+    _check(block_tables.is_contiguous(), "block_tables must be contiguous")
+    _check(seq_lens.dim() == 1 and seq_lens.numel() >= s and seq_lens.is_contiguous(),
+           "seq_lens must be a contiguous [num_seqs] tensor")
+    _check(query.stride(2) == 1 and out.stride(2) == 1, "head_dim must be the contiguous dim")
+    if s == 0:
+        return
+    need = attention_workspace_bytes(s, h, kvh, d, bs, mb)
+    stream = _stream(dev)
+    ws_ptr = 0
+    if need > 0:
+        if workspace is None:
+            workspace = _decode_workspace(dev, stream, need)
+        _check(workspace.numel() * workspace.element_size() >= need,
+               f"workspace of {need} bytes needed")
+        ws_ptr = workspace.data_ptr()
+    _lib.call("npd_paged_attention_fp8", out.data_ptr(), query.data_ptr(), key_cache.data_ptr(),
+              value_cache.data_ptr(), block_tables.data_ptr(), seq_lens.data_ptr(),
+              k_scale.data_ptr(), v_scale.data_ptr(), s, h, kvh, d, num_blocks, bs, mb,
+              float(scale), query.stride(0), query.stride(1), out.stride(0), out.stride(1), ws_ptr,
+              need, code, stream)
 
 
 # ---------------------------------------------------------------------------

@@ -50,6 +50,63 @@ def f32_to_bits(x: np.ndarray, dtype: str) -> np.ndarray:
 
 
 # ---------------------------------------------------------------------------
+# FP8 (OCP e4m3, "e4m3fn") storage: 1 sign, 4 exponent (bias 7), 3 mantissa
+# bits; no infinities; S.1111.111 is NaN; largest finite 448.
+# ---------------------------------------------------------------------------
+
+
+def e4m3_to_f32(codes: np.ndarray) -> np.ndarray:
+    """e4m3 bytes -> float32 (exact)."""
+    c = np.asarray(codes, dtype=np.uint8).astype(np.int32)
+    sign = np.where(c & 0x80, -1.0, 1.0)
+    e, m = (c >> 3) & 0xF, c & 0x7
+    mag = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * 2.0 ** (e - 7))
+    out = (sign * mag).astype(np.float32)
+    out[(c & 0x7F) == 0x7F] = np.nan
+    return out
+
+
+_E4M3_POS = e4m3_to_f32(np.arange(0x7F, dtype=np.uint8)).astype(np.float64)   # codes 0..126, ascending
+
+
+def f32_to_e4m3(x: np.ndarray) -> np.ndarray:
+    """float -> e4m3 bytes, round to nearest, ties to the even code; values
+    beyond 448 saturate; NaN -> 0x7F. Negative values keep the sign bit (a
+    negative value that rounds to zero gives 0x80)."""
+    x = np.asarray(x, dtype=np.float32).astype(np.float64)
+    a = np.minimum(np.abs(x), 448.0)
+    hi = np.searchsorted(_E4M3_POS, a, side="left").clip(0, 0x7E)
+    lo = np.maximum(hi - 1, 0)
+    dl, dh = a - _E4M3_POS[lo], _E4M3_POS[hi] - a
+    pick = np.where(dl < dh, lo, np.where(dh < dl, hi, np.where(lo % 2 == 0, lo, hi)))
+    pick = np.where(a == _E4M3_POS[hi], hi, pick)
+    out = (pick | np.where(np.signbit(x), 0x80, 0)).astype(np.uint8)
+    out[np.isnan(x)] = 0x7F
+    return out
+
+
+def kv_store_slots_fp8(k_cache: np.ndarray, v_cache: np.ndarray, k_src: np.ndarray,
+                       v_src: np.ndarray, slots: np.ndarray, k_scale: np.ndarray,
+                       v_scale: np.ndarray) -> None:
+    """FP8 pool store: caches uint8 [N, kvh, bs, D], sources float [T, kvh, D]
+    (the exact values of the 2-byte inputs); byte = e4m3(clamp(x / scale[h])),
+    the division in fp32. Slots outside the pool are skipped."""
+    n, kvh, bs, _ = k_cache.shape
+    ks = np.asarray(k_scale, np.float32)[:, None]
+    vs = np.asarray(v_scale, np.float32)[:, None]
+    for t, slot in enumerate(np.asarray(slots)):
+        if 0 <= slot < n * bs:
+            b, o = divmod(int(slot), bs)
+            k_cache[b, :, o] = f32_to_e4m3(np.asarray(k_src[t], np.float32) / ks)
+            v_cache[b, :, o] = f32_to_e4m3(np.asarray(v_src[t], np.float32) / vs)
+
+
+def fp8_pool_values(cache: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """Element values of an fp8 pool: e4m3(byte) * scale[kv head] (float64)."""
+    return e4m3_to_f32(cache).astype(np.float64) * np.asarray(scale, np.float64)[None, :, None, None]
+
+
+# ---------------------------------------------------------------------------
 # KV store (bit-exact scatter)
 # ---------------------------------------------------------------------------
 

@@ -1,0 +1,163 @@
+"""FP8 (OCP e4m3) KV pool on the GPU, through the C-ABI: the store is
+bit-exact against the oracle's e4m3 rounding (itself pinned to
+torch.float8_e4m3fn), and decode attention over the pool is within the
+2-byte path's tolerance of the float64 oracle over the dequantised pool
+(e4m3 values are exact in fp16 and bf16; the per-head scales are applied in
+fp32, to the scores and to the output)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from nanopd_amd import paged_kernels as pk
+from oracle import paged_oracle as O
+from tests.helpers import ATOL, f32, max_abs
+
+pytestmark = pytest.mark.gpu
+
+
+def _u8(t):
+    return t.contiguous().view(torch.uint8).cpu().numpy()
+
+
+def _scales(kvh, seed):
+    g = torch.Generator().manual_seed(seed)
+    return (0.01 + 0.05 * torch.rand(kvh, generator=g)).float()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("kvh,D,bs", [(2, 128, 16), (8, 128, 32), (4, 64, 16), (1, 256, 8)])
+def test_store_bit_exact(device, dtype, kvh, D, bs):
+    g = torch.Generator().manual_seed(kvh * D + bs)
+    N, T = 20, 37
+    kc = torch.full((N, kvh, bs, D), 0x5A, dtype=torch.uint8)
+    vc = kc.clone()
+    k = (torch.randn(T, kvh, D, generator=g) * 2).to(dtype)
+    v = (torch.randn(T, kvh, D, generator=g) * 2).to(dtype)
+    k[0, 0, :4] = torch.tensor([1e4, -1e4, 0.0, -0.0]).to(dtype)     # saturation, signed zeros
+    slots = torch.randperm(N * bs, generator=g)[:T].to(torch.int32)
+    slots[3] = -1
+    slots[5] = N * bs + 7                                          # outside the pool: skipped
+    ks, vs = _scales(kvh, 1), _scales(kvh, 2)
+    want_k, want_v = kc.numpy().copy(), vc.numpy().copy()
+    O.kv_store_slots_fp8(want_k, want_v, f32(k), f32(v), slots.numpy(), ks.numpy(), vs.numpy())
+    dk, dv = kc.to(device).view(torch.float8_e4m3fn), vc.to(device).view(torch.float8_e4m3fn)
+    pk.paged_kv_store_slots_fp8(dk, dv, k.to(device), v.to(device), slots.to(device),
+                                ks.to(device), vs.to(device))
+    torch.cuda.synchronize()
+    assert np.array_equal(_u8(dk), want_k) and np.array_equal(_u8(dv), want_v)
+
+
+def _fp8_case(device, seq_lens, H, kvh, bs, dtype, seed):
+    """Random e4m3 pool (no NaN codes), shuffled tables, per-head scales."""
+    g = torch.Generator().manual_seed(seed)
+    nbs = [(s + bs - 1) // bs for s in seq_lens]
+    mb, total = max(nbs + [1]), max(sum(nbs), 1)
+    codes = torch.randint(0, 0x7E, (2, total, kvh, bs, 128), generator=g, dtype=torch.int32)
+    codes = codes | (torch.randint(0, 2, codes.shape, generator=g, dtype=torch.int32) << 7)
+    kc, vc = codes[0].to(torch.uint8), codes[1].to(torch.uint8)
+    q = torch.randn(len(seq_lens), H, 128, generator=g).to(dtype)
+    order = torch.randperm(total, generator=g)
+    bt = torch.zeros(len(seq_lens), mb, dtype=torch.int32)
+    o = 0
+    for i, n in enumerate(nbs):
+        bt[i, :n] = order[o:o + n]
+        o += n
+    sl = torch.tensor(seq_lens, dtype=torch.int32)
+    # element magnitudes up to about 1.5 (like the 2-byte tests' values): the
+    # absolute tolerance is then above the output's own rounding
+    ks = (0.5 + torch.rand(kvh, generator=g)) / 448
+    vs = (0.5 + torch.rand(kvh, generator=g)) / 448
+    return q, kc, vc, bt, sl, ks.float(), vs.float(), mb
+
+
+def _run_and_check(device, q, kc, vc, bt, sl, ks, vs, mb, bs, dtype):
+    scale = 1 / math.sqrt(128)
+    out = torch.full_like(q, float("nan")).to(device)
+    pk.paged_attention_forward_fp8(out, q.to(device), kc.to(device).view(torch.float8_e4m3fn),
+                                   vc.to(device).view(torch.float8_e4m3fn), bt.to(device),
+                                   sl.to(device), scale, bs, mb, ks.to(device), vs.to(device))
+    torch.cuda.synchronize()
+    want = O.decode_attention(f32(q), O.fp8_pool_values(kc.numpy(), ks.numpy()),
+                              O.fp8_pool_values(vc.numpy(), vs.numpy()), bt.numpy(), sl.numpy(),
+                              scale)
+    assert np.isfinite(f32(out)).all()
+    err = max_abs(out, want)
+    assert err <= ATOL[dtype], f"max-abs {err}"
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("G", [1, 2, 4, 6, 8])
+def test_decode_group_sizes(device, dtype, G):
+    kvh = 2
+    args = _fp8_case(device, [1, 17, 300, 777, 0], G * kvh, kvh, 16, dtype, seed=G)
+    _run_and_check(device, *args, 16, dtype)
+
+
+@pytest.mark.parametrize("bs", [16, 32])
+def test_decode_block_sizes_and_long_context(device, bs):
+    args = _fp8_case(device, [4097, 64, 2500], 32, 8, bs, torch.bfloat16, seed=bs)
+    _run_and_check(device, *args, bs, torch.bfloat16)
+
+
+def test_store_then_decode_matches_bf16_pool(device):
+    """Config-2 shape, 16 sequences: the same bf16 K/V stored into a bf16 pool
+    and into an fp8 pool; attention over the fp8 pool is the fp64 attention
+    over its dequantised values, and stays close to the bf16 pool's."""
+    g = torch.Generator().manual_seed(5)
+    H, kvh, bs, S = 32, 8, 16, 16
+    lens = torch.randint(128, 1500, (S,), generator=g).tolist()
+    nbs = [(n + bs - 1) // bs for n in lens]
+    N, mb = sum(nbs), max(nbs)
+    order = torch.randperm(N, generator=g)
+    bt = torch.zeros(S, mb, dtype=torch.int32)
+    slots = []
+    o = 0
+    for i, (n, nb) in enumerate(zip(lens, nbs)):
+        bt[i, :nb] = order[o:o + nb]
+        o += nb
+        slots += [int(bt[i, p // bs]) * bs + p % bs for p in range(n)]
+    T = len(slots)
+    k = (torch.randn(T, kvh, 128, generator=g) * 0.5).to(torch.bfloat16).to(device)
+    v = (torch.randn(T, kvh, 128, generator=g) * 0.5).to(torch.bfloat16).to(device)
+    sm = torch.tensor(slots, dtype=torch.int32, device=device)
+    ks = torch.full((kvh,), 2.0 / 448, device=device)
+    vs = torch.full((kvh,), 2.0 / 448, device=device)
+    k8 = torch.zeros((N, kvh, bs, 128), dtype=torch.float8_e4m3fn, device=device)
+    v8 = torch.zeros_like(k8)
+    k16 = torch.zeros((N, kvh, bs, 128), dtype=torch.bfloat16, device=device)
+    v16 = torch.zeros_like(k16)
+    pk.paged_kv_store_slots_fp8(k8, v8, k, v, sm, ks, vs)
+    pk.paged_kv_store_slots(k16, v16, k, v, sm)
+    q = (torch.randn(S, H, 128, generator=g) * 0.5).to(torch.bfloat16).to(device)
+    sl = torch.tensor(lens, dtype=torch.int32, device=device)
+    btd = bt.to(device)
+    o8, o16 = torch.empty_like(q), torch.empty_like(q)
+    pk.paged_attention_forward_fp8(o8, q, k8, v8, btd, sl, 128 ** -0.5, bs, mb, ks, vs)
+    pk.paged_attention_forward(o16, q, k16, v16, btd, sl, 128 ** -0.5, bs, mb)
+    torch.cuda.synchronize()
+    want = O.decode_attention(f32(q), O.fp8_pool_values(_u8(k8), ks.cpu().numpy()),
+                              O.fp8_pool_values(_u8(v8), vs.cpu().numpy()), bt.numpy(),
+                              sl.cpu().numpy(), 128 ** -0.5)
+    assert max_abs(o8, want) <= ATOL[torch.bfloat16]
+    # e4m3 keeps 3 mantissa bits: the outputs move by about 2^-5 of the V values
+    assert (o8.float() - o16.float()).abs().max().item() <= 0.05
+
+
+def test_argument_checks(device):
+    q = torch.zeros(1, 8, 64, dtype=torch.bfloat16, device=device)
+    kc = torch.zeros(4, 2, 16, 64, dtype=torch.float8_e4m3fn, device=device)
+    sc = torch.ones(2, device=device)
+    bt = torch.zeros(1, 1, dtype=torch.int32, device=device)
+    sl = torch.ones(1, dtype=torch.int32, device=device)
+    with pytest.raises(RuntimeError, match="head_dim"):
+        pk.paged_attention_forward_fp8(torch.empty_like(q), q, kc, kc, bt, sl, 0.1, 16, 1, sc, sc)
+    kc = torch.zeros(4, 2, 8, 128, dtype=torch.float8_e4m3fn, device=device)
+    q = torch.zeros(1, 8, 128, dtype=torch.bfloat16, device=device)
+    with pytest.raises(RuntimeError, match="block_size"):
+        pk.paged_attention_forward_fp8(torch.empty_like(q), q, kc, kc, bt, sl, 0.1, 8, 1, sc, sc)
+    with pytest.raises(RuntimeError, match="k_scale"):
+        pk.paged_attention_forward_fp8(torch.empty_like(q), q, kc, kc, bt, sl, 0.1, 8, 1,
+                                       torch.ones(3, device=device), sc)

@@ -5,6 +5,11 @@ inputs on a CUDA device); its pins are case lists and tolerances. Each oracle
 function is therefore checked against something that does not share its code:
 
 * bits_to_f32 / f32_to_bits  -- torch's own fp16/bf16 casts (library routine).
+* e4m3_to_f32 / f32_to_e4m3  -- torch.float8_e4m3fn casts (library routine) on
+  every code and on random, tie, subnormal and boundary values in range;
+  saturation beyond 448 by hand.
+* kv_store_slots_fp8         -- dequantised bytes are within half an e4m3 step
+  of x (relative 2^-4) at the right slots; untouched slots keep their poison.
 * kv_store                   -- the reference's Python scatter loop restated in
   torch (oracle/torch_ref.py), plus: untouched slots keep their poison, the
   reference test cases (start_pos 8 mid-block; seq_len {1,8,16,32,64}; 8 heads),
@@ -144,6 +149,46 @@ def test_copy_blocks():
     assert np.array_equal(kc[7], k0[3]) and np.array_equal(vc[2], v0[1])
     keep = [i for i in range(10) if i not in (7, 2)]
     assert np.array_equal(kc[keep], k0[keep]) and np.array_equal(vc[keep], v0[keep])
+
+
+def test_e4m3_matches_torch():
+    codes = np.arange(256, dtype=np.uint8)
+    want = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    got = O.e4m3_to_f32(codes)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    fin = ~np.isnan(want)
+    assert np.array_equal(got[fin], want[fin])
+    rng = np.random.default_rng(7)
+    pos = O._E4M3_POS
+    mids = (pos[:-1] + pos[1:]) / 2                       # exact ties between neighbours
+    x = np.concatenate([rng.standard_normal(20000) * 40, rng.standard_normal(2000) * 1e-2,
+                        mids, -mids, pos, -pos, [0.0, -0.0, 448.0, -448.0, 2.0 ** -10]])
+    x = x.astype(np.float32)
+    want = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    got = O.f32_to_e4m3(x)
+    assert np.array_equal(got, want)
+    assert np.array_equal(O.f32_to_e4m3(np.array([1e4, -500.0, np.nan], np.float32)),
+                          np.array([0x7E, 0xFE, 0x7F], np.uint8))
+
+
+def test_kv_store_slots_fp8():
+    rng = np.random.default_rng(8)
+    kc = np.full((6, 2, 4, 16), 0x33, np.uint8)
+    vc = kc.copy()
+    ks, vs = np.array([0.05, 0.2], np.float32), np.array([0.1, 0.01], np.float32)
+    k = rng.standard_normal((3, 2, 16)).astype(np.float32)
+    v = rng.standard_normal((3, 2, 16)).astype(np.float32)
+    O.kv_store_slots_fp8(kc, vc, k, v, np.array([5, -1, 22]), ks, vs)
+    kf, vf = O.fp8_pool_values(kc, ks), O.fp8_pool_values(vc, vs)
+    for t, slot in ((0, 5), (2, 22)):
+        b, o = divmod(slot, 4)
+        assert np.all(np.abs(kf[b, :, o] - k[t]) <= np.abs(k[t]) * 2.0 ** -4 + ks[:, None] * 2.0 ** -10)
+        assert np.all(np.abs(vf[b, :, o] - v[t]) <= np.abs(v[t]) * 2.0 ** -4 + vs[:, None] * 2.0 ** -10)
+    written = {(1, 1), (5, 2)}
+    for b in range(6):
+        for o in range(4):
+            if (b, o) not in written:
+                assert (kc[b, :, o] == 0x33).all() and (vc[b, :, o] == 0x33).all()
 
 
 def test_extract_and_load_kv():
