@@ -126,21 +126,25 @@ def bench_decode(args, w) -> dict:
         attend()
     torch.cuda.synchronize()
     # timed region: exactly `steps` steps, wall clock, sync on both sides
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        store()
+        attend()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall * 1e3 / args.steps
+    # per-call figures, outside the timed region
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
     for a, b in ev:
         store()
         a.record()
         attend()
         b.record()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
     attn_ms = [a.elapsed_time(b) for a, b in ev]
-    ms_step = wall * 1e3 / args.steps
     attn_avg = _launch_avg_ms(attend, args.steps)
-    store_ms = statistics.median(_events_ms(store, 20))
+    store_ms = _launch_avg_ms(store, args.steps)
     # cold-cache variant: read a 1 GiB buffer (> 256 MB MALL + L2) before each
     # call, so the KV rows come from HBM; a read leaves no dirty lines behind
     flush_buf = torch.ones(1 << 28, dtype=torch.int32, device=dev)
@@ -160,7 +164,7 @@ def bench_decode(args, w) -> dict:
             "attention_us_in_step_median": round(statistics.median(attn_ms) * 1e3, 2),
             "attention_us_cold_l2_flushed": round(cold * 1e3, 2),
             "attention_gbs_cold": round(w.attention_bytes() / (cold * 1e-3) / 1e9, 1),
-            "store_us_median": round(store_ms * 1e3, 2),
+            "store_us_mean": round(store_ms * 1e3, 2),
             "store_gbs": round(w.store_bytes() / (store_ms * 1e-3) / 1e9, 1),
             "attention_bytes": w.attention_bytes(),
             "store_bytes": w.store_bytes(),
@@ -232,10 +236,19 @@ def bench_prefill(args, w) -> dict:
         store()
         prefill()
         decode()
+    torch.cuda.synchronize()
+    # timed region: exactly `steps` steps, wall clock, sync on both sides
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        store()
+        prefill()
+        decode()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall * 1e3 / args.steps
+    # per-call figures, outside the timed region
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
     for a, b in ev:
         store()
         a.record()
@@ -243,9 +256,7 @@ def bench_prefill(args, w) -> dict:
         b.record()
         decode()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
     pf_step_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
-    ms_step = wall * 1e3 / args.steps
     pf_ms = _launch_avg_ms(prefill, args.steps)
     flops = w.prefill_flops()
     tflops = flops / (pf_ms * 1e-3) / 1e12
@@ -258,8 +269,8 @@ def bench_prefill(args, w) -> dict:
         "detail": {
             "prefill_us_mean": round(pf_ms * 1e3, 2),
             "prefill_us_in_step_mean": round(pf_step_ms * 1e3, 2),
-            "store_us_median": round(statistics.median(_events_ms(store, 20)) * 1e3, 2),
-            "decode_us_median": round(statistics.median(_events_ms(decode, 20)) * 1e3, 2),
+            "store_us_mean": round(_launch_avg_ms(store, args.steps) * 1e3, 2),
+            "decode_us_mean": round(_launch_avg_ms(decode, args.steps) * 1e3, 2),
             "prefill_flops": flops,
             "prefill_tokens": tp,
             "decode_seqs": len(w.chunk_lens) - npf,
