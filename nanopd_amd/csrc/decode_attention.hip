@@ -78,9 +78,10 @@ struct DecodeArgs {
   const u32x4* v_cache;
   const int32_t* block_tables;
   const int32_t* seq_lens;
-  float* part_acc;   // [S*kvh, max_parts, G, D]
-  float* part_ml;    // [S*kvh, max_parts, G, 2]
-  int* counters;     // [S*kvh] arrival counters of the fused merge
+  float* part_acc;   // [S*kvh, max_parts, G, D], then [S*kvh, max_groups, G, D]
+  float* part_ml;    // the same slots' (m, l): [..., G, 2]
+  int* counters;     // [S*kvh] arrival counters of the fused merge, then
+                     // [S*kvh, max_groups] those of its merge groups
   int* sched;        // fast path, more than 64 sequences: [1] number of work items
   const float* k_scale;   // fp8 pool: per-kv-head scales (element = e4m3 byte * scale)
   const float* v_scale;
@@ -92,6 +93,7 @@ struct DecodeArgs {
   int max_bps;
   int partition;     // PS, multiple of kStep, <= kMaxPartition
   int max_parts;
+  int max_groups;    // fast path: merge groups per unit (0: one-level merge)
   float scale_log2;  // softmax scale * log2(e)
   int64_t q_stride_seq, q_stride_head, out_stride_seq, out_stride_head;
 };
@@ -393,6 +395,51 @@ constexpr int kDppRor8 = 0x128;        // row_ror:8      -> lane ^ 8 within a ro
 constexpr int kDppHalfMirror = 0x141;  // row_half_mirror -> lane ^ 7 within 8
 constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
 constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int kDppMirror = 0x140;      // row_mirror      -> lane ^ 15 within a row of 16
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, false);
+}
+// Sum / max of an int over the whole wave (all 64 lanes active), returned as a
+// wave-uniform value: four DPP steps give every lane its row's total, then the
+// four row totals are read into scalars.
+__device__ __forceinline__ int wave_sum_i(int x) {
+  x += dpp_i<kDppXor1>(x);
+  x += dpp_i<kDppXor2>(x);
+  x += dpp_i<kDppHalfMirror>(x);
+  x += dpp_i<kDppMirror>(x);
+  return __builtin_amdgcn_readlane(x, 0) + __builtin_amdgcn_readlane(x, 16) +
+         __builtin_amdgcn_readlane(x, 32) + __builtin_amdgcn_readlane(x, 48);
+}
+__device__ __forceinline__ float uniform_f(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
+}
+__device__ __forceinline__ float lane_f(float x, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+}
+__device__ __forceinline__ float wave_sum_f(float x) {
+  x += dpp<kDppXor1>(x);
+  x += dpp<kDppXor2>(x);
+  x += dpp<kDppHalfMirror>(x);
+  x += dpp<kDppMirror>(x);
+  return (lane_f(x, 0) + lane_f(x, 16)) + (lane_f(x, 32) + lane_f(x, 48));
+}
+__device__ __forceinline__ float wave_max_f(float x) {
+  x = fmaxf(x, dpp<kDppXor1>(x));
+  x = fmaxf(x, dpp<kDppXor2>(x));
+  x = fmaxf(x, dpp<kDppHalfMirror>(x));
+  x = fmaxf(x, dpp<kDppMirror>(x));
+  return fmaxf(fmaxf(lane_f(x, 0), lane_f(x, 16)), fmaxf(lane_f(x, 32), lane_f(x, 48)));
+}
+__device__ __forceinline__ int wave_max_i(int x) {
+  x = max(x, dpp_i<kDppXor1>(x));
+  x = max(x, dpp_i<kDppXor2>(x));
+  x = max(x, dpp_i<kDppHalfMirror>(x));
+  x = max(x, dpp_i<kDppMirror>(x));
+  return max(max(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
+             max(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
+}
 
 // Coordinates of lane j (0..15) in the basis of the stage partner masks
 // m = (8, 7, 2, 1) of GF(2)^4: j = a1*8 ^ a2*7 ^ a3*2 ^ a4*1, so a1 = j3,
@@ -451,13 +498,19 @@ using npd::st_coherent2;
 //      with kMergeFlight partitions of loads in flight. The loads are
 //      unconditional (clamped to the chunk's last partition, weight 0), so
 //      each wait covers exactly one batch.
+// The partials merged are the nparts consecutive slots from slot0. dst >= 0
+// (wave-uniform): the result is itself a partial (accumulator and (m, l)
+// relative to the merged max, not normalised), written to slot dst; else the
+// normalised rows of (sequence s, kv-head kh) go to the output.
 constexpr int kMergeFlight = 4;
+constexpr int kMergeGroup = 16;   // partitions per first-level merge (long contexts)
 template <class TT, int G>
-__device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int unit, int s, int kh,
-                                                int nparts, int lane, float* s_w, float oscale) {
+__device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int64_t slot0, int nparts,
+                                                int64_t dst, int s, int kh, int lane, float* s_w,
+                                                float oscale) {
   constexpr int D = 128, GP = pow2ceil(G), CH = D / 8;
   constexpr int OWN = (G * CH + 63) / 64;   // (head, chunk) pairs per lane
-  const int64_t base = (int64_t)unit * a.max_parts;
+  auto slot = [&](int p) -> int64_t { return slot0 + p; };
   // the first batch of partial rows of the lane's first (head, chunk) pair is
   // requested together with the (m, l) values: it does not depend on them
   const int n0 = nparts < 64 ? nparts : 64;
@@ -468,7 +521,7 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int unit, i
 #pragma unroll
     for (int q = 0; q < kMergeFlight; ++q) {
       const int pq = p0 + (q0 + q < n ? q0 + q : n - 1);
-      const float* src = a.part_acc + ((base + pq) * G + h) * D + c * 2;
+      const float* src = a.part_acc + (slot(pq) * G + h) * D + c * 2;
 #pragma unroll
       for (int k2 = 0; k2 < 4; ++k2) ld_coherent2(src + k2 * 32, x[q][2 * k2], x[q][2 * k2 + 1]);
     }
@@ -479,7 +532,7 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int unit, i
   for (int h = 0; h < G; ++h) { m0[h] = -INFINITY; l0[h] = 0.f; }
   if (lane < nparts) {
 #pragma unroll
-    for (int h = 0; h < G; ++h) ld_coherent2(a.part_ml + ((base + lane) * G + h) * 2, m0[h], l0[h]);
+    for (int h = 0; h < G; ++h) ld_coherent2(a.part_ml + (slot(lane) * G + h) * 2, m0[h], l0[h]);
   }
 #pragma unroll
   for (int h = 0; h < G; ++h) { M[h] = m0[h]; L[h] = 0.f; }
@@ -487,14 +540,13 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int unit, i
 #pragma unroll
     for (int h = 0; h < G; ++h) {
       float mp, lp;
-      ld_coherent2(a.part_ml + ((base + p) * G + h) * 2, mp, lp);
+      ld_coherent2(a.part_ml + (slot(p) * G + h) * 2, mp, lp);
       M[h] = fmaxf(M[h], mp);
     }
   }
+  // M and L are wave-uniform (held in scalar registers)
 #pragma unroll
-  for (int h = 0; h < G; ++h)
-#pragma unroll
-    for (int x = 1; x < 64; x <<= 1) M[h] = fmaxf(M[h], shfl_xor(M[h], x));
+  for (int h = 0; h < G; ++h) M[h] = uniform_f(wave_max_f(M[h]));
   float o[OWN][8];
 #pragma unroll
   for (int k = 0; k < OWN; ++k)
@@ -504,14 +556,15 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int unit, i
     const int p = p0 + lane;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      float w = 0.f;
+      float w = 0.f, lw = 0.f;
       if (p < nparts) {
         float mp = m0[h], lp = l0[h];
-        if (p0 > 0) ld_coherent2(a.part_ml + ((base + p) * G + h) * 2, mp, lp);
+        if (p0 > 0) ld_coherent2(a.part_ml + (slot(p) * G + h) * 2, mp, lp);
         w = __builtin_amdgcn_exp2f(mp - M[h]);
-        L[h] = fmaf(lp, w, L[h]);
+        lw = lp * w;
       }
       s_w[lane * GP + h] = w;
+      L[h] = uniform_f(L[h] + wave_sum_f(lw));
     }
     __syncthreads();
     const int n = nparts - p0 < 64 ? nparts - p0 : 64;
@@ -534,17 +587,24 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int unit, i
     __syncthreads();
   }
 #pragma unroll
-  for (int h = 0; h < G; ++h)
-#pragma unroll
-    for (int x = 1; x < 64; x <<= 1) L[h] += shfl_xor(L[h], x);
-#pragma unroll
   for (int k = 0; k < OWN; ++k) {
     const int idx = lane + 64 * k;
     if (idx < G * CH) {
       const int h = idx / CH, c = idx % CH;
-      store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + c * 8,
-                     o[k], oscale / L[h]);
+      if (dst >= 0) {
+        // same layout as a published partition: [dim pair][chunk][2]
+        float* row = a.part_acc + (dst * G + h) * D + c * 2;
+#pragma unroll
+        for (int k2 = 0; k2 < 4; ++k2) st_coherent2(row + k2 * 32, o[k][2 * k2], o[k][2 * k2 + 1]);
+      } else {
+        store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + c * 8,
+                       o[k], oscale / L[h]);
+      }
     }
+  }
+  if (dst >= 0 && lane == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) st_coherent2(a.part_ml + (dst * G + h) * 2, M[h], L[h]);
   }
 }
 
@@ -889,9 +949,23 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
   // 16 lanes of a row write 128 contiguous bytes per store; after the row
   // reduction every row of the wave holds the sums, so row r stores heads
   // r, r + 4, ...
+  //
+  // Long contexts (merge groups on) merge in two levels. The last of each
+  // group of kMergeGroup partitions to arrive merges the group into the
+  // group's result slot (a partition that is a group of one publishes there
+  // directly); the last group to finish merges the group results into the
+  // output. Group merges run as groups complete, so the merge left after the
+  // last partition covers one group and the group results, not every
+  // partition. Group result slots follow the partition slots of all units.
   const int64_t ubase = (int64_t)unit * a.max_parts;
+  const bool grouped = a.max_groups > 0 && nparts > kMergeGroup;
+  const int ngroups = (nparts + kMergeGroup - 1) / kMergeGroup;
+  const int g = part / kMergeGroup;
+  const int gsize = min(kMergeGroup, nparts - g * kMergeGroup);
+  const int64_t gbase =
+      (int64_t)a.num_seqs * a.num_kv_heads * a.max_parts + (int64_t)unit * a.max_groups;
   {
-    const int64_t base = ubase + part;
+    const int64_t base = grouped && gsize == 1 ? gbase + g : ubase + part;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
       if ((h & 3) != r) continue;
@@ -899,26 +973,45 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
 #pragma unroll
       for (int k = 0; k < 4; ++k) st_coherent2(dst + k * 32, acc[h][2 * k], acc[h][2 * k + 1]);
     }
-  }
-  if (lane < 16) {
-    const int64_t base = ubase + part;
-    if (j == 0) {
+    if (lane < 16 && j == 0) {
 #pragma unroll
-      for (int h = 0; h < G; ++h) {
-        st_coherent2(a.part_ml + (base * G + h) * 2, m[h], l[h]);
-      }
+      for (int h = 0; h < G; ++h) st_coherent2(a.part_ml + (base * G + h) * 2, m[h], l[h]);
     }
   }
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);   // every store of this wave has completed
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  int ticket = 0;
-  if (lane == 0)
-    ticket = __hip_atomic_fetch_add(a.counters + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  ticket = __shfl(ticket, 0, 64);
-  if (ticket != nparts - 1) return;
-  merge_unit_fast<TT, G>(a, unit, s, kh, nparts, lane, s_p, out_scale);
-  if (lane == 0) __hip_atomic_store(a.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  auto ticket_of = [&](int* counter) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);   // every store of this wave has completed
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    int t = 0;
+    if (lane == 0) t = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __shfl(t, 0, 64);
+  };
+  // one merge call site, so that its registers are allocated once
+  int* counter = a.counters + unit;
+  int64_t slot0 = ubase, dst = -1;
+  int n = nparts;
+  if (grouped) {
+    if (gsize > 1) {   // first level: this partition's group
+      counter = a.counters + a.num_seqs * a.num_kv_heads + unit * a.max_groups + g;
+      slot0 = ubase + g * kMergeGroup;
+      n = gsize;
+      dst = gbase + g;
+    } else {
+      slot0 = gbase;
+      n = ngroups;
+    }
+  }
+  for (;;) {
+    if (ticket_of(counter) != n - 1) return;
+    merge_unit_fast<TT, G>(a, slot0, n, dst, s, kh, lane, s_p, dst >= 0 ? 1.f : out_scale);
+    if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (dst < 0) return;
+    // second level: the group results
+    counter = a.counters + unit;
+    slot0 = gbase;
+    n = ngroups;
+    dst = -1;
+  }
 }
 
 
@@ -940,12 +1033,14 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
   int unit, part;
   if (a.num_seqs <= kInlineSchedMax) {
     // Small batch: every workgroup derives its item from seq_lens alone, in
-    // longest-processing-time order, with scalar loops over ballots:
+    // longest-processing-time order:
     //   A. the full partitions (PS tokens) of every sequence but its last,
     //      level by level (partition 0 of every unit, then partition 1, ...);
+    //      the level of an item is found by binary search over the counts of
+    //      items before each level (DPP wave sums);
     //   B. the last partition of every sequence (PS tokens or fewer; an empty
     //      context has one item that writes zeros), longest first, in 16-token
-    //      buckets.
+    //      buckets (binary search over ballot counts).
     // Items past the resident capacity of the GPU start as earlier ones end,
     // so the ones dispatched last are the shortest.
     const int lane = threadIdx.x;
@@ -967,33 +1062,40 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
       return __builtin_ctzll(__ballot(((m >> lane) & 1) && rank == k));
     };
+    // items before level p: kvh * sum over sequences of min(full, p)
+    auto before = [&](int p) -> int { return wave_sum_i(full < p ? full : p) * kvh; };
+    const int maxfull = wave_max_i(full);
     int id = blockIdx.x, seq = -1;
     part = 0;
-    for (int p = 0;; ++p) {
-      const uint64_t m = __ballot(full > p);
-      if (m == 0) break;
-      const int c = __popcll(m) * kvh;
-      if (id < c) {
-        seq = nth(m, id / kvh);
-        unit = seq * kvh + id % kvh;
-        part = p;
-        break;
+    const int nfull = before(maxfull);
+    if (id < nfull) {
+      // level of item id: the last p with before(p) <= id (binary search)
+      int lo = 0, hi = maxfull - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (before(mid) <= id) lo = mid; else hi = mid - 1;
       }
-      id -= c;
+      id -= before(lo);
+      seq = nth(__ballot(full > lo), id / kvh);
+      unit = seq * kvh + id % kvh;
+      part = lo;
+    } else {
+      id -= nfull;
     }
     if (seq < 0) {
-      for (int b = a.partition >> 4; b >= 0; --b) {
-        const uint64_t m = __ballot(valid && bucket == b);
-        const int c = __popcll(m) * kvh;
-        if (id < c) {
-          seq = nth(m, id / kvh);
-          unit = seq * kvh + id % kvh;
-          part = __builtin_amdgcn_readlane(full, seq);
-          break;
-        }
-        id -= c;
+      // items in buckets >= b, non-increasing in b; item id is in the last
+      // bucket b with from(b) > id (binary search)
+      auto from = [&](int b) -> int { return __popcll(__ballot(valid && bucket >= b)) * kvh; };
+      if (id >= from(0)) return;   // past the last item
+      int lo = 0, hi = a.partition >> 4;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (from(mid) > id) lo = mid; else hi = mid - 1;
       }
-      if (seq < 0) return;   // past the last item
+      id -= from(lo + 1);
+      seq = nth(__ballot(valid && bucket == lo), id / kvh);
+      unit = seq * kvh + id % kvh;
+      part = __builtin_amdgcn_readlane(full, seq);
     }
   } else {
     if ((int)blockIdx.x >= a.sched[1]) return;
@@ -1005,7 +1107,7 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
 }
 
 // Builds the work list of decode_d128_kernel (one workgroup):
-//   - zeroes the per-unit merge counters;
+//   - zeroes the merge counters (per unit and per merge group);
 //   - counting-sorts the sequences by partition count, descending;
 //   - lists the items of each sequence in that order, unit by unit
 //     (item = (unit, partition)); a sequence with no context gets one item,
@@ -1040,7 +1142,7 @@ __global__ __launch_bounds__(kSchedThreads) void decode_schedule_kernel(DecodeAr
     __syncthreads();
     return pre + inc - c;   // exclusive prefix; pre + inc is the inclusive one
   };
-  for (int u = tid; u < units; u += kSchedThreads) a.counters[u] = 0;
+  for (int u = tid; u < units * (1 + a.max_groups); u += kSchedThreads) a.counters[u] = 0;
   s_hist[tid] = 0;
   __syncthreads();
   for (int sq = tid; sq < num_seqs; sq += kSchedThreads) {
@@ -1208,6 +1310,14 @@ int dispatch_d(int64_t d, int g, const DecodeArgs& a, int64_t units, hipStream_t
   }
 }
 
+// Merge groups per unit of the fast path's two-level merge (0: one level):
+// used when a unit has more than one group of partitions and the counter
+// region holds a counter per unit and per group.
+int64_t merge_groups(bool fast, int64_t units, int64_t parts) {
+  const int64_t ng = (parts + kMergeGroup - 1) / kMergeGroup;
+  return fast && parts > kMergeGroup && units * (1 + ng) <= npd::kMaxCounters ? ng : 0;
+}
+
 }  // namespace
 
 extern "C" int64_t npd_paged_attention_workspace_size(int64_t num_seqs, int64_t num_heads,
@@ -1221,11 +1331,14 @@ extern "C" int64_t npd_paged_attention_workspace_size(int64_t num_seqs, int64_t 
   const int ps = choose_partition(num_seqs, num_kv_heads, head_dim, block_size, max_ctx);
   const int64_t parts = (max_ctx + ps - 1) / ps;
   if (parts <= 1 && !use_fast_path(head_dim, block_size, num_seqs)) return 0;
-  const int64_t partials = num_seqs * num_heads * parts * (head_dim + 2) * (int64_t)sizeof(float);
-  if (!use_fast_path(head_dim, block_size, num_seqs)) return npd::kCounterBytes + partials;
-  // fast path: counter region, item count (16 B), work list, partials
+  if (!use_fast_path(head_dim, block_size, num_seqs))
+    return npd::kCounterBytes + num_seqs * num_heads * parts * (head_dim + 2) * (int64_t)sizeof(float);
+  // fast path: counter region, item count (16 B), work list, partials of the
+  // partitions and of the merge groups
   const int64_t units = num_seqs * num_kv_heads;
-  return (npd::kCounterBytes + 16 + units * parts * 8 + 255) / 256 * 256 + partials;
+  const int64_t slots = parts + merge_groups(true, units, parts);
+  return (npd::kCounterBytes + 16 + units * parts * 8 + 255) / 256 * 256 +
+         num_seqs * num_heads * slots * (head_dim + 2) * (int64_t)sizeof(float);
 }
 
 namespace {
@@ -1320,7 +1433,8 @@ int attention_impl(void* out, const void* query, const void* key_cache, const vo
   a.sched = wsb ? reinterpret_cast<int*>(wsb + kCounterBytes) : nullptr;
   a.items = wsb ? reinterpret_cast<int2*>(wsb + kCounterBytes + 16) : nullptr;
   a.part_acc = wsb ? reinterpret_cast<float*>(wsb + part_off) : nullptr;
-  a.part_ml = wsb ? a.part_acc + units * max_parts * g * head_dim : nullptr;
+  a.max_groups = (int)merge_groups(fast_ws, units, max_parts);
+  a.part_ml = wsb ? a.part_acc + units * (max_parts + a.max_groups) * g * head_dim : nullptr;
   a.num_kv_heads = (int)num_kv_heads;
   a.num_seqs = (int)num_seqs;
   a.block_size = (int)block_size;

@@ -105,10 +105,12 @@ def test_workspace_size():
     # fast path (head_dim 128): the fixed 1 MiB counter region every workspace
     # starts with, a 16-byte item count, an 8-byte (unit, partition) work-list
     # entry per possible partition (padded to 256 bytes), then fp32 partials
-    # (G*D + 2G floats per partition).
+    # (G*D + 2G floats per partition and, past 16 partitions, per group of 16
+    # partitions: the first level of the two-level merge).
     def fast(S, H, kvh, P):
         units = S * kvh
-        return (2**20 + 16 + units * P * 8 + 255) // 256 * 256 + S * H * P * 130 * 4
+        groups = (P + 15) // 16 if P > 16 else 0
+        return (2**20 + 16 + units * P * 8 + 255) // 256 * 256 + S * H * (P + groups) * 130 * 4
     # 1024 seqs x 8 kv heads x 256 tokens: one partition of 256 each
     assert lib.npd_paged_attention_workspace_size(1024, 32, 8, 128, 16, 16) == fast(1024, 32, 8, 1)
     # 64 seqs x 8 kv heads x 256 tokens: 512 waves -> partitions of 64 (4 each)
@@ -117,6 +119,12 @@ def test_workspace_size():
     assert lib.npd_paged_attention_workspace_size(8, 32, 8, 128, 16, 2048) == fast(8, 32, 8, 128)
     # 1 seq x 8 kv heads x 4k tokens: too few waves -> partitions of 64
     assert lib.npd_paged_attention_workspace_size(1, 32, 8, 128, 16, 256) == fast(1, 32, 8, 64)
+    # 4096 seqs x 8 kv heads x 32k tokens: 128 partitions of 256, but a counter
+    # per unit and per group (32768 x 9) would not fit the 262144 counters ->
+    # one level, no group partials; 2048 seqs (16384 x 9 counters) fit
+    n = lib.npd_paged_attention_workspace_size(4096, 32, 8, 128, 16, 2048)
+    assert n == fast(4096, 32, 8, 128) - 4096 * 32 * 8 * 130 * 4
+    assert lib.npd_paged_attention_workspace_size(2048, 32, 8, 128, 16, 2048) == fast(2048, 32, 8, 128)
     # generic path (head_dim 64): partitions of 256 below 4096 waves
     n = lib.npd_paged_attention_workspace_size(2, 8, 8, 64, 16, 64)
     assert n == 2**20 + 2 * 8 * 4 * (64 + 2) * 4

@@ -101,6 +101,37 @@ def test_group_sizes_and_head_dims(device, dtype, D, G):
     check(run(*args, 16), q, kc, vc, bt, sl, scale)
 
 
+@pytest.mark.parametrize("lens", [[1024], [1025], [2048], [2049], [100, 1025, 3000, 5000, 17]])
+def test_two_level_merge_group_boundaries(device, lens):
+    """Few sequences take 64-token partitions, and a (sequence, kv-head) with
+    more than 16 partitions merges in two levels: groups of 16, then the group
+    results. Lengths at the group boundaries: 16 partitions (one level), 17
+    (the last group has one partition, published as its group's result), 32,
+    33, and a mix of one- and two-level units."""
+    args = make_inputs(len(lens), 32, 8, 128, lens, 16, torch.bfloat16, device, seed=sum(lens))
+    q, kc, vc, bt, sl, scale, mb = args
+    check(run(*args, 16), q, kc, vc, bt, sl, scale)
+
+
+def test_two_level_merge_many_groups(device):
+    """1025 partitions of 64 tokens in one unit: 65 group results, so the
+    second level reads them in two 64-lane chunks."""
+    args = make_inputs(1, 4, 2, 128, [65537], 16, torch.bfloat16, device, seed=7)
+    q, kc, vc, bt, sl, scale, mb = args
+    check(run(*args, 16), q, kc, vc, bt, sl, scale)
+
+
+def test_two_level_merge_scheduled_path(device):
+    """More than 64 sequences (the work list built by the schedule kernel) with
+    256-token partitions and up to 32 of them per unit."""
+    g = torch.Generator().manual_seed(70)
+    lens = torch.randint(1, 8193, (70,), generator=g).tolist()
+    lens[3] = 8192
+    args = make_inputs(70, 4, 2, 128, lens, 16, torch.bfloat16, device, seed=70)
+    q, kc, vc, bt, sl, scale, mb = args
+    check(run(*args, 16), q, kc, vc, bt, sl, scale)
+
+
 def test_output_shape_and_int64_tables_raise(device):
     args = make_inputs(4, 8, 8, 128, [10] * 4, 16, torch.float16, device)
     q, kc, vc, bt, sl, scale, mb = args
