@@ -41,14 +41,23 @@ constexpr int kStep = 16;            // tokens per step
 #ifndef NPD_DECODE_NT
 #define NPD_DECODE_NT 1
 #endif
-#ifndef NPD_DECODE_PV_DOT2
-#define NPD_DECODE_PV_DOT2 1
-#endif
 constexpr int kRing = NPD_DECODE_RING;   // fast path: K/V steps in flight per wave
 #ifndef NPD_FAST_MAX_PARTITION
-#define NPD_FAST_MAX_PARTITION 256
+#define NPD_FAST_MAX_PARTITION 2048
 #endif
 constexpr int kFastMaxPartition = NPD_FAST_MAX_PARTITION;   // fast path: tokens per wave, max
+// fast path: at most this many scores (tokens x padded heads) per wave: a
+// wave's scores then take at most 16.5 KB of LDS, and 9 such waves fit a CU
+// (2304 resident on 256 CUs, above kFastMinItems)
+constexpr int kFastMaxScores = 4096;
+// fast path: the partition is chosen to give at least this many work items
+// at the longest context (5 per CU of a 256-CU device)
+constexpr int64_t kFastMinItems = 1280;
+// FP8 pools: a row is half the bytes, so a wave has half the bytes in flight
+// and more, shorter items keep HBM busy: at least 4096 items, partitions of at
+// most 256 tokens
+constexpr int64_t kFastMinItemsFp8 = 4096;
+constexpr int kFastMaxPartitionFp8 = 256;
 #ifndef NPD_DECODE_INLINE_SCHED_MAX
 #define NPD_DECODE_INLINE_SCHED_MAX 64
 #endif
@@ -91,7 +100,7 @@ struct DecodeArgs {
   int block_size;
   int num_blocks;
   int max_bps;
-  int partition;     // PS, multiple of kStep, <= kMaxPartition
+  int partition;     // PS, multiple of kStep, <= kMaxPartition (fast path: kFastMaxPartition)
   int max_parts;
   int max_groups;    // fast path: merge groups per unit (0: one-level merge)
   float scale_log2;  // softmax scale * log2(e)
@@ -654,6 +663,9 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
   constexpr int HELD = NV >> NH;
   constexpr int BS = 16 * SPB;
   constexpr int NBUF = kRing;           // steps in flight per pass
+  // pass 3 on packed 2-byte probabilities with v_dot2 (FP8 pools: their short
+  // partitions leave LDS room for the packed copy), else on the fp32 ones
+  constexpr bool kDot2 = kF8;
   constexpr int MAXT = kFastMaxPartition + 16 * NBUF;   // tokens incl. ring padding
 
   (void)MAXT;
@@ -701,15 +713,17 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
       qv[h] = hh < G ? *reinterpret_cast<const u32x4*>(qb + hh * a.q_stride_head) : u32x4{0, 0, 0, 0};
     }
   }
-  // lane e holds the block id of the e-th block of the partition (clamped);
-  // lanes past the partition hold block 0
-  int myblk = 0;
+  // lane e holds the block ids of blocks e and 64 + e of the partition
+  // (clamped; at most 128 blocks: kFastMaxPartition / 16); entries past the
+  // partition hold block 0
+  static_assert(kFastMaxPartition / 16 <= 128, "two block ids per lane");
+  int myblk0 = 0, myblk1 = 0;
   {
     const int nb = (ntok + BS - 1) / BS;
-    if (lane < nb) {
-      int b = a.block_tables[(int64_t)s * a.max_bps + b0 + lane];
-      myblk = b < 0 ? 0 : (b >= a.num_blocks ? a.num_blocks - 1 : b);
-    }
+    const int32_t* row = a.block_tables + (int64_t)s * a.max_bps + b0;
+    auto clamp_blk = [&](int b) { return b < 0 ? 0 : (b >= a.num_blocks ? a.num_blocks - 1 : b); };
+    if (lane < nb) myblk0 = clamp_blk(row[lane]);
+    if (lane + 64 < nb) myblk1 = clamp_blk(row[lane + 64]);
   }
   const int voff = (r * 16) + j;   // offset (in lane chunks) of the lane's chunk: slot i is token i*4 + r
   // scores in log2 units (times the K scale of an fp8 pool); output scale
@@ -719,7 +733,8 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
   const int64_t head_rows = (int64_t)kh * BS;            // rows of head kh in a block
   const int64_t blk_rows = (int64_t)a.num_kv_heads * BS; // rows per block
   auto step_base = [&](int st) -> int64_t {              // chunk index of the step's first row
-    const int blk = __builtin_amdgcn_readlane(myblk, (st / SPB) & 63);
+    const int bi = st / SPB;   // wave-uniform
+    const int blk = __builtin_amdgcn_readlane(bi < 64 ? myblk0 : myblk1, bi & 63);
     return ((int64_t)blk * blk_rows + head_rows + (st % SPB) * 16) * 16;
   };
   // K/V rows are read once per call: nontemporal loads keep them from
@@ -806,7 +821,7 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
   for (int h = 0; h < G; ++h)
 #pragma unroll
     for (int x = 1; x < 64; x <<= 1) m[h] = fmaxf(m[h], shfl_xor(m[h], x));
-#if NPD_DECODE_PV_DOT2
+  if constexpr (kDot2) {
   // Probabilities of the token pair (8q + rr, 8q + 4 + rr) of each step, packed
   // as two 2-byte values per head: the pair a pass-3 lane multiplies into one
   // v_dot2 with V. l sums the rounded values, so the normalisation matches them.
@@ -820,7 +835,7 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
       s_pp[pi * GP + h] = ua | (ub << 16);
     }
   }
-#else
+  } else {
   for (int t = lane; t < ntl; t += 64) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -829,7 +844,7 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
       l[h] += p;
     }
   }
-#endif
+  }
 #pragma unroll
   for (int h = 0; h < G; ++h)
 #pragma unroll
@@ -851,7 +866,7 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
       for (int i = 0; i < 4; ++i)
         if (st * 16 + i * 4 + r >= ntok) vbuf[i] = u32x4{0, 0, 0, 0};
     }
-#if NPD_DECODE_PV_DOT2
+  if constexpr (kDot2) {
     // slots 2q and 2q+1 hold tokens 8q + r and 8q + 4 + r: pack their values
     // per dim (v_perm) and take both products with one v_dot2
 #pragma unroll
@@ -882,7 +897,7 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
         }
       }
     }
-#else
+  } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int tl = st * 16 + i * 4 + r;
@@ -908,7 +923,7 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
         }
       }
     }
-#endif
+  }
   };
   {
     auto round = [&](int st0) {
@@ -1020,16 +1035,14 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
 // consecutive -- so long units start together, finish and merge early, and the
 // short ones fill the tail. The grid is sized for the most items possible;
 // workgroups past the list (all at the end of the grid) exit at once.
+// LDS is dynamic, sized for the launch's partition (fast_lds_bytes).
 template <class TT, int G, int SPB, bool kF8>
 __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
   constexpr int GP = pow2ceil(G);
-  constexpr int MAXT = kFastMaxPartition + 16 * kRing;
-  __shared__ __attribute__((aligned(16))) float s_p[MAXT * GP];
-#if NPD_DECODE_PV_DOT2
-  __shared__ __attribute__((aligned(16))) uint32_t s_pp[MAXT / 2 * GP];
-#else
-  uint32_t* s_pp = nullptr;
-#endif
+  extern __shared__ __attribute__((aligned(16))) float s_dyn[];
+  float* s_p = s_dyn;   // [partition + ring padding][GP] scores
+  uint32_t* s_pp =   // [(partition + ring padding) / 2][GP] packed probabilities (kDot2)
+      kF8 ? reinterpret_cast<uint32_t*>(s_dyn + (a.partition + 16 * kRing) * GP) : nullptr;
   int unit, part;
   if (a.num_seqs <= kInlineSchedMax) {
     // Small batch: every workgroup derives its item from seq_lens alone, in
@@ -1203,32 +1216,50 @@ bool use_fast_path(int64_t head_dim, int64_t block_size, int64_t num_seqs) {
          (block_size & (block_size - 1)) == 0 && num_seqs <= kSchedMaxSeqs;
 }
 
-// Partition length (tokens per wave). The fast path takes the largest of
-// 256 / 128 / 64 that still gives >= 4096 waves for the longest context (256
-// CUs x 16 resident waves), never below the block size; the generic path uses
-// 512 or 256. The workspace is sized with the same rule.
-int choose_partition(int64_t num_seqs, int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
-                     int64_t max_ctx) {
+// Partition length (tokens per wave). The fast path takes the longest of
+// 2048 / 1024 / ... / 64 tokens (at most kFastMaxScores / GP) that gives
+// kFastMinItems work items at the longest context, never below the block
+// size. Long partitions cost less per token: each work item pays a fixed
+// latency (work-list lookup, q load, the softmax pass over LDS, publishing
+// its partial) that the streaming loops of other waves hide only in part,
+// and 1280 waves with two 16-token steps in flight each still keep HBM busy.
+// FP8 pools follow kFastMinItemsFp8 / kFastMaxPartitionFp8. The generic path
+// uses 512 or 256. The workspace is sized with the same rule.
+int choose_partition(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                     int64_t block_size, int64_t max_ctx, bool fp8) {
   const int64_t units = num_seqs * num_kv_heads;
   if (use_fast_path(head_dim, block_size, num_seqs)) {
 #ifdef NPD_DECODE_PARTITION
     if (NPD_DECODE_PARTITION >= block_size) return NPD_DECODE_PARTITION;
 #endif
-    for (int ps = 256; ps >= 64; ps >>= 1) {
+    const int gp = pow2ceil((int)(num_heads / num_kv_heads));
+    const int top = fp8 ? kFastMaxPartitionFp8 : kFastMaxPartition;
+    const int64_t min_items = fp8 ? kFastMinItemsFp8 : kFastMinItems;
+    for (int ps = top; ps >= 64; ps >>= 1) {
       if (ps <= block_size) return (int)block_size;
-      if (units * ((max_ctx + ps - 1) / ps) >= 4096) return ps;
+      if (ps * gp > kFastMaxScores) continue;
+      if (units * ((max_ctx + ps - 1) / ps) >= min_items) return ps;
     }
     return block_size > 64 ? (int)block_size : 64;
   }
   return units * ((max_ctx + 511) / 512) >= 4096 ? 512 : 256;
 }
 
+// Dynamic LDS of decode_d128_kernel for a partition: scores (fp32) of every
+// token of the partition plus the ring padding, and their packed bf16/fp16
+// probabilities when pass 3 uses v_dot2 (FP8 pools).
+int64_t fast_lds_bytes(int partition, int g, bool fp8) {
+  const int64_t t = partition + 16 * kRing;
+  const int64_t gp = pow2ceil(g);
+  return t * gp * 4 + (fp8 ? t / 2 * gp * 4 : 0);
+}
+
 template <class TT, int G, int SPB, bool kF8 = false>
 int launch_fast_bs(const DecodeArgs& a, int num_seqs, int64_t max_items, hipStream_t st) {
   if (num_seqs > kInlineSchedMax)
     hipLaunchKernelGGL(decode_schedule_kernel, dim3(1), dim3(kSchedThreads), 0, st, a, num_seqs);
-  hipLaunchKernelGGL((decode_d128_kernel<TT, G, SPB, kF8>), dim3((unsigned)max_items), dim3(64), 0,
-                     st, a);
+  hipLaunchKernelGGL((decode_d128_kernel<TT, G, SPB, kF8>), dim3((unsigned)max_items), dim3(64),
+                     (unsigned)fast_lds_bytes(a.partition, G, kF8), st, a);
   return NPD_OK;
 }
 
@@ -1328,17 +1359,30 @@ extern "C" int64_t npd_paged_attention_workspace_size(int64_t num_seqs, int64_t 
       max_blocks_per_seq <= 0)
     return 0;
   const int64_t max_ctx = block_size * max_blocks_per_seq;
-  const int ps = choose_partition(num_seqs, num_kv_heads, head_dim, block_size, max_ctx);
-  const int64_t parts = (max_ctx + ps - 1) / ps;
-  if (parts <= 1 && !use_fast_path(head_dim, block_size, num_seqs)) return 0;
-  if (!use_fast_path(head_dim, block_size, num_seqs))
+  if (!use_fast_path(head_dim, block_size, num_seqs)) {
+    const int ps =
+        choose_partition(num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_ctx, false);
+    const int64_t parts = (max_ctx + ps - 1) / ps;
+    if (parts <= 1) return 0;
     return npd::kCounterBytes + num_seqs * num_heads * parts * (head_dim + 2) * (int64_t)sizeof(float);
+  }
   // fast path: counter region, item count (16 B), work list, partials of the
-  // partitions and of the merge groups
+  // partitions and of the merge groups; enough for a 2-byte pool and, for the
+  // block sizes the FP8 entry point takes, an FP8 pool (whose partitions may
+  // be shorter)
   const int64_t units = num_seqs * num_kv_heads;
-  const int64_t slots = parts + merge_groups(true, units, parts);
-  return (npd::kCounterBytes + 16 + units * parts * 8 + 255) / 256 * 256 +
-         num_seqs * num_heads * slots * (head_dim + 2) * (int64_t)sizeof(float);
+  auto need = [&](bool fp8) {
+    const int ps =
+        choose_partition(num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_ctx, fp8);
+    const int64_t parts = (max_ctx + ps - 1) / ps;
+    const int64_t slots = parts + merge_groups(true, units, parts);
+    return (npd::kCounterBytes + 16 + units * parts * 8 + 255) / 256 * 256 +
+           num_seqs * num_heads * slots * (head_dim + 2) * (int64_t)sizeof(float);
+  };
+  const int64_t n = need(false);
+  if (block_size != 16 && block_size != 32) return n;
+  const int64_t n8 = need(true);
+  return n8 > n ? n8 : n;
 }
 
 namespace {
@@ -1396,11 +1440,14 @@ int attention_impl(void* out, const void* query, const void* key_cache, const vo
                 fp8 ? 8 : 16);
 
   const int64_t max_ctx = block_size * max_blocks_per_seq;
-  const int partition = choose_partition(num_seqs, num_kv_heads, head_dim, block_size, max_ctx);
-  if (partition > kMaxPartition ||
-      (use_fast_path(head_dim, block_size, num_seqs) && partition > kFastMaxPartition))
-    return fail(NPD_E_INVALID, "%s: block_size %lld is above %d", name, (long long)block_size,
-                use_fast_path(head_dim, block_size, num_seqs) ? kFastMaxPartition : kMaxPartition);
+  const int partition =
+      choose_partition(num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_ctx, fp8);
+  {
+    const int limit = use_fast_path(head_dim, block_size, num_seqs) ? kFastMaxPartition : kMaxPartition;
+    if (partition > limit)
+      return fail(NPD_E_INVALID, "%s: block_size %lld is above %d", name, (long long)block_size,
+                  limit);
+  }
   const int64_t max_parts = (max_ctx + partition - 1) / partition;
   if (max_parts > 65535) return fail(NPD_E_INVALID, "%s: context too long", name);
   const int64_t need = npd_paged_attention_workspace_size(num_seqs, num_heads, num_kv_heads,

@@ -111,20 +111,38 @@ def test_workspace_size():
         units = S * kvh
         groups = (P + 15) // 16 if P > 16 else 0
         return (2**20 + 16 + units * P * 8 + 255) // 256 * 256 + S * H * (P + groups) * 130 * 4
-    # 1024 seqs x 8 kv heads x 256 tokens: one partition of 256 each
-    assert lib.npd_paged_attention_workspace_size(1024, 32, 8, 128, 16, 16) == fast(1024, 32, 8, 1)
-    # 64 seqs x 8 kv heads x 256 tokens: 512 waves -> partitions of 64 (4 each)
-    assert lib.npd_paged_attention_workspace_size(64, 32, 8, 128, 16, 16) == fast(64, 32, 8, 4)
-    # 8 seqs x 8 kv heads x 32k tokens: 128 partitions of 256 already give >= 4096 waves
-    assert lib.npd_paged_attention_workspace_size(8, 32, 8, 128, 16, 2048) == fast(8, 32, 8, 128)
-    # 1 seq x 8 kv heads x 4k tokens: too few waves -> partitions of 64
-    assert lib.npd_paged_attention_workspace_size(1, 32, 8, 128, 16, 256) == fast(1, 32, 8, 64)
-    # 4096 seqs x 8 kv heads x 32k tokens: 128 partitions of 256, but a counter
-    # per unit and per group (32768 x 9) would not fit the 262144 counters ->
-    # one level, no group partials; 2048 seqs (16384 x 9 counters) fit
-    n = lib.npd_paged_attention_workspace_size(4096, 32, 8, 128, 16, 2048)
-    assert n == fast(4096, 32, 8, 128) - 4096 * 32 * 8 * 130 * 4
-    assert lib.npd_paged_attention_workspace_size(2048, 32, 8, 128, 16, 2048) == fast(2048, 32, 8, 128)
+    ws = lib.npd_paged_attention_workspace_size
+    # 2-byte pools (block size 64 here, a size the FP8 entry point does not
+    # take): the partition is the longest of 2048 .. 64 tokens (at most 4096 / G
+    # tokens for G query heads per kv head, G rounded up to a power of two)
+    # that gives >= 1280 work items at the longest context.
+    # 1024 seqs x 8 kv heads x 256 tokens: one partition each
+    assert ws(1024, 32, 8, 128, 64, 4) == fast(1024, 32, 8, 1)
+    # 64 seqs x 8 kv heads x 256 tokens: 512 units -> partitions of 64 (4 each)
+    assert ws(64, 32, 8, 128, 64, 4) == fast(64, 32, 8, 4)
+    # 8 seqs x 8 kv heads x 32k tokens: 2048 gives 1024 items, 1024 gives 2048
+    assert ws(8, 32, 8, 128, 64, 512) == fast(8, 32, 8, 32)
+    # 10 seqs x 8 kv heads x 32832 tokens: G = 4 caps the partition at 1024
+    # (33 each), G = 8 at 512 (65 each); G = 2 takes 2048 (17 each, 1360 items)
+    assert ws(10, 32, 8, 128, 64, 513) == fast(10, 32, 8, 33)
+    assert ws(10, 64, 8, 128, 64, 513) == fast(10, 64, 8, 65)
+    assert ws(10, 16, 8, 128, 64, 513) == fast(10, 16, 8, 17)
+    # 1 seq x 8 kv heads x 4k tokens: too few items at any length -> the block
+    assert ws(1, 32, 8, 128, 64, 64) == fast(1, 32, 8, 64)
+    # 4096 seqs x 8 kv heads x 128k tokens: 128 partitions of 1024, but a
+    # counter per unit and per group (32768 x 9) would not fit the 262144
+    # counters -> one level, no group partials; 2048 seqs (16384 x 9) fit
+    assert ws(4096, 32, 8, 128, 64, 2048) == fast(4096, 32, 8, 128) - 4096 * 32 * 8 * 130 * 4
+    assert ws(2048, 32, 8, 128, 64, 2048) == fast(2048, 32, 8, 128)
+    # Blocks of 16 or 32 (which the FP8 entry point takes): the workspace also
+    # covers the FP8 rule (>= 4096 items, at most 256 tokens), here 128
+    # partitions of 256 against the 2-byte rule's 32 of 1024
+    assert ws(8, 32, 8, 128, 16, 2048) == fast(8, 32, 8, 128)
+    assert ws(8, 32, 8, 128, 32, 1024) == fast(8, 32, 8, 128)
+    # 1024 seqs x 256 tokens: both rules give one partition
+    assert ws(1024, 32, 8, 128, 16, 16) == fast(1024, 32, 8, 1)
+    # 1 seq x 8 kv heads x 4k tokens in blocks of 16: partitions of 64
+    assert ws(1, 32, 8, 128, 16, 256) == fast(1, 32, 8, 64)
     # generic path (head_dim 64): partitions of 256 below 4096 waves
     n = lib.npd_paged_attention_workspace_size(2, 8, 8, 64, 16, 64)
     assert n == 2**20 + 2 * 8 * 4 * (64 + 2) * 4

@@ -103,11 +103,12 @@ def test_group_sizes_and_head_dims(device, dtype, D, G):
 
 @pytest.mark.parametrize("lens", [[1024], [1025], [2048], [2049], [100, 1025, 3000, 5000, 17]])
 def test_two_level_merge_group_boundaries(device, lens):
-    """Few sequences take 64-token partitions, and a (sequence, kv-head) with
-    more than 16 partitions merges in two levels: groups of 16, then the group
-    results. Lengths at the group boundaries: 16 partitions (one level), 17
-    (the last group has one partition, published as its group's result), 32,
-    33, and a mix of one- and two-level units."""
+    """A (sequence, kv-head) with more than 16 partitions merges in two
+    levels: groups of 16, then the group results. One sequence (8 units) takes
+    64-token partitions, so the lengths sit at the group boundaries: 16
+    partitions (one level), 17 (the last group has one partition, published as
+    its group's result), 32, 33; then a mix of one- and two-level units
+    (128-token partitions)."""
     args = make_inputs(len(lens), 32, 8, 128, lens, 16, torch.bfloat16, device, seed=sum(lens))
     q, kc, vc, bt, sl, scale, mb = args
     check(run(*args, 16), q, kc, vc, bt, sl, scale)
@@ -122,13 +123,24 @@ def test_two_level_merge_many_groups(device):
 
 
 def test_two_level_merge_scheduled_path(device):
-    """More than 64 sequences (the work list built by the schedule kernel) with
-    256-token partitions and up to 32 of them per unit."""
+    """More than 64 sequences (the work list built by the schedule kernel):
+    70 units with 256-token partitions, up to 32 of them per unit."""
     g = torch.Generator().manual_seed(70)
     lens = torch.randint(1, 8193, (70,), generator=g).tolist()
     lens[3] = 8192
-    args = make_inputs(70, 4, 2, 128, lens, 16, torch.bfloat16, device, seed=70)
+    args = make_inputs(70, 4, 1, 128, lens, 16, torch.bfloat16, device, seed=70)
     q, kc, vc, bt, sl, scale, mb = args
+    check(run(*args, 16), q, kc, vc, bt, sl, scale)
+
+
+def test_2048_token_partitions_span_128_blocks(device):
+    """A 32769-token context in a table 2049 blocks wide with 80 units and 2
+    query heads per kv head: 17 partitions of 2048 tokens each, 128 blocks of
+    16 (two block ids per lane). Short and empty sequences share the batch."""
+    lens = [32769, 5000, 17, 1, 2048, 2049, 4097, 100, 0, 9000]
+    args = make_inputs(len(lens), 16, 8, 128, lens, 16, torch.bfloat16, device, seed=2048)
+    q, kc, vc, bt, sl, scale, mb = args
+    assert mb == 2049
     check(run(*args, 16), q, kc, vc, bt, sl, scale)
 
 

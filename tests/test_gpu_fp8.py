@@ -102,6 +102,14 @@ def test_decode_block_sizes_and_long_context(device, bs):
     _run_and_check(device, *args, bs, torch.bfloat16)
 
 
+def test_decode_long_context_merge_groups(device):
+    """80 units with a 32769-token context: partitions of 256 tokens (the FP8
+    rule), 129 of them, merged in 9 groups (the last a group of one)."""
+    lens = [32769, 5000, 17, 1, 2048, 2049, 4097, 100, 0, 9000]
+    args = _fp8_case(device, lens, 16, 8, 16, torch.bfloat16, seed=2048)
+    _run_and_check(device, *args, 16, torch.bfloat16)
+
+
 def test_store_then_decode_matches_bf16_pool(device):
     """Config-2 shape, 16 sequences: the same bf16 K/V stored into a bf16 pool
     and into an fp8 pool; attention over the fp8 pool is the fp64 attention
