@@ -53,6 +53,9 @@ constexpr int kFastMaxScores = 4096;
 // fast path: the partition is chosen to give at least this many work items
 // at the longest context (5 per CU of a 256-CU device)
 constexpr int64_t kFastMinItems = 1280;
+// fast path, at most 64 sequences: the kernel halves the host's partition
+// (down to a quarter of it) while the actual contexts give fewer items
+constexpr int kFastMinItemsActual = 1024;
 // FP8 pools: a row is half the bytes, so a wave has half the bytes in flight
 // and more, shorter items keep HBM busy: at least 4096 items, partitions of at
 // most 256 tokens
@@ -101,6 +104,7 @@ struct DecodeArgs {
   int num_blocks;
   int max_bps;
   int partition;     // PS, multiple of kStep, <= kMaxPartition (fast path: kFastMaxPartition)
+  int min_partition; // fast path, <= 64 sequences: the kernel may halve PS down to this
   int max_parts;
   int max_groups;    // fast path: merge groups per unit (0: one-level merge)
   float scale_log2;  // softmax scale * log2(e)
@@ -651,7 +655,7 @@ struct KvSrc<TT, true> {
 
 template <class TT, int G, int SPB, bool kF8 = false>
 __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, int part,
-                                                 float* s_p, uint32_t* s_pp) {
+                                                 int ps, float* s_p, uint32_t* s_pp) {
   typedef KvSrc<TT, kF8> Src;
   typedef typename Src::raw raw_t;
   constexpr int D = 128;
@@ -685,10 +689,10 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
     }
     return;
   }
-  const int nparts = (ctx + a.partition - 1) / a.partition;
+  const int nparts = (ctx + ps - 1) / ps;
   if (part >= nparts) return;
-  const int t0 = part * a.partition;
-  const int ntok = (ctx - t0) < a.partition ? (ctx - t0) : a.partition;
+  const int t0 = part * ps;
+  const int ntok = (ctx - t0) < ps ? (ctx - t0) : ps;
   // steps rounded up to the ring size; steps past the context read block 0
   // of the pool (always present) and are masked out
   const int nsteps = (((ntok + 15) >> 4) + NBUF - 1) / NBUF * NBUF;
@@ -1043,7 +1047,7 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
   float* s_p = s_dyn;   // [partition + ring padding][GP] scores
   uint32_t* s_pp =   // [(partition + ring padding) / 2][GP] packed probabilities (kDot2)
       kF8 ? reinterpret_cast<uint32_t*>(s_dyn + (a.partition + 16 * kRing) * GP) : nullptr;
-  int unit, part;
+  int unit, part, ps = a.partition;
   if (a.num_seqs <= kInlineSchedMax) {
     // Small batch: every workgroup derives its item from seq_lens alone, in
     // longest-processing-time order:
@@ -1056,18 +1060,28 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
     //      buckets (binary search over ballot counts).
     // Items past the resident capacity of the GPU start as earlier ones end,
     // so the ones dispatched last are the shortest.
+    // The partition is the host's (chosen from the table width) or, when
+    // the actual contexts give fewer than kFastMinItemsActual items at that
+    // length, the longest of its halves down to a.min_partition that does.
     const int lane = threadIdx.x;
     const int cap = a.max_bps * a.block_size;
     const int kvh = a.num_kv_heads;
     const bool valid = lane < a.num_seqs;
-    int full = 0, bucket = 0;   // full partitions before the last; last one's length in 16s
-    if (valid) {
-      int c = a.seq_lens[lane];
-      c = c < cap ? c : cap;
-      if (c > 0) {
-        full = (c - 1) / a.partition;
-        bucket = (c - full * a.partition + 15) >> 4;
+    int c = valid ? a.seq_lens[lane] : 0;
+    c = c < cap ? c : cap;
+    ps = a.min_partition;
+    for (int p = a.partition; p > a.min_partition; p >>= 1) {
+      const int sh = __builtin_ctz(p);   // partitions are powers of two
+      const int n = valid ? (c > 0 ? (c + p - 1) >> sh : 1) : 0;
+      if (wave_sum_i(n) * kvh >= kFastMinItemsActual) {
+        ps = p;
+        break;
       }
+    }
+    int full = 0, bucket = 0;   // full partitions before the last; last one's length in 16s
+    if (valid && c > 0) {
+      full = (c - 1) / ps;
+      bucket = (c - full * ps + 15) >> 4;
     }
     // sequence = the k-th set bit of m
     auto nth = [&](uint64_t m, int k) -> int {
@@ -1100,7 +1114,7 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
       // bucket b with from(b) > id (binary search)
       auto from = [&](int b) -> int { return __popcll(__ballot(valid && bucket >= b)) * kvh; };
       if (id >= from(0)) return;   // past the last item
-      int lo = 0, hi = a.partition >> 4;
+      int lo = 0, hi = ps >> 4;
       while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
         if (from(mid) > id) lo = mid; else hi = mid - 1;
@@ -1116,7 +1130,7 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
     unit = it.x;
     part = it.y;
   }
-  decode_d128_item<TT, G, SPB, kF8>(a, unit, part, s_p, s_pp);
+  decode_d128_item<TT, G, SPB, kF8>(a, unit, part, ps, s_p, s_pp);
 }
 
 // Builds the work list of decode_d128_kernel (one workgroup):
@@ -1245,6 +1259,32 @@ int choose_partition(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads, 
   return units * ((max_ctx + 511) / 512) >= 4096 ? 512 : 256;
 }
 
+// Shortest partition the fast path's kernel may take for a host partition ps
+// (2-byte pools: down to ps / 4, never below 64 tokens or the block); the
+// workspace and the grid are sized for it.
+int fast_min_partition(int ps, int64_t block_size, bool fp8) {
+  if (fp8) return ps;
+  int lo = ps / 4;
+  lo = lo < 64 ? 64 : lo;
+  lo = lo < block_size ? (int)block_size : lo;
+  return lo < ps ? lo : ps;
+}
+
+// Grid of the fast path: the items at the host's partition or, when the
+// kernel may halve it, at most 2 * kFastMinItemsActual - 2 (it halves only
+// while a length gives fewer than kFastMinItemsActual items, and halving at
+// most doubles the count), within the slots the workspace holds.
+int64_t fast_grid(const DecodeArgs& a, int64_t units) {
+  const int64_t max_ctx = (int64_t)a.max_bps * a.block_size;
+  int64_t n = units * ((max_ctx + a.partition - 1) / a.partition);
+  if (a.min_partition < a.partition) {
+    int64_t h = units * a.max_parts;
+    h = h < 2 * kFastMinItemsActual ? h : 2 * kFastMinItemsActual;
+    n = n > h ? n : h;
+  }
+  return n;
+}
+
 // Dynamic LDS of decode_d128_kernel for a partition: scores (fp32) of every
 // token of the partition plus the ring padding, and their packed bf16/fp16
 // probabilities when pass 3 uses v_dot2 (FP8 pools).
@@ -1284,7 +1324,7 @@ int launch_fast_fp8(const DecodeArgs& a, int num_seqs, int64_t max_items, hipStr
 template <class TT>
 int dispatch_fp8(int g, const DecodeArgs& a, int64_t units, hipStream_t st) {
   const int ns = (int)(units / a.num_kv_heads);
-  const int64_t mi = units * a.max_parts;
+  const int64_t mi = fast_grid(a, units);
   switch (g) {
     case 1: launch_fast_fp8<TT, 1>(a, ns, mi, st); break;
     case 2: launch_fast_fp8<TT, 2>(a, ns, mi, st); break;
@@ -1302,7 +1342,7 @@ template <class TT, int D, int G>
 int launch_decode(const DecodeArgs& a, int64_t units, hipStream_t st) {
   if constexpr (D == 128) {
     if (use_fast_path(D, a.block_size, units / a.num_kv_heads)) {
-      const int rc = launch_fast<TT, G>(a, (int)(units / a.num_kv_heads), units * a.max_parts, st);
+      const int rc = launch_fast<TT, G>(a, (int)(units / a.num_kv_heads), fast_grid(a, units), st);
       if (rc != NPD_OK) return rc;
       return npd::check_launch("npd_paged_attention");
     } else {
@@ -1372,8 +1412,9 @@ extern "C" int64_t npd_paged_attention_workspace_size(int64_t num_seqs, int64_t 
   // be shorter)
   const int64_t units = num_seqs * num_kv_heads;
   auto need = [&](bool fp8) {
-    const int ps =
-        choose_partition(num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_ctx, fp8);
+    const int ps = fast_min_partition(
+        choose_partition(num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_ctx, fp8),
+        block_size, fp8);
     const int64_t parts = (max_ctx + ps - 1) / ps;
     const int64_t slots = parts + merge_groups(true, units, parts);
     return (npd::kCounterBytes + 16 + units * parts * 8 + 255) / 256 * 256 +
@@ -1448,7 +1489,10 @@ int attention_impl(void* out, const void* query, const void* key_cache, const vo
       return fail(NPD_E_INVALID, "%s: block_size %lld is above %d", name, (long long)block_size,
                   limit);
   }
-  const int64_t max_parts = (max_ctx + partition - 1) / partition;
+  const bool fast = use_fast_path(head_dim, block_size, num_seqs);
+  const int min_partition = fast ? fast_min_partition(partition, block_size, fp8) : partition;
+  // partial slots per unit: for the shortest partition the kernel may take
+  const int64_t max_parts = (max_ctx + min_partition - 1) / min_partition;
   if (max_parts > 65535) return fail(NPD_E_INVALID, "%s: context too long", name);
   const int64_t need = npd_paged_attention_workspace_size(num_seqs, num_heads, num_kv_heads,
                                                           head_dim, block_size, max_blocks_per_seq);
@@ -1488,6 +1532,7 @@ int attention_impl(void* out, const void* query, const void* key_cache, const vo
   a.num_blocks = (int)num_blocks;
   a.max_bps = (int)max_blocks_per_seq;
   a.partition = partition;
+  a.min_partition = min_partition;
   a.max_parts = (int)max_parts;
   a.scale_log2 = scale * kLog2e;
   a.q_stride_seq = q_stride_seq;

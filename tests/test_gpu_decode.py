@@ -144,6 +144,21 @@ def test_2048_token_partitions_span_128_blocks(device):
     check(run(*args, 16), q, kc, vc, bt, sl, scale)
 
 
+def test_partition_halved_for_short_contexts(device):
+    """A table 224 blocks wide (3584 tokens) makes the host take 1024-token
+    partitions for 48 x 8 units; the actual contexts (256 .. 2048) give fewer
+    than 1024 items at that length, so the kernel halves the partition (here
+    to 256) from seq_lens alone."""
+    g = torch.Generator().manual_seed(48)
+    lens = torch.randint(256, 2049, (48,), generator=g).tolist()
+    q, kc, vc, bt, sl, scale, mb = make_inputs(48, 32, 8, 128, lens, 16, torch.bfloat16, device,
+                                               seed=48)
+    btw = torch.zeros(48, 224, dtype=torch.int32, device=device)
+    btw[:, :mb] = bt
+    out = run(q, kc, vc, btw, sl, scale, 224, 16)
+    check(out, q, kc, vc, btw, sl, scale)
+
+
 def test_output_shape_and_int64_tables_raise(device):
     args = make_inputs(4, 8, 8, 128, [10] * 4, 16, torch.float16, device)
     q, kc, vc, bt, sl, scale, mb = args
