@@ -189,6 +189,32 @@ int npd_paged_prefill_attention(void* out, const void* query,
                                 int32_t dtype, void* stream);
 
 /*
+ * npd_paged_prefill_attention over an FP8 (e4m3) pool written by
+ * npd_paged_kv_store_slots_fp8 (no reference counterpart; the reference's
+ * prefill, nanoPD/engine/model_runner.py:152-168, reads fp16 K/V). K and V
+ * elements are e4m3(byte) * k_scale[kv head] (v_scale for V), converted
+ * exactly to the query's type (fp16/bf16, dtype) before the MFMAs; arithmetic
+ * and workspace as in npd_paged_prefill_attention. head_dim 128; caches
+ * 8-byte aligned.
+ */
+int npd_paged_prefill_attention_fp8(void* out, const void* query,
+                                    const void* key_cache, const void* value_cache,
+                                    const int32_t* block_tables,
+                                    const int32_t* cu_seqlens_q,
+                                    const int32_t* context_lens,
+                                    const float* k_scale, const float* v_scale,
+                                    int64_t num_seqs, int64_t total_q,
+                                    int64_t num_heads, int64_t num_kv_heads,
+                                    int64_t head_dim, int64_t num_blocks,
+                                    int64_t block_size, int64_t max_blocks_per_seq,
+                                    int64_t max_q_len, int64_t max_context_len,
+                                    float scale,
+                                    int64_t q_stride_token, int64_t q_stride_head,
+                                    int64_t out_stride_token, int64_t out_stride_head,
+                                    void* workspace, int64_t workspace_bytes,
+                                    int32_t dtype, void* stream);
+
+/*
  * npd_paged_attention over an FP8 (e4m3) pool written by
  * npd_paged_kv_store_slots_fp8 (no reference counterpart). K and V elements
  * are e4m3(byte) * k_scale[kv head] (v_scale for V); query/out are fp16 or

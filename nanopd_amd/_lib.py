@@ -40,6 +40,10 @@ SIGNATURES = {
     "npd_paged_prefill_attention": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64,
                                                    _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F,
                                                    _I64, _I64, _I64, _I64, _P, _I64, _I32, _P]),
+    "npd_paged_prefill_attention_fp8": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
+                                                       _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+                                                       _I64, _I64, _F, _I64, _I64, _I64, _I64, _P,
+                                                       _I64, _I32, _P]),
     "npd_copy_blocks": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _I64, _I32, _P]),
     "npd_kv_gather_blocks": (ctypes.c_int, [_P, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P]),
     "npd_kv_scatter_blocks": (ctypes.c_int, [_P, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P]),

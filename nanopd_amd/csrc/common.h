@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/nanopd.h"
 
 namespace npd {
@@ -80,6 +82,17 @@ struct F16 {
     return __builtin_bit_cast(uint32_t, v);
   }
 };
+
+// Four OCP e4m3 bytes (one dword) -> two packed pairs of TT, exact (every
+// e4m3 value is a bf16 and an fp16 value): v_cvt_scalef32_pk_{bf16,f16}_fp8
+// with scale 1 converts the byte pair of the low (kHi false) or high half.
+template <class TT, bool kHi>
+__device__ __forceinline__ uint32_t e4m3x2_to(uint32_t w) {
+  if constexpr (std::is_same<TT, BF16>::value)
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, kHi));
+  else
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.f, kHi));
+}
 
 // Agent-scope relaxed atomic accesses: written through to, and read from, the
 // device-coherent level, so partials published by a workgroup on one XCD are

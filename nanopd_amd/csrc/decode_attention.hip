@@ -641,15 +641,9 @@ struct KvSrc<TT, true> {
   static __device__ __forceinline__ raw load(const void* base, int64_t idx) {
     return __builtin_nontemporal_load(static_cast<const u32x2*>(base) + idx);
   }
-  template <bool kHi>
-  static __device__ __forceinline__ uint32_t cvt(uint32_t w) {
-    if constexpr (std::is_same<TT, npd::BF16>::value)
-      return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, kHi));
-    else
-      return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.f, kHi));
-  }
   static __device__ __forceinline__ u32x4 pairs(raw w) {
-    return u32x4{cvt<false>(w.x), cvt<true>(w.x), cvt<false>(w.y), cvt<true>(w.y)};
+    return u32x4{npd::e4m3x2_to<TT, false>(w.x), npd::e4m3x2_to<TT, true>(w.x),
+                 npd::e4m3x2_to<TT, false>(w.y), npd::e4m3x2_to<TT, true>(w.y)};
   }
 };
 

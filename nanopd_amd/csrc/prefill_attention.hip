@@ -97,6 +97,8 @@ struct PrefillArgs {
   int* counters;
   float* part_o;
   float* part_ml;
+  const float* k_scale;   // FP8 pools: per-kv-head scales (element = e4m3 byte * scale)
+  const float* v_scale;
   int num_seqs, num_kv_heads, group, hgroups, block_size, bs_shift, num_blocks, max_bps;
   int tiles_max, subtiles, splits_max;   // subtiles: 32-row subtiles per sequence
   int ks_steps, num_groups;              // key steps per split; (split, seq, kv-head) groups
@@ -149,8 +151,10 @@ __device__ __forceinline__ u32x2 lds_read_tr(const uint16_t* p) {
 }
 
 // kOff32: every K/V element of the pool lies within 4 GiB of the cache base,
-// so gather offsets are 32-bit
-template <class TT, int HW, bool kOff32>
+// so gather offsets are 32-bit. kF8: the pool holds OCP e4m3 bytes; a K/V
+// chunk is 8 bytes, converted exactly to four TT pairs when copied into LDS,
+// and the per-kv-head scales go into the score scale and the output.
+template <class TT, int HW, bool kOff32, bool kF8>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   constexpr int RT = kPairs / HW;                      // row tiles of 64 per workgroup
   constexpr int TR = 64 * RT;                          // query rows per workgroup
@@ -346,14 +350,15 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   // through a register ring (slot = step % kDepth): one 32 KB tile in flight
   // per CU leaves a step waiting on memory latency.
   constexpr int kPer = kKT * kD / 8 / kThreads;        // 2
-  u32x4 kst[kDepth][kPer], vst[kDepth][kPer];
+  typedef typename std::conditional<kF8, u32x2, u32x4>::type raw_t;   // 8 elements
+  raw_t kst[kDepth][kPer], vst[kDepth][kPer];
   const int col = tid & 15;
   // Every fetch issues the same loads, so the compiler's count of loads in
   // flight stays exact and its waits cover only the slot being used: tokens
   // past the split's range are clamped to its last key. Such keys only occur
   // past the tile's last row (the causal mask removes them) and hold real
   // context rows, so their V is finite and P = 0 cancels it.
-  auto fetch = [&](int step, u32x4* ks, u32x4* vs) {
+  auto fetch = [&](int step, raw_t* ks, raw_t* vs) {
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
       int tok = step * kKT + (tid >> 4) + 32 * e;
@@ -361,7 +366,19 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
       const int lb = a.bs_shift >= 0 ? tok >> a.bs_shift : tok / bs;
       const int blk = s_blk[lb - blk0];
       const int row = (blk * a.num_kv_heads + kh) * bs + (tok - lb * bs);   // < 2^31 (host check)
-      if (kOff32) {
+      if constexpr (kF8) {   // 128-byte rows, 8-byte chunks
+        const char* kb = reinterpret_cast<const char*>(a.k_cache);
+        const char* vb = reinterpret_cast<const char*>(a.v_cache);
+        if (kOff32) {
+          const uint32_t off = (uint32_t)row * 128u + (uint32_t)col * 8u;
+          ks[e] = *reinterpret_cast<const u32x2*>(kb + off);
+          vs[e] = *reinterpret_cast<const u32x2*>(vb + off);
+        } else {
+          const int64_t off = (int64_t)row * 128 + col * 8;
+          ks[e] = *reinterpret_cast<const u32x2*>(kb + off);
+          vs[e] = *reinterpret_cast<const u32x2*>(vb + off);
+        }
+      } else if (kOff32) {
         const uint32_t off = (uint32_t)row * 256u + (uint32_t)col * 16u;
         ks[e] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(a.k_cache) + off);
         vs[e] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(a.v_cache) + off);
@@ -372,12 +389,19 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
       }
     }
   };
-  auto stash = [&](int kbuf, int vbuf, const u32x4* ks, const u32x4* vs) {
+  auto pairs = [](raw_t w) -> u32x4 {
+    if constexpr (kF8)
+      return u32x4{npd::e4m3x2_to<TT, false>(w.x), npd::e4m3x2_to<TT, true>(w.x),
+                   npd::e4m3x2_to<TT, false>(w.y), npd::e4m3x2_to<TT, true>(w.y)};
+    else
+      return w;
+  };
+  auto stash = [&](int kbuf, int vbuf, const raw_t* ks, const raw_t* vs) {
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
       const int kk = (tid >> 4) + 32 * e;
-      *reinterpret_cast<u32x4*>(&s_k[kbuf][kk * kRow + col * 8]) = ks[e];
-      *reinterpret_cast<u32x4*>(&s_v[vbuf][kk * kRow + col * 8]) = vs[e];
+      *reinterpret_cast<u32x4*>(&s_k[kbuf][kk * kRow + col * 8]) = pairs(ks[e]);
+      *reinterpret_cast<u32x4*>(&s_v[vbuf][kk * kRow + col * 8]) = pairs(vs[e]);
     }
   };
 
@@ -393,7 +417,8 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     nmref[mb] = 0.f;
     lrow[mb] = 0.f;
   }
-  const float c2 = a.scale_log2;
+  const float c2 = kF8 ? a.scale_log2 * a.k_scale[kh] : a.scale_log2;
+  const float oscale = kF8 ? a.v_scale[kh] : 1.f;
 
 #pragma unroll
   for (int d = 0; d < kDepth; ++d) fetch(st0 + d, kst[d], vst[d]);
@@ -626,7 +651,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     const int row = wrow0 + mb * 16 + r;
     if (row >= qlen) continue;
     const float l = lrow[mb];
-    const float inv = (l > 0.f && wpos0 + mb * 16 + r >= 0) ? 1.f / l : 0.f;
+    const float inv = (l > 0.f && wpos0 + mb * 16 + r >= 0) ? oscale / l : 0.f;
     uint16_t* op = a.out + (int64_t)(q0 + row) * a.out_stride_token + (int64_t)h * a.out_stride_head;
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) {
@@ -639,15 +664,22 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   }
 }
 
-template <class TT, bool kOff32>
-int launch(int hw, const PrefillArgs& a, int64_t grid, hipStream_t st) {
+template <class TT, bool kOff32, bool kF8>
+int launch(int hw, const PrefillArgs& a, int64_t grid, hipStream_t st, const char* name) {
   switch (hw) {
-    case 1: hipLaunchKernelGGL((prefill_kernel<TT, 1, kOff32>), dim3((unsigned)grid), dim3(kThreads), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((prefill_kernel<TT, 2, kOff32>), dim3((unsigned)grid), dim3(kThreads), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((prefill_kernel<TT, 4, kOff32>), dim3((unsigned)grid), dim3(kThreads), 0, st, a); break;
-    default: return npd::fail(NPD_E_INVALID, "npd_paged_prefill_attention: heads per workgroup %d", hw);
+    case 1: hipLaunchKernelGGL((prefill_kernel<TT, 1, kOff32, kF8>), dim3((unsigned)grid), dim3(kThreads), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((prefill_kernel<TT, 2, kOff32, kF8>), dim3((unsigned)grid), dim3(kThreads), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((prefill_kernel<TT, 4, kOff32, kF8>), dim3((unsigned)grid), dim3(kThreads), 0, st, a); break;
+    default: return npd::fail(NPD_E_INVALID, "%s: heads per workgroup %d", name, hw);
   }
-  return npd::check_launch("npd_paged_prefill_attention");
+  return npd::check_launch(name);
+}
+
+template <class TT, bool kF8>
+int launch_dt(bool off32, int hw, const PrefillArgs& a, int64_t grid, hipStream_t st,
+              const char* name) {
+  return off32 ? launch<TT, true, kF8>(hw, a, grid, st, name)
+               : launch<TT, false, kF8>(hw, a, grid, st, name);
 }
 
 // Workspace: [counter region (kCounterBytes) | O partials | (m, l) partials].
@@ -692,16 +724,21 @@ extern "C" int64_t npd_paged_prefill_workspace_size(int64_t num_seqs, int64_t to
   return prefill_layout(num_seqs, num_heads, max_q_len, max_context_len).total;
 }
 
-extern "C" int npd_paged_prefill_attention(
-    void* out, const void* query, const void* key_cache, const void* value_cache,
-    const int32_t* block_tables, const int32_t* cu_seqlens_q, const int32_t* context_lens,
-    int64_t num_seqs, int64_t total_q, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
-    int64_t num_blocks, int64_t block_size, int64_t max_blocks_per_seq, int64_t max_q_len,
-    int64_t max_context_len, float scale, int64_t q_stride_token, int64_t q_stride_head,
-    int64_t out_stride_token, int64_t out_stride_head, void* workspace, int64_t workspace_bytes,
-    int32_t dtype, void* stream) {
+namespace {
+
+// Shared by the 2-byte and the FP8 entry points: k_scale / v_scale are null
+// for 2-byte pools.
+int prefill_impl(void* out, const void* query, const void* key_cache, const void* value_cache,
+                 const int32_t* block_tables, const int32_t* cu_seqlens_q,
+                 const int32_t* context_lens, const float* k_scale, const float* v_scale,
+                 int64_t num_seqs, int64_t total_q, int64_t num_heads, int64_t num_kv_heads,
+                 int64_t head_dim, int64_t num_blocks, int64_t block_size,
+                 int64_t max_blocks_per_seq, int64_t max_q_len, int64_t max_context_len,
+                 float scale, int64_t q_stride_token, int64_t q_stride_head,
+                 int64_t out_stride_token, int64_t out_stride_head, void* workspace,
+                 int64_t workspace_bytes, int32_t dtype, void* stream, bool fp8,
+                 const char* name) {
   using namespace npd;
-  const char* name = "npd_paged_prefill_attention";
   if (dtype != NPD_DTYPE_F16 && dtype != NPD_DTYPE_BF16)
     return fail(NPD_E_DTYPE, "%s: unsupported dtype code %d (fp16/bf16 only)", name, dtype);
   if (num_seqs < 0 || total_q < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_blocks <= 0 ||
@@ -729,9 +766,13 @@ extern "C" int npd_paged_prefill_attention(
   if (num_seqs == 0 || total_q == 0 || max_q_len == 0) return NPD_OK;
   if (!out || !query || !key_cache || !value_cache || !block_tables || !cu_seqlens_q || !context_lens)
     return fail(NPD_E_INVALID, "%s: null pointer", name);
-  if (!aligned16(query) || !aligned16(key_cache) || !aligned16(value_cache) ||
+  if (fp8 && (!k_scale || !v_scale)) return fail(NPD_E_INVALID, "%s: null scale pointer", name);
+  const uintptr_t cache_align = fp8 ? 7u : 15u;   // FP8 chunks are 8 bytes
+  if (!aligned16(query) || (reinterpret_cast<uintptr_t>(key_cache) & cache_align) != 0 ||
+      (reinterpret_cast<uintptr_t>(value_cache) & cache_align) != 0 ||
       (reinterpret_cast<uintptr_t>(out) & 7u) != 0)
-    return fail(NPD_E_ALIGN, "%s: query/cache pointers must be 16-byte aligned, out 8-byte", name);
+    return fail(NPD_E_ALIGN, "%s: query pointer must be 16-byte aligned, caches %d-byte, out 8-byte",
+                name, fp8 ? 8 : 16);
   const Layout L = prefill_layout(num_seqs, num_heads, max_q_len, max_context_len);
   if (L.total > 0) {
     if (!workspace || workspace_bytes < L.total)
@@ -762,6 +803,8 @@ extern "C" int npd_paged_prefill_attention(
   a.counters = L.total > 0 ? reinterpret_cast<int*>(ws) : nullptr;
   a.part_o = L.total > 0 ? reinterpret_cast<float*>(ws + L.o_off) : nullptr;
   a.part_ml = L.total > 0 ? reinterpret_cast<float*>(ws + L.ml_off) : nullptr;
+  a.k_scale = k_scale;
+  a.v_scale = v_scale;
   a.num_seqs = (int)num_seqs;
   a.num_kv_heads = (int)num_kv_heads;
   a.group = (int)g;
@@ -782,8 +825,46 @@ extern "C" int npd_paged_prefill_attention(
   a.out_stride_token = out_stride_token;
   a.out_stride_head = out_stride_head;
   hipStream_t st = as_stream(stream);
-  const bool off32 = num_blocks * num_kv_heads * block_size * head_dim * 2 <= (int64_t)UINT32_MAX;
+  const int64_t elt = fp8 ? 1 : 2;
+  const bool off32 = num_blocks * num_kv_heads * block_size * head_dim * elt <= (int64_t)UINT32_MAX;
   if (dtype == NPD_DTYPE_BF16)
-    return off32 ? launch<BF16, true>(hw, a, grid, st) : launch<BF16, false>(hw, a, grid, st);
-  return off32 ? launch<F16, true>(hw, a, grid, st) : launch<F16, false>(hw, a, grid, st);
+    return fp8 ? launch_dt<BF16, true>(off32, hw, a, grid, st, name)
+               : launch_dt<BF16, false>(off32, hw, a, grid, st, name);
+  return fp8 ? launch_dt<F16, true>(off32, hw, a, grid, st, name)
+             : launch_dt<F16, false>(off32, hw, a, grid, st, name);
+}
+
+}  // namespace
+
+extern "C" int npd_paged_prefill_attention(
+    void* out, const void* query, const void* key_cache, const void* value_cache,
+    const int32_t* block_tables, const int32_t* cu_seqlens_q, const int32_t* context_lens,
+    int64_t num_seqs, int64_t total_q, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+    int64_t num_blocks, int64_t block_size, int64_t max_blocks_per_seq, int64_t max_q_len,
+    int64_t max_context_len, float scale, int64_t q_stride_token, int64_t q_stride_head,
+    int64_t out_stride_token, int64_t out_stride_head, void* workspace, int64_t workspace_bytes,
+    int32_t dtype, void* stream) {
+  return prefill_impl(out, query, key_cache, value_cache, block_tables, cu_seqlens_q,
+                      context_lens, nullptr, nullptr, num_seqs, total_q, num_heads, num_kv_heads,
+                      head_dim, num_blocks, block_size, max_blocks_per_seq, max_q_len,
+                      max_context_len, scale, q_stride_token, q_stride_head, out_stride_token,
+                      out_stride_head, workspace, workspace_bytes, dtype, stream, false,
+                      "npd_paged_prefill_attention");
+}
+
+extern "C" int npd_paged_prefill_attention_fp8(
+    void* out, const void* query, const void* key_cache, const void* value_cache,
+    const int32_t* block_tables, const int32_t* cu_seqlens_q, const int32_t* context_lens,
+    const float* k_scale, const float* v_scale, int64_t num_seqs, int64_t total_q,
+    int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t num_blocks,
+    int64_t block_size, int64_t max_blocks_per_seq, int64_t max_q_len, int64_t max_context_len,
+    float scale, int64_t q_stride_token, int64_t q_stride_head, int64_t out_stride_token,
+    int64_t out_stride_head, void* workspace, int64_t workspace_bytes, int32_t dtype,
+    void* stream) {
+  return prefill_impl(out, query, key_cache, value_cache, block_tables, cu_seqlens_q,
+                      context_lens, k_scale, v_scale, num_seqs, total_q, num_heads, num_kv_heads,
+                      head_dim, num_blocks, block_size, max_blocks_per_seq, max_q_len,
+                      max_context_len, scale, q_stride_token, q_stride_head, out_stride_token,
+                      out_stride_head, workspace, workspace_bytes, dtype, stream, true,
+                      "npd_paged_prefill_attention_fp8");
 }

@@ -348,40 +348,29 @@ def prefill_workspace_bytes(num_seqs: int, total_q: int, num_heads: int, head_di
         num_seqs, total_q, num_heads, head_dim, max_q_len, max_context_len))
 
 
-def paged_prefill_attention(out: torch.Tensor, query: torch.Tensor, key_cache: torch.Tensor,
-                            value_cache: torch.Tensor, block_tables: torch.Tensor,
-                            cu_seqlens_q: torch.Tensor, context_lens: torch.Tensor, scale: float,
-                            block_size: int, max_num_blocks_per_seq: int, max_q_len: int,
-                            max_context_len: int | None = None,
-                            workspace: torch.Tensor | None = None) -> None:
-    """Causal varlen attention over the paged prefix plus the new chunk.
-
-    Replaces the SDPA prefill of paged_forward (nanoPD/engine/model_runner.py:
-    152-168), which attends within the chunk only. query/out: [total_q,
-    num_heads, head_dim]; sequence s owns rows cu_seqlens_q[s]:cu_seqlens_q[s+1];
-    its chunk K/V must already be in the pool; context_lens[s] = prefix + chunk.
-    Row i of s sits at position context_lens[s] - q_len + i and sees keys 0..pos.
-    max_q_len / max_context_len are host-side upper bounds (grid sizing; the
-    context bound, default max_num_blocks_per_seq * block_size, sets how long
-    key ranges are split). An optional uint8 ``workspace`` of at least
-    :func:`prefill_workspace_bytes` bytes, zero-filled before its first use,
-    replaces the cached per-stream one; calls sharing one run in stream order.
-    """
+def _prefill(out, query, key_cache, value_cache, block_tables, cu_seqlens_q, context_lens, scale,
+             block_size, max_num_blocks_per_seq, max_q_len, max_context_len, workspace,
+             fp8_scales):
     _check(isinstance(query, torch.Tensor) and query.is_cuda, "query is must be on CUDA")
     _check(query.dim() == 3, "query must be [total_q, num_heads, head_size]")
     _int32(block_tables, "block_tables")
     _int32(cu_seqlens_q, "cu_seqlens_q")
     _int32(context_lens, "context_lens")
-    _cache_checks(key_cache, value_cache)
+    if fp8_scales is None:
+        _cache_checks(key_cache, value_cache)
+    else:
+        _fp8_cache_checks(key_cache, value_cache, *fp8_scales)
     dev = query.device
-    _same_device(dev, out, key_cache, value_cache, block_tables, cu_seqlens_q, context_lens)
+    _same_device(dev, out, key_cache, value_cache, block_tables, cu_seqlens_q, context_lens,
+                 *(fp8_scales or ()))
     tq, h, d = query.shape
     num_blocks, kvh, bs, cd = key_cache.shape
     _check(cd == d, f"head_dim {d} does not match cache head_dim {cd}")
     _check(int(block_size) == bs, f"block_size {block_size} does not match cache block size {bs}")
     _check(h % kvh == 0, f"num_heads {h} is not a multiple of num_kv_heads {kvh}")
     _check(out.shape == query.shape and out.dtype == query.dtype, "out must match query")
-    _check(query.dtype == key_cache.dtype, "query/cache dtype mismatch")
+    if fp8_scales is None:
+        _check(query.dtype == key_cache.dtype, "query/cache dtype mismatch")
     code = _dtype_code(query, "paged_prefill_attention")
     ns = cu_seqlens_q.numel() - 1
     mb = int(max_num_blocks_per_seq)
@@ -404,11 +393,55 @@ def paged_prefill_attention(out: torch.Tensor, query: torch.Tensor, key_cache: t
         _check(workspace.numel() * workspace.element_size() >= need,
                f"workspace of {need} bytes needed")
         ws_ptr = workspace.data_ptr()
-    _lib.call("npd_paged_prefill_attention", out.data_ptr(), query.data_ptr(),
-              key_cache.data_ptr(), value_cache.data_ptr(), block_tables.data_ptr(),
-              cu_seqlens_q.data_ptr(), context_lens.data_ptr(), ns, tq, h, kvh, d, num_blocks, bs,
-              mb, int(max_q_len), mctx, float(scale), query.stride(0), query.stride(1),
-              out.stride(0), out.stride(1), ws_ptr, need, code, stream)
+    ptrs = (out.data_ptr(), query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+            block_tables.data_ptr(), cu_seqlens_q.data_ptr(), context_lens.data_ptr())
+    sizes = (ns, tq, h, kvh, d, num_blocks, bs, mb, int(max_q_len), mctx, float(scale),
+             query.stride(0), query.stride(1), out.stride(0), out.stride(1), ws_ptr, need, code,
+             stream)
+    if fp8_scales is None:
+        _lib.call("npd_paged_prefill_attention", *ptrs, *sizes)
+    else:
+        _lib.call("npd_paged_prefill_attention_fp8", *ptrs, fp8_scales[0].data_ptr(),
+                  fp8_scales[1].data_ptr(), *sizes)
+
+
+def paged_prefill_attention(out: torch.Tensor, query: torch.Tensor, key_cache: torch.Tensor,
+                            value_cache: torch.Tensor, block_tables: torch.Tensor,
+                            cu_seqlens_q: torch.Tensor, context_lens: torch.Tensor, scale: float,
+                            block_size: int, max_num_blocks_per_seq: int, max_q_len: int,
+                            max_context_len: int | None = None,
+                            workspace: torch.Tensor | None = None) -> None:
+    """Causal varlen attention over the paged prefix plus the new chunk.
+
+    Replaces the SDPA prefill of paged_forward (nanoPD/engine/model_runner.py:
+    152-168), which attends within the chunk only. query/out: [total_q,
+    num_heads, head_dim]; sequence s owns rows cu_seqlens_q[s]:cu_seqlens_q[s+1];
+    its chunk K/V must already be in the pool; context_lens[s] = prefix + chunk.
+    Row i of s sits at position context_lens[s] - q_len + i and sees keys 0..pos.
+    max_q_len / max_context_len are host-side upper bounds (grid sizing; the
+    context bound, default max_num_blocks_per_seq * block_size, sets how long
+    key ranges are split). An optional uint8 ``workspace`` of at least
+    :func:`prefill_workspace_bytes` bytes, zero-filled before its first use,
+    replaces the cached per-stream one; calls sharing one run in stream order.
+    """
+    _prefill(out, query, key_cache, value_cache, block_tables, cu_seqlens_q, context_lens, scale,
+             block_size, max_num_blocks_per_seq, max_q_len, max_context_len, workspace, None)
+
+
+def paged_prefill_attention_fp8(out: torch.Tensor, query: torch.Tensor, key_cache: torch.Tensor,
+                                value_cache: torch.Tensor, block_tables: torch.Tensor,
+                                cu_seqlens_q: torch.Tensor, context_lens: torch.Tensor,
+                                scale: float, block_size: int, max_num_blocks_per_seq: int,
+                                max_q_len: int, k_scale: torch.Tensor, v_scale: torch.Tensor,
+                                max_context_len: int | None = None,
+                                workspace: torch.Tensor | None = None) -> None:
+    """:func:`paged_prefill_attention` over an FP8 pool written by
+    :func:`paged_kv_store_slots_fp8` (no reference counterpart): K =
+    e4m3(byte) * k_scale[kv head], V likewise, converted exactly to the
+    query's type before the MFMAs. query/out fp16 or bf16; head_dim 128."""
+    _prefill(out, query, key_cache, value_cache, block_tables, cu_seqlens_q, context_lens, scale,
+             block_size, max_num_blocks_per_seq, max_q_len, max_context_len, workspace,
+             (k_scale, v_scale))
 
 
 # ---------------------------------------------------------------------------

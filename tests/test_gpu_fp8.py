@@ -169,3 +169,75 @@ def test_argument_checks(device):
     with pytest.raises(RuntimeError, match="k_scale"):
         pk.paged_attention_forward_fp8(torch.empty_like(q), q, kc, kc, bt, sl, 0.1, 8, 1,
                                        torch.ones(3, device=device), sc)
+
+
+def _fp8_prefill_case(device, prefixes, chunks, H, kvh, dtype, seed, bs=16):
+    """Random e4m3 pool (no NaN codes) with per-head scales, shuffled tables
+    of prefix + chunk blocks, and the chunks' queries packed varlen."""
+    g = torch.Generator().manual_seed(seed)
+    ctx = [p + c for p, c in zip(prefixes, chunks)]
+    nbs = [(n + bs - 1) // bs for n in ctx]
+    total = sum(nbs) + 3
+    codes = torch.randint(0, 0x7E, (2, total, kvh, bs, 128), generator=g, dtype=torch.int32)
+    codes = codes | (torch.randint(0, 2, codes.shape, generator=g, dtype=torch.int32) << 7)
+    kc, vc = codes[0].to(torch.uint8), codes[1].to(torch.uint8)
+    order = torch.randperm(total, generator=g)
+    bt = torch.zeros(len(ctx), max(nbs), dtype=torch.int32)
+    o = 0
+    for s, n in enumerate(nbs):
+        bt[s, :n] = order[o:o + n]
+        o += n
+    q = (torch.randn(sum(chunks), H, 128, generator=g) * 0.5).to(dtype)
+    cu = torch.tensor([0] + list(np.cumsum(chunks)), dtype=torch.int32)
+    ks = (0.5 + torch.rand(kvh, generator=g)) / 448
+    vs = (0.5 + torch.rand(kvh, generator=g)) / 448
+    return q, kc, vc, bt, cu, torch.tensor(ctx, dtype=torch.int32), ks.float(), vs.float(), max(chunks)
+
+
+def _prefill_run_and_check(device, q, kc, vc, bt, cu, ctx, ks, vs, max_q, dtype):
+    scale = 1 / math.sqrt(128)
+    out = torch.full_like(q, float("nan")).to(device)
+    pk.paged_prefill_attention_fp8(out, q.to(device), kc.to(device).view(torch.float8_e4m3fn),
+                                   vc.to(device).view(torch.float8_e4m3fn), bt.to(device),
+                                   cu.to(device), ctx.to(device), scale, kc.size(2), bt.size(1),
+                                   max_q, ks.to(device), vs.to(device))
+    torch.cuda.synchronize()
+    want = O.prefill_attention(f32(q), O.fp8_pool_values(kc.numpy(), ks.numpy()),
+                               O.fp8_pool_values(vc.numpy(), vs.numpy()), bt.numpy(), cu.numpy(),
+                               ctx.numpy(), scale)
+    assert np.isfinite(f32(out)).all()
+    err = max_abs(out, want)
+    assert err <= ATOL[dtype], f"max-abs {err}"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("G", [1, 2, 4, 6])
+def test_prefill_group_sizes(device, dtype, G):
+    """Every heads-per-workgroup tiling (1, 2, 4) over an FP8 pool, with an
+    empty prefix, a ragged chunk and a key range long enough to be split."""
+    kvh = 2
+    case = _fp8_prefill_case(device, [0, 100, 1500], [64, 37, 200], G * kvh, kvh, dtype, seed=G)
+    _prefill_run_and_check(device, *case, dtype)
+
+
+def test_prefill_config3_shape(device):
+    """Configuration 3's chunks and prefixes (4 x 512 on {0, 512, 1536, 3072}),
+    Qwen3-8B heads, over an FP8 pool."""
+    case = _fp8_prefill_case(device, [0, 512, 1536, 3072], [512] * 4, 32, 8, torch.bfloat16,
+                             seed=3)
+    _prefill_run_and_check(device, *case, torch.bfloat16)
+
+
+def test_prefill_fp8_argument_checks(device):
+    case = _fp8_prefill_case(device, [0], [16], 8, 2, torch.bfloat16, seed=5)
+    q, kc, vc, bt, cu, ctx, ks, vs, max_q = case
+    dk, dv = kc.to(device).view(torch.float8_e4m3fn), vc.to(device).view(torch.float8_e4m3fn)
+    out = torch.empty_like(q).to(device)
+    args = (out, q.to(device), dk, dv, bt.to(device), cu.to(device), ctx.to(device), 0.1, 16,
+            bt.size(1), max_q)
+    with pytest.raises(RuntimeError):   # one scale per kv head
+        pk.paged_prefill_attention_fp8(*args, ks[:1].to(device), vs.to(device))
+    with pytest.raises(RuntimeError):   # 2-byte caches are not FP8 pools
+        pk.paged_prefill_attention_fp8(out, q.to(device), dk.to(torch.bfloat16),
+                                       dv.to(torch.bfloat16), *args[4:], ks.to(device),
+                                       vs.to(device))
