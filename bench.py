@@ -260,6 +260,20 @@ def bench_prefill(args, w) -> dict:
     pf_ms = _launch_avg_ms(prefill, args.steps)
     flops = w.prefill_flops()
     tflops = flops / (pf_ms * 1e-3) / 1e12
+    # the same prefill over an FP8 copy of the pool (per-kv-head scales,
+    # amax / 448), outside the timed region
+    ks = (w.k_cache.float().abs().amax(dim=(0, 2, 3)) / 448).clamp_min(1e-8).contiguous()
+    vs = (w.v_cache.float().abs().amax(dim=(0, 2, 3)) / 448).clamp_min(1e-8).contiguous()
+    k8 = (w.k_cache.float() / ks[None, :, None, None]).to(torch.float8_e4m3fn)
+    v8 = (w.v_cache.float() / vs[None, :, None, None]).to(torch.float8_e4m3fn)
+
+    def prefill_fp8():
+        pk.paged_prefill_attention_fp8(out[:tp], w.query[:tp], k8, v8, bt_p, cu_p, cl_p, w.scale,
+                                       w.block_size, mb, max_q, ks, vs)
+
+    prefill_fp8()
+    pf8_ms = _launch_avg_ms(prefill_fp8, args.steps)
+    del k8, v8
     return {
         "ms_per_step": ms_step,
         "value": flops / (ms_step * 1e-3) / 1e12,
@@ -271,6 +285,7 @@ def bench_prefill(args, w) -> dict:
             "prefill_us_in_step_mean": round(pf_step_ms * 1e3, 2),
             "store_us_mean": round(_launch_avg_ms(store, args.steps) * 1e3, 2),
             "decode_us_mean": round(_launch_avg_ms(decode, args.steps) * 1e3, 2),
+            "prefill_fp8_pool_us_mean": round(pf8_ms * 1e3, 2),
             "prefill_flops": flops,
             "prefill_tokens": tp,
             "decode_seqs": len(w.chunk_lens) - npf,
