@@ -304,6 +304,25 @@ int npd_qk_norm_rope_store(void* q_out, void* k_cache, void* v_cache,
                            float eps, int32_t dtype, void* stream);
 
 /*
+ * npd_qk_norm_rope_store into an FP8 (e4m3) pool (no reference counterpart;
+ * the reference's caches are fp16, nanoPD/engine/model_runner.py:24-31):
+ * q_out as above; the rotated k and the raw v, rounded to dtype as above, are
+ * stored as the e4m3 bytes of value / k_scale[kv head] (v_scale for v) with
+ * the rounding of npd_paged_kv_store_slots_fp8, so both paths write the same
+ * bytes. Caches are [num_blocks, num_kv_heads, block_size, head_dim] bytes.
+ */
+int npd_qk_norm_rope_store_fp8(void* q_out, void* k_cache, void* v_cache,
+                               const void* qkv, const int32_t* slot_mapping,
+                               const int32_t* positions, const float* inv_freq,
+                               const void* q_norm_weight, const void* k_norm_weight,
+                               const float* k_scale, const float* v_scale,
+                               int64_t num_tokens, int64_t num_heads,
+                               int64_t num_kv_heads, int64_t head_dim,
+                               int64_t num_blocks, int64_t block_size,
+                               int64_t qkv_stride_token, int64_t q_stride_token,
+                               float eps, int32_t dtype, void* stream);
+
+/*
  * Ragged-batch metadata packing on the GPU (no reference counterpart: the
  * reference re-tensorises its context dict per layer with host loops,
  * nanoPD/engine/model_runner.py:129-187, from nanoPD/engine/engine.py:45-90).

@@ -49,6 +49,9 @@ SIGNATURES = {
     "npd_kv_scatter_blocks": (ctypes.c_int, [_P, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P]),
     "npd_qk_norm_rope_store": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
                                               _I64, _I64, _I64, _I64, _I64, _I64, _F, _I32, _P]),
+    "npd_qk_norm_rope_store_fp8": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                                  _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+                                                  _F, _I32, _P]),
     "npd_pack_metadata": (ctypes.c_int, [_P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P,
                                          _P, _P]),
 }

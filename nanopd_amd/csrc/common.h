@@ -94,6 +94,18 @@ __device__ __forceinline__ uint32_t e4m3x2_to(uint32_t w) {
     return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.f, kHi));
 }
 
+// Largest finite OCP e4m3 magnitude, and x / scale clamped to it (NaN passes
+// through): the input of the e4m3 rounding of the FP8 pool's store.
+constexpr float kE4m3Max = 448.f;
+__device__ __forceinline__ float e4m3_clamp(float x) {
+  return x != x ? x : fminf(fmaxf(x, -kE4m3Max), kE4m3Max);
+}
+// One value -> its e4m3 byte: x / scale (IEEE fp32 division), clamped, then
+// rounded to the nearest e4m3 value, ties to even (v_cvt_pk_fp8_f32).
+__device__ __forceinline__ uint32_t e4m3_byte(float x, float scale) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(e4m3_clamp(x / scale), 0.f, 0, false) & 0xffu;
+}
+
 // Agent-scope relaxed atomic accesses: written through to, and read from, the
 // device-coherent level, so partials published by a workgroup on one XCD are
 // seen by a workgroup on another without an L2 writeback or invalidate.

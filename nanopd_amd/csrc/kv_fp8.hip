@@ -19,11 +19,8 @@ namespace {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kThreads = 256;
-constexpr float kE4m3Max = 448.f;
 
-__device__ __forceinline__ float clamp8(float x) {
-  return x != x ? x : fminf(fmaxf(x, -kE4m3Max), kE4m3Max);   // NaN passes through
-}
+__device__ __forceinline__ float clamp8(float x) { return npd::e4m3_clamp(x); }
 
 // 8 source elements (4 packed pairs) / scale -> 8 e4m3 bytes
 template <class TT>

@@ -20,6 +20,9 @@
 // apply_rotary_pos_emb rounds cos / sin and each product to the model dtype
 // first; the fp32 rotation here is the more accurate of the two and differs
 // from it by a few half-precision ulps at most.
+// FP8 pools (kF8): the rotated k and the raw v, rounded to the 2-byte type as
+// above, are stored as e4m3 bytes of value / scale[kv head] (the rounding of
+// npd_paged_kv_store_slots_fp8, so both paths write the same bytes).
 #include "common.h"
 
 namespace {
@@ -29,8 +32,10 @@ constexpr int kD = 128;
 
 struct RopeArgs {
   uint16_t* q_out;
-  uint16_t* k_cache;
-  uint16_t* v_cache;
+  void* k_cache;   // 2-byte elements, or e4m3 bytes (kF8)
+  void* v_cache;
+  const float* k_scale;   // kF8: per-kv-head scales
+  const float* v_scale;
   const uint16_t* qkv;
   const int32_t* slots;
   const int32_t* positions;
@@ -54,7 +59,7 @@ __device__ __forceinline__ float ld(const uint16_t* p) {
   return TT::lo((uint32_t)*p);
 }
 
-template <class TT>
+template <class TT, bool kF8>
 __global__ __launch_bounds__(kThreads) void qk_norm_rope_store_kernel(RopeArgs a) {
   const int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
   if (row >= a.rows) return;
@@ -72,9 +77,18 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_store_kernel(RopeArgs a
 
   if (hh >= a.heads + a.kv_heads) {   // v: plain store
     if (!store) return;
-    uint16_t* dst = a.v_cache + ((blk * a.kv_heads + (hh - a.heads - a.kv_heads)) * a.block_size + off) * kD;
-    dst[l] = src[l];
-    dst[l + 64] = src[l + 64];
+    const int kh = hh - a.heads - a.kv_heads;
+    const int64_t e = ((blk * a.kv_heads + kh) * a.block_size + off) * kD;
+    if constexpr (kF8) {
+      uint8_t* dst = static_cast<uint8_t*>(a.v_cache) + e;
+      const float sc = a.v_scale[kh];
+      dst[l] = (uint8_t)npd::e4m3_byte(x0, sc);
+      dst[l + 64] = (uint8_t)npd::e4m3_byte(x1, sc);
+    } else {
+      uint16_t* dst = static_cast<uint16_t*>(a.v_cache) + e;
+      dst[l] = src[l];
+      dst[l + 64] = src[l + 64];
+    }
     return;
   }
   const bool is_q = hh < a.heads;
@@ -91,7 +105,16 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_store_kernel(RopeArgs a
     dst = a.q_out + t * a.q_stride + (int64_t)hh * kD;
   } else {
     if (!store) return;
-    dst = a.k_cache + ((blk * a.kv_heads + (hh - a.heads)) * a.block_size + off) * kD;
+    const int kh = hh - a.heads;
+    const int64_t e = ((blk * a.kv_heads + kh) * a.block_size + off) * kD;
+    if constexpr (kF8) {
+      uint8_t* d8 = static_cast<uint8_t*>(a.k_cache) + e;
+      const float sc = a.k_scale[kh];
+      d8[l] = (uint8_t)npd::e4m3_byte(TT::lo(y0), sc);
+      d8[l + 64] = (uint8_t)npd::e4m3_byte(TT::lo(y1), sc);
+      return;
+    }
+    dst = static_cast<uint16_t*>(a.k_cache) + e;
   }
   dst[l] = y0;
   dst[l + 64] = y1;
@@ -99,16 +122,18 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_store_kernel(RopeArgs a
 
 }  // namespace
 
-extern "C" int npd_qk_norm_rope_store(void* q_out, void* k_cache, void* v_cache, const void* qkv,
-                                      const int32_t* slot_mapping, const int32_t* positions,
-                                      const float* inv_freq, const void* q_norm_weight,
-                                      const void* k_norm_weight, int64_t num_tokens,
-                                      int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
-                                      int64_t num_blocks, int64_t block_size,
-                                      int64_t qkv_stride_token, int64_t q_stride_token, float eps,
-                                      int32_t dtype, void* stream) {
+namespace {
+
+// Shared by the 2-byte and the FP8 entry points (k_scale / v_scale null for
+// 2-byte pools).
+int rope_impl(void* q_out, void* k_cache, void* v_cache, const void* qkv,
+              const int32_t* slot_mapping, const int32_t* positions, const float* inv_freq,
+              const void* q_norm_weight, const void* k_norm_weight, const float* k_scale,
+              const float* v_scale, int64_t num_tokens, int64_t num_heads, int64_t num_kv_heads,
+              int64_t head_dim, int64_t num_blocks, int64_t block_size, int64_t qkv_stride_token,
+              int64_t q_stride_token, float eps, int32_t dtype, void* stream, bool fp8,
+              const char* name) {
   using namespace npd;
-  const char* name = "npd_qk_norm_rope_store";
   if (dtype != NPD_DTYPE_F16 && dtype != NPD_DTYPE_BF16)
     return fail(NPD_E_DTYPE, "%s: unsupported dtype code %d (fp16/bf16 only)", name, dtype);
   if (head_dim != kD)
@@ -124,15 +149,17 @@ extern "C" int npd_qk_norm_rope_store(void* q_out, void* k_cache, void* v_cache,
     return fail(NPD_E_INVALID, "%s: eps must be non-negative", name);
   if (num_tokens == 0) return NPD_OK;
   if (!q_out || !k_cache || !v_cache || !qkv || !slot_mapping || !positions || !inv_freq ||
-      !q_norm_weight || !k_norm_weight)
+      !q_norm_weight || !k_norm_weight || (fp8 && (!k_scale || !v_scale)))
     return fail(NPD_E_INVALID, "%s: null pointer", name);
   const int64_t rows = num_tokens * (num_heads + 2 * num_kv_heads);
   const int64_t grid = (rows + 3) / 4;
   if (grid > INT32_MAX) return fail(NPD_E_INVALID, "%s: too many rows", name);
   RopeArgs a;
   a.q_out = static_cast<uint16_t*>(q_out);
-  a.k_cache = static_cast<uint16_t*>(k_cache);
-  a.v_cache = static_cast<uint16_t*>(v_cache);
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.k_scale = k_scale;
+  a.v_scale = v_scale;
   a.qkv = static_cast<const uint16_t*>(qkv);
   a.slots = slot_mapping;
   a.positions = positions;
@@ -148,9 +175,48 @@ extern "C" int npd_qk_norm_rope_store(void* q_out, void* k_cache, void* v_cache,
   a.q_stride = q_stride_token;
   a.eps = eps;
   hipStream_t st = as_stream(stream);
-  if (dtype == NPD_DTYPE_BF16)
-    hipLaunchKernelGGL(qk_norm_rope_store_kernel<BF16>, dim3((unsigned)grid), dim3(kThreads), 0, st, a);
-  else
-    hipLaunchKernelGGL(qk_norm_rope_store_kernel<F16>, dim3((unsigned)grid), dim3(kThreads), 0, st, a);
+  if (dtype == NPD_DTYPE_BF16) {
+    if (fp8)
+      hipLaunchKernelGGL((qk_norm_rope_store_kernel<BF16, true>), dim3((unsigned)grid), dim3(kThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((qk_norm_rope_store_kernel<BF16, false>), dim3((unsigned)grid), dim3(kThreads), 0, st, a);
+  } else {
+    if (fp8)
+      hipLaunchKernelGGL((qk_norm_rope_store_kernel<F16, true>), dim3((unsigned)grid), dim3(kThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((qk_norm_rope_store_kernel<F16, false>), dim3((unsigned)grid), dim3(kThreads), 0, st, a);
+  }
   return check_launch(name);
+}
+
+}  // namespace
+
+extern "C" int npd_qk_norm_rope_store(void* q_out, void* k_cache, void* v_cache, const void* qkv,
+                                      const int32_t* slot_mapping, const int32_t* positions,
+                                      const float* inv_freq, const void* q_norm_weight,
+                                      const void* k_norm_weight, int64_t num_tokens,
+                                      int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                                      int64_t num_blocks, int64_t block_size,
+                                      int64_t qkv_stride_token, int64_t q_stride_token, float eps,
+                                      int32_t dtype, void* stream) {
+  return rope_impl(q_out, k_cache, v_cache, qkv, slot_mapping, positions, inv_freq, q_norm_weight,
+                   k_norm_weight, nullptr, nullptr, num_tokens, num_heads, num_kv_heads, head_dim,
+                   num_blocks, block_size, qkv_stride_token, q_stride_token, eps, dtype, stream,
+                   false, "npd_qk_norm_rope_store");
+}
+
+extern "C" int npd_qk_norm_rope_store_fp8(void* q_out, void* k_cache, void* v_cache,
+                                          const void* qkv, const int32_t* slot_mapping,
+                                          const int32_t* positions, const float* inv_freq,
+                                          const void* q_norm_weight, const void* k_norm_weight,
+                                          const float* k_scale, const float* v_scale,
+                                          int64_t num_tokens, int64_t num_heads,
+                                          int64_t num_kv_heads, int64_t head_dim,
+                                          int64_t num_blocks, int64_t block_size,
+                                          int64_t qkv_stride_token, int64_t q_stride_token,
+                                          float eps, int32_t dtype, void* stream) {
+  return rope_impl(q_out, k_cache, v_cache, qkv, slot_mapping, positions, inv_freq, q_norm_weight,
+                   k_norm_weight, k_scale, v_scale, num_tokens, num_heads, num_kv_heads, head_dim,
+                   num_blocks, block_size, qkv_stride_token, q_stride_token, eps, dtype, stream,
+                   true, "npd_qk_norm_rope_store_fp8");
 }

@@ -454,7 +454,15 @@ def copy_blocks(k_cache: torch.Tensor, v_cache: torch.Tensor, block_pairs) -> No
     block_pairs: int32 [N, 2] device tensor of (src, dst), or a sequence of
     pairs (uploaded with one copy). Completes the CoW contract of
     BlockSpaceManager.append_slot (nanoPD/block_manager/block_manager.py:91-96).
+    FP8 pools (torch.float8_e4m3fn / uint8) are copied as the same bytes.
     """
+    if k_cache.dtype in FP8_DTYPES and v_cache.dtype == k_cache.dtype:
+        # a block copy moves bytes: a 1-byte pool is passed as 2-byte
+        # elements, half as many per row (head_dim is even)
+        _check(k_cache.is_contiguous() and v_cache.is_contiguous() and k_cache.size(-1) % 2 == 0,
+               "fp8 caches must be contiguous with an even head_dim")
+        k_cache = k_cache.view(torch.uint8).view(torch.bfloat16)
+        v_cache = v_cache.view(torch.uint8).view(torch.bfloat16)
     _cache_checks(k_cache, v_cache)
     dev = k_cache.device
     _check(k_cache.is_cuda, "caches must be on CUDA")
@@ -541,7 +549,9 @@ def load_kv(k_cache: torch.Tensor, v_cache: torch.Tensor, block_table, wire_k: t
 def qk_norm_rope_store(q_out: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                        qkv: torch.Tensor, slot_mapping: torch.Tensor, positions: torch.Tensor,
                        inv_freq: torch.Tensor, q_norm_weight: torch.Tensor,
-                       k_norm_weight: torch.Tensor, eps: float) -> None:
+                       k_norm_weight: torch.Tensor, eps: float,
+                       k_scale: torch.Tensor | None = None,
+                       v_scale: torch.Tensor | None = None) -> None:
     """Qwen3 attention prologue in one launch (replaces q_norm / k_norm,
     rotary embedding, the K/V copies and paged_kv_store of
     nanoPD/engine/model_runner.py:97-115, :142-146, :189-192).
@@ -552,8 +562,15 @@ def qk_norm_rope_store(q_out: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     norm weights: [D] in the cache dtype. Writes normalised + rotated q to
     q_out, normalised + rotated k and raw v to the caches at slot_mapping
     (negative slots are not stored). D = 128.
+    With ``k_scale`` / ``v_scale`` (fp32 [num_kv_heads]) the caches are an FP8
+    pool (torch.float8_e4m3fn or uint8): k and v are stored as the e4m3 bytes
+    of value / scale, as :func:`paged_kv_store_slots_fp8` rounds them.
     """
-    _cache_checks(k_cache, v_cache)
+    fp8 = k_scale is not None or v_scale is not None
+    if fp8:
+        _fp8_cache_checks(k_cache, v_cache, k_scale, v_scale)
+    else:
+        _cache_checks(k_cache, v_cache)
     dev = qkv.device
     _check(qkv.is_cuda, "qkv must be on CUDA")
     _same_device(dev, q_out, k_cache, v_cache, slot_mapping, positions, inv_freq, q_norm_weight,
@@ -568,7 +585,8 @@ def qk_norm_rope_store(q_out: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     _check(qkv.stride(1) == 1, "qkv rows must be contiguous")
     _check(q_out.stride(2) == 1 and q_out.stride(1) == d, "q_out heads must be contiguous")
     for x in (q_out, qkv, q_norm_weight, k_norm_weight):
-        _check(x.dtype == k_cache.dtype, "qkv / q_out / norm weights must have the cache dtype")
+        _check(x.dtype == (qkv.dtype if fp8 else k_cache.dtype),
+               "qkv / q_out / norm weights must have one dtype (the cache dtype of a 2-byte pool)")
     _check(q_norm_weight.numel() == d and k_norm_weight.numel() == d
            and q_norm_weight.is_contiguous() and k_norm_weight.is_contiguous(),
            "norm weights must be contiguous [head_dim]")
@@ -577,8 +595,16 @@ def qk_norm_rope_store(q_out: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     for x, nm in ((slot_mapping, "slot_mapping"), (positions, "positions")):
         _check(x.dim() == 1 and x.numel() >= t and x.is_contiguous(),
                f"{nm} must be a contiguous [num_tokens] tensor")
-    code = _dtype_code(k_cache, "qk_norm_rope_store")
+    code = _dtype_code(qkv if fp8 else k_cache, "qk_norm_rope_store")
     if t == 0:
+        return
+    if fp8:
+        _same_device(dev, k_scale, v_scale)
+        _lib.call("npd_qk_norm_rope_store_fp8", q_out.data_ptr(), k_cache.data_ptr(),
+                  v_cache.data_ptr(), qkv.data_ptr(), slot_mapping.data_ptr(),
+                  positions.data_ptr(), inv_freq.data_ptr(), q_norm_weight.data_ptr(),
+                  k_norm_weight.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr(), t, h, kvh, d,
+                  num_blocks, bs, qkv.stride(0), q_out.stride(0), float(eps), code, _stream(dev))
         return
     _lib.call("npd_qk_norm_rope_store", q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
               qkv.data_ptr(), slot_mapping.data_ptr(), positions.data_ptr(), inv_freq.data_ptr(),

@@ -79,11 +79,23 @@ class StepBatch:
 Attention = Callable[[int, torch.Tensor, torch.Tensor, torch.Tensor, StepBatch, torch.Tensor], None]
 
 
+def _check_kv_dtype(kv_cache_dtype: str) -> None:
+    if kv_cache_dtype not in ("auto", "fp8"):
+        raise ValueError(f"kv_cache_dtype must be 'auto' or 'fp8', not {kv_cache_dtype!r}")
+
+
 class PagedQwen3:
     def __init__(self, cfg: Qwen3Config, num_blocks: int, block_size: int = 16,
                  device: str | torch.device = "cuda", dtype: torch.dtype = torch.bfloat16,
                  seed: int = 0, attention: Optional[Attention] = None,
-                 fused_prologue: bool = True):
+                 fused_prologue: bool = True, kv_cache_dtype: str = "auto",
+                 kv_scale: float = 1.0 / 16):
+        """kv_cache_dtype "fp8": the K/V pools hold OCP e4m3 bytes with static
+        per-(layer, kv head) scales ``kv_scale`` (element = e4m3 * scale; the
+        default covers |x| <= 28), written by the fused prologue (or the FP8
+        slot store) and read by the FP8 prefill and decode ops. "auto": pools
+        in ``dtype``."""
+        _check_kv_dtype(kv_cache_dtype)
         self.cfg = cfg
         self.device = torch.device(device)
         self.dtype = dtype
@@ -122,8 +134,18 @@ class PagedQwen3:
         self.inv_freq = 1.0 / (cfg.rope_theta ** (torch.arange(0, D, 2, dtype=torch.float32,
                                                                device=self.device) / D))
         shape = (cfg.num_layers, num_blocks, KV, block_size, D)
-        self.k_cache = torch.zeros(shape, dtype=dtype, device=self.device)
-        self.v_cache = torch.zeros(shape, dtype=dtype, device=self.device)
+        self.fp8 = kv_cache_dtype == "fp8"
+        if self.fp8:
+            self.k_cache = torch.zeros(shape, dtype=torch.uint8,
+                                       device=self.device).view(torch.float8_e4m3fn)
+            self.v_cache = torch.zeros(shape, dtype=torch.uint8,
+                                       device=self.device).view(torch.float8_e4m3fn)
+            self.k_scale = torch.full((cfg.num_layers, KV), float(kv_scale), dtype=torch.float32,
+                                      device=self.device)
+            self.v_scale = self.k_scale.clone()
+        else:
+            self.k_cache = torch.zeros(shape, dtype=dtype, device=self.device)
+            self.v_cache = torch.zeros(shape, dtype=dtype, device=self.device)
 
     # -- pieces ------------------------------------------------------------
     def _rope(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
@@ -145,9 +167,10 @@ class PagedQwen3:
         cfg = self.cfg
         H, KV, D = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
         kc, vc = self.k_cache[li], self.v_cache[li]
+        scales = (self.k_scale[li], self.v_scale[li]) if self.fp8 else (None, None)
         if self.fused_prologue:
             pk.qk_norm_rope_store(q, kc, vc, qkv, b.meta.slot_mapping, b.meta.positions,
-                                  self.inv_freq, w["q_norm"], w["k_norm"], cfg.rms_eps)
+                                  self.inv_freq, w["q_norm"], w["k_norm"], cfg.rms_eps, *scales)
             return
         T = qkv.size(0)
         cos, sin = rope
@@ -156,21 +179,32 @@ class PagedQwen3:
         v = qkv[:, (H + KV) * D:].view(T, KV, D)
         q.copy_(self._rope(self._rms_norm_heads(qh, w["q_norm"]), cos, sin))
         k = self._rope(self._rms_norm_heads(k, w["k_norm"]), cos, sin)
-        pk.paged_kv_store_slots(kc, vc, k, v, b.meta.slot_mapping)
+        if self.fp8:
+            pk.paged_kv_store_slots_fp8(kc, vc, k, v, b.meta.slot_mapping, *scales)
+        else:
+            pk.paged_kv_store_slots(kc, vc, k, v, b.meta.slot_mapping)
 
     def _paged_attention(self, layer: int, q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor,
                          b: StepBatch, out: torch.Tensor) -> None:
         m, npf, tp = b.meta, b.num_prefill_seqs, b.num_prefill_tokens
         T = q.size(0)
         if npf:
-            pk.paged_prefill_attention(out[:tp], q[:tp], kc, vc, m.block_tables[:npf],
-                                       m.cu_seqlens_q[:npf + 1], m.seq_lens[:npf], self.scale,
-                                       self.block_size, m.max_blocks_per_seq,
-                                       max(1, b.max_prefill_q), m.max_seq_len)
+            args = (out[:tp], q[:tp], kc, vc, m.block_tables[:npf], m.cu_seqlens_q[:npf + 1],
+                    m.seq_lens[:npf], self.scale, self.block_size, m.max_blocks_per_seq,
+                    max(1, b.max_prefill_q))
+            if self.fp8:
+                pk.paged_prefill_attention_fp8(*args, self.k_scale[layer], self.v_scale[layer],
+                                               m.max_seq_len)
+            else:
+                pk.paged_prefill_attention(*args, m.max_seq_len)
         if T > tp:
-            pk.paged_attention_forward(out[tp:], q[tp:], kc, vc, m.block_tables[npf:],
-                                       m.seq_lens[npf:], self.scale, self.block_size,
-                                       m.max_blocks_per_seq, workspace=b.decode_workspace)
+            args = (out[tp:], q[tp:], kc, vc, m.block_tables[npf:], m.seq_lens[npf:], self.scale,
+                    self.block_size, m.max_blocks_per_seq)
+            if self.fp8:
+                pk.paged_attention_forward_fp8(*args, self.k_scale[layer], self.v_scale[layer],
+                                               workspace=b.decode_workspace)
+            else:
+                pk.paged_attention_forward(*args, workspace=b.decode_workspace)
 
     # -- forward -------------------------------------------------------------
     @torch.no_grad()

@@ -161,3 +161,62 @@ def test_serve_reports_throughput(device):
     assert res["requests"] == 5
     assert res["output_tokens"] == sum(r.max_new_tokens for r in reqs)
     assert res["tok_per_s"] > 0 and res["wall_s"] > 0
+
+
+def test_fp8_pool_step_matches_torch_attention(device):
+    """The model with an FP8 (e4m3) KV pool: the fused prologue stores e4m3
+    bytes, the FP8 prefill and decode ops read them. Against the same model
+    with the fp32 PyTorch attention over the dequantised pool (e4m3 * scale),
+    after identical random prefix/context bytes in both pools: the logits agree
+    as closely as the 2-byte pools' A/B, and the step's own K/V bytes are the
+    same in both pools (layer 0 sees identical inputs)."""
+    def torch_attention_fp8(model):
+        def attend(layer, q, kc, vc, b, out):
+            ks = model.k_scale[layer][None, :, None, None]
+            vs = model.v_scale[layer][None, :, None, None]
+            torch_attention(layer, q, kc.float() * ks, vc.float() * vs, b, out)
+        return attend
+
+    hip = PagedQwen3(SMALL, num_blocks=512, block_size=16, device=device, seed=3,
+                     kv_cache_dtype="fp8")
+    ref = PagedQwen3(SMALL, num_blocks=512, block_size=16, device=device, seed=3,
+                     kv_cache_dtype="fp8")
+    ref.attention = torch_attention_fp8(ref)
+    g = torch.Generator(device=device).manual_seed(9)
+    codes = torch.randint(0, 0x7E, hip.k_cache.shape, generator=g, device=device,
+                          dtype=torch.int32) | (torch.randint(0, 2, hip.k_cache.shape, generator=g,
+                                                              device=device, dtype=torch.int32) << 7)
+    for m in (hip, ref):
+        m.k_cache.view(torch.uint8).copy_(codes.to(torch.uint8))
+        m.v_cache.view(torch.uint8).copy_(codes.flip(0).to(torch.uint8))
+    del codes
+    b = _mixed_batch(hip, device)
+    lh = hip.forward(b)
+    lr = ref.forward(b)
+    torch.cuda.synchronize()
+    assert torch.isfinite(lh).all()
+    err = (lh - lr).abs().max().item()
+    spread = lr.abs().max().item()
+    print(f"fp8 pool: logits max-abs {err:.3e} (|logits| max {spread:.2f})")
+    assert err <= 2e-2 * max(1.0, spread)
+    assert (lh.argmax(-1) == lr.argmax(-1)).float().mean().item() >= 5 / 6
+    assert torch.equal(hip.k_cache[0].view(torch.uint8), ref.k_cache[0].view(torch.uint8))
+    assert torch.equal(hip.v_cache[0].view(torch.uint8), ref.v_cache[0].view(torch.uint8))
+
+
+def test_fp8_pool_served_batch(device):
+    """An engine over the FP8-pool model serves a small batch to completion
+    (prefill chunks, decodes, graph-replayed decode steps) with finite logits
+    and the requested output lengths."""
+    from nanopd_amd.graphs import DecodeGraphs
+    model = PagedQwen3(SMALL, num_blocks=512, block_size=16, device=device, seed=3,
+                       kv_cache_dtype="fp8")
+    reqs = make_requests(5, seed=5, prompt_median=120, prompt_clip=(20, 400), out_median=10,
+                         out_clip=(4, 16), vocab=SMALL.vocab)
+    eng = Engine(model, max_batch_size=4, budget=256, chunk=128,
+                 graphs=DecodeGraphs(model, max_width=32))
+    seqs = [eng.add(Request(r.rid, list(r.prompt), r.max_new_tokens)) for r in reqs]
+    while eng.sched.has_work():
+        eng.step()
+    for r, s in zip(reqs, seqs):
+        assert len(s.output) == r.max_new_tokens

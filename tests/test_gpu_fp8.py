@@ -241,3 +241,44 @@ def test_prefill_fp8_argument_checks(device):
         pk.paged_prefill_attention_fp8(out, q.to(device), dk.to(torch.bfloat16),
                                        dv.to(torch.bfloat16), *args[4:], ks.to(device),
                                        vs.to(device))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_fused_prologue_fp8_bytes(device, dtype):
+    """The fused q/k-norm + RoPE prologue into an FP8 pool writes the same
+    bytes as the 2-byte prologue followed by the FP8 store of its K/V rows,
+    and the same q; negative slots leave the pool untouched."""
+    g = torch.Generator(device=device).manual_seed(11)
+    T, H, KV, N, bs = 45, 16, 4, 32, 16
+    width = (H + 2 * KV) * 128
+    qkv = (torch.randn(T, width + 8, generator=g, device=device) * 1.5).to(dtype)[:, :width]
+    qw = (1.0 + 0.2 * torch.randn(128, generator=g, device=device)).to(dtype)
+    kw = (1.0 + 0.2 * torch.randn(128, generator=g, device=device)).to(dtype)
+    slots = torch.randperm(N * bs, generator=g, device=device)[:T].to(torch.int32)
+    slots[::7] = -1
+    pos = torch.randint(0, 40000, (T,), generator=g, device=device, dtype=torch.int32)
+    inv_freq = 1.0 / (1.0e6 ** (torch.arange(0, 128, 2, dtype=torch.float32, device=device) / 128))
+    ks = (0.01 + 0.05 * torch.rand(KV, generator=g, device=device)).float()
+    vs = (0.01 + 0.05 * torch.rand(KV, generator=g, device=device)).float()
+    # 2-byte prologue into a 2-byte pool, then the FP8 store of the stored rows
+    kc = torch.zeros(N, KV, bs, 128, dtype=dtype, device=device)
+    vc = torch.zeros_like(kc)
+    q2 = torch.empty(T, H, 128, dtype=dtype, device=device)
+    pk.qk_norm_rope_store(q2, kc, vc, qkv, slots, pos, inv_freq, qw, kw, 1e-6)
+    keep = slots >= 0
+    sl = slots[keep].long()
+    k_rows = kc.permute(0, 2, 1, 3).reshape(N * bs, KV, 128)[sl]
+    v_rows = vc.permute(0, 2, 1, 3).reshape(N * bs, KV, 128)[sl]
+    want_k = torch.full((N, KV, bs, 128), 0x5A, dtype=torch.uint8, device=device)
+    want_v = want_k.clone()
+    pk.paged_kv_store_slots_fp8(want_k.view(torch.float8_e4m3fn), want_v.view(torch.float8_e4m3fn),
+                                k_rows, v_rows, slots[keep].contiguous(), ks, vs)
+    # fused FP8 prologue
+    got_k = torch.full_like(want_k, 0x5A)
+    got_v = torch.full_like(want_v, 0x5A)
+    q8 = torch.empty_like(q2)
+    pk.qk_norm_rope_store(q8, got_k.view(torch.float8_e4m3fn), got_v.view(torch.float8_e4m3fn), qkv,
+                          slots, pos, inv_freq, qw, kw, 1e-6, k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    assert torch.equal(q8, q2)
+    assert torch.equal(got_k, want_k) and torch.equal(got_v, want_v)
