@@ -315,7 +315,8 @@ def bench_e2e(args, dev) -> int:
     from nanopd_amd.graphs import DecodeGraphs
     from nanopd_amd.qwen3 import QWEN3_8B, PagedQwen3
     t0 = time.perf_counter()
-    model = PagedQwen3(QWEN3_8B, num_blocks=args.kv_blocks, block_size=16, device=dev, seed=0)
+    model = PagedQwen3(QWEN3_8B, num_blocks=args.kv_blocks, block_size=16, device=dev, seed=0,
+                       kv_cache_dtype="fp8" if args.kv_fp8 else "auto")
     torch.cuda.synchronize()
     t_init = time.perf_counter() - t0
     # warm-up: kernels, GEMM heuristics and allocator, on short requests
@@ -352,6 +353,7 @@ def bench_e2e(args, dev) -> int:
         "config": {"workload": "cfg5_qwen3_8b_collocated", "requests": args.requests,
                    "arrival_rate": 8.0, "chunk": 512, "max_running": 16, "block_size": 16,
                    "kv_blocks": args.kv_blocks, "params": QWEN3_8B.num_params,
+                   "kv_cache": "fp8 e4m3, scale 1/16" if args.kv_fp8 else "bf16",
                    "decode_steps": "hip graphs" if graphs is not None else "eager"},
         "detail": {**{k: (round(v, 4) if isinstance(v, float) else v) for k, v in res.items()},
                    "init_s": round(t_init, 1), "graph_capture_s": round(t_graphs, 1)},
@@ -555,6 +557,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--requests", type=int, default=256, help="e2e: number of requests")
     ap.add_argument("--kv-blocks", type=int, default=12288, help="e2e: KV pool blocks of 16")
+    ap.add_argument("--kv-fp8", action="store_true",
+                    help="e2e: FP8 (e4m3) KV pool instead of bf16")
     ap.add_argument("--no-graphs", action="store_true",
                     help="e2e: launch decode-only steps kernel by kernel instead of from HIP graphs")
     args = ap.parse_args()
