@@ -749,6 +749,7 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
   };
 
   // ---------------- pass 1: scores ----------------
+  float runmax = -INFINITY;   // max of the scores this lane stored (its head: headmask)
   auto score_step = [&](const raw_t* kraw, int st) {
     float v[NV];   // v[h * 4 + i]: q slot h . token slot i
 #pragma unroll
@@ -779,7 +780,11 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
       const int h = headmask;
       const int ti = (tup1 ? 2 : 0) + (HELD == 2 ? e : (tup0 ? 1 : 0));
       const int tl = st * 16 + ti * 4 + r;
-      if (h < G) s_p[tl * GP + h] = (tl < ntok) ? v[e] * score_scale : -INFINITY;
+      if (h < G) {
+        const float sv = (tl < ntok) ? v[e] * score_scale : -INFINITY;
+        s_p[tl * GP + h] = sv;
+        runmax = fmaxf(runmax, sv);
+      }
     }
   };
   {
@@ -807,18 +812,15 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
   __syncthreads();
 
   // ---------------- pass 2: softmax statistics over the partition ----------------
+  // the maxima come from pass 1's running maxima (DPP wave reductions, one
+  // per head over the lanes that stored that head's scores)
   float m[GP], l[GP];
 #pragma unroll
-  for (int h = 0; h < GP; ++h) { m[h] = -INFINITY; l[h] = 0.f; }
-  const int ntl = nsteps * 16;
-  for (int t = lane; t < ntl; t += 64) {
-#pragma unroll
-    for (int h = 0; h < G; ++h) m[h] = fmaxf(m[h], s_p[t * GP + h]);
+  for (int h = 0; h < GP; ++h) {
+    m[h] = h < G ? wave_max_f(headmask == h ? runmax : -INFINITY) : -INFINITY;
+    l[h] = 0.f;
   }
-#pragma unroll
-  for (int h = 0; h < G; ++h)
-#pragma unroll
-    for (int x = 1; x < 64; x <<= 1) m[h] = fmaxf(m[h], shfl_xor(m[h], x));
+  const int ntl = nsteps * 16;
   if constexpr (kDot2) {
   // Probabilities of the token pair (8q + rr, 8q + 4 + rr) of each step, packed
   // as two 2-byte values per head: the pair a pass-3 lane multiplies into one
@@ -844,9 +846,7 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
   }
   }
 #pragma unroll
-  for (int h = 0; h < G; ++h)
-#pragma unroll
-    for (int x = 1; x < 64; x <<= 1) l[h] += shfl_xor(l[h], x);
+  for (int h = 0; h < G; ++h) l[h] = wave_sum_f(l[h]);
   __syncthreads();
 
   // ---------------- pass 3: probabilities x V ----------------
