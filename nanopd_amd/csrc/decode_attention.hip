@@ -936,12 +936,20 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
 #pragma unroll
     for (int b = 0; b < NBUF; ++b) pv_step(vb[b], st0 + b);
   }
+  // sum over the 4 rows (lane, lane ^ 16, ^ 32, ^ 48) with the gfx950 row
+  // swaps: v_permlane16_swap / v_permlane32_swap with both operands x hand
+  // every lane {x, x of lane ^ 16} (^ 32) in some order
 #pragma unroll
-  for (int x = 16; x < 64; x <<= 1)
+  for (int h = 0; h < G; ++h)
 #pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-      for (int d = 0; d < 8; ++d) acc[h][d] += shfl_xor(acc[h][d], x);
+    for (int d = 0; d < 8; ++d) {
+      const uint32_t x = __float_as_uint(acc[h][d]);
+      const auto p16 = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+      const float y = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
+      const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y),
+                                                        false, false);
+      acc[h][d] = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
+    }
 
   if (nparts == 1) {
     if (lane < 16) {
