@@ -106,6 +106,65 @@ __device__ __forceinline__ uint32_t e4m3_byte(float x, float scale) {
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(e4m3_clamp(x / scale), 0.f, 0, false) & 0xffu;
 }
 
+// ---------------------------------------------------------------------------
+// DPP lane exchanges within rows of 16 lanes, and wave reductions built on
+// them (every lane of the wave active).
+// ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
+                                                               CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppRor8 = 0x128;        // row_ror:8      -> lane ^ 8 within a row of 16
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror -> lane ^ 7 within 8
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int kDppMirror = 0x140;      // row_mirror      -> lane ^ 15 within a row of 16
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, false);
+}
+// Sum / max over the whole wave (all 64 lanes active), returned as a
+// wave-uniform value: four DPP steps give every lane its row's total, then the
+// four row totals are read into scalars.
+__device__ __forceinline__ int wave_sum_i(int x) {
+  x += dpp_i<kDppXor1>(x);
+  x += dpp_i<kDppXor2>(x);
+  x += dpp_i<kDppHalfMirror>(x);
+  x += dpp_i<kDppMirror>(x);
+  return __builtin_amdgcn_readlane(x, 0) + __builtin_amdgcn_readlane(x, 16) +
+         __builtin_amdgcn_readlane(x, 32) + __builtin_amdgcn_readlane(x, 48);
+}
+__device__ __forceinline__ float uniform_f(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
+}
+__device__ __forceinline__ float lane_f(float x, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+}
+__device__ __forceinline__ float wave_sum_f(float x) {
+  x += dpp<kDppXor1>(x);
+  x += dpp<kDppXor2>(x);
+  x += dpp<kDppHalfMirror>(x);
+  x += dpp<kDppMirror>(x);
+  return (lane_f(x, 0) + lane_f(x, 16)) + (lane_f(x, 32) + lane_f(x, 48));
+}
+__device__ __forceinline__ float wave_max_f(float x) {
+  x = fmaxf(x, dpp<kDppXor1>(x));
+  x = fmaxf(x, dpp<kDppXor2>(x));
+  x = fmaxf(x, dpp<kDppHalfMirror>(x));
+  x = fmaxf(x, dpp<kDppMirror>(x));
+  return fmaxf(fmaxf(lane_f(x, 0), lane_f(x, 16)), fmaxf(lane_f(x, 32), lane_f(x, 48)));
+}
+__device__ __forceinline__ int wave_max_i(int x) {
+  x = max(x, dpp_i<kDppXor1>(x));
+  x = max(x, dpp_i<kDppXor2>(x));
+  x = max(x, dpp_i<kDppHalfMirror>(x));
+  x = max(x, dpp_i<kDppMirror>(x));
+  return max(max(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
+             max(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
+}
+
 // Agent-scope relaxed atomic accesses: written through to, and read from, the
 // device-coherent level, so partials published by a workgroup on one XCD are
 // seen by a workgroup on another without an L2 writeback or invalidate.

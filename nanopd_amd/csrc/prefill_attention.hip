@@ -200,12 +200,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
       }
     }
     const int per_item = a.num_kv_heads * a.hgroups;   // workgroups per (sequence, tile, split)
-    int tot = n, nmax = n;
-#pragma unroll
-    for (int x = 1; x < 64; x <<= 1) {
-      tot += __shfl_xor(tot, x, 64);
-      nmax = max(nmax, __shfl_xor(nmax, x, 64));
-    }
+    const int tot = npd::wave_sum_i(n), nmax = npd::wave_max_i(n);   // DPP, wave-uniform
     const int avg = (int)(((int64_t)tot * per_item + a.num_cus - 1) / a.num_cus);
     int parts = avg > 0 ? nmax / avg : 1;
     parts = parts < 1 ? 1 : parts;
@@ -237,17 +232,18 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
       id -= c;
     }
     if (sel < 0) {
-      for (int b = ks; b >= 0; --b) {
-        const uint64_t m = __ballot(last == b);
-        const int c = __popcll(m) * per_item;
-        if (id < c) {
-          sel = nth(m, id / per_item);
-          j = __builtin_amdgcn_readlane(full, sel);
-          break;
-        }
-        id -= c;
+      // items in buckets >= b, non-increasing in b; item id is in the last
+      // bucket b with from(b) > id (binary search over ballot counts)
+      auto from = [&](int b) -> int { return __popcll(__ballot(last >= b)) * per_item; };
+      if (id >= from(0)) return;   // past the last item
+      int lo = 0, hi = ks;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (from(mid) > id) lo = mid; else hi = mid - 1;
       }
-      if (sel < 0) return;   // past the last item
+      id -= from(lo + 1);
+      sel = nth(__ballot(last == lo), id / per_item);
+      j = __builtin_amdgcn_readlane(full, sel);
     }
     const int rem = id % per_item;
     kh = rem % a.num_kv_heads;
