@@ -56,6 +56,18 @@ def _events_ms(fn, iters: int, pre=None) -> list:
     return times
 
 
+def _settle(step, seconds: float = 0.3) -> None:
+    """Untimed: repeats a step for `seconds` before the warm-up steps, so that
+    the GPU has left its idle clocks when the timed steps start (on a fresh
+    process the first tenth of a second of launches ran 3-7% slower)."""
+    torch.cuda.synchronize()
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(20):
+            step()
+        torch.cuda.synchronize()
+
+
 def _launch_avg_ms(fn, iters: int = 50) -> float:
     """Average duration (ms) of one launch of fn, HIP events around `iters`
     back-to-back launches on the current stream. A spin kernel queued first
@@ -121,6 +133,7 @@ def bench_decode(args, w) -> dict:
         pk.paged_attention_forward(out, w.query, w.k_cache, w.v_cache, w.block_tables, w.seq_lens,
                                    w.scale, w.block_size, w.max_blocks_per_seq, workspace=ws)
 
+    _settle(lambda: [store(), attend()])
     for _ in range(args.warmup):
         store()
         attend()
@@ -232,6 +245,7 @@ def bench_prefill(args, w) -> dict:
         pk.paged_attention_forward(out[tp:], w.query[tp:], w.k_cache, w.v_cache, bt_d, cl_d,
                                    w.scale, w.block_size, mb)
 
+    _settle(lambda: [store(), prefill(), decode()])
     for _ in range(args.warmup):
         store()
         prefill()
@@ -367,6 +381,7 @@ def bench_copy(args, dev) -> int:
     n = 256 << 20
     src = torch.ones(n, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
+    _settle(lambda: [dst.copy_(src)])
     for _ in range(args.warmup):
         dst.copy_(src)
     torch.cuda.synchronize()
@@ -416,6 +431,7 @@ def bench_decode_fp8(args, w) -> int:
         pk.paged_attention_forward_fp8(out, w.query, k8, v8, w.block_tables, w.seq_lens, w.scale,
                                        w.block_size, w.max_blocks_per_seq, ks, vs, workspace=ws)
 
+    _settle(lambda: [store(), attend()])
     for _ in range(args.warmup):
         store()
         attend()
@@ -476,6 +492,7 @@ def bench_transfer(args, dev) -> int:
         pk.extract_kv(k, v, src, wk, wv)
         pk.load_kv(k2, v2, dst, wk, wv)
 
+    _settle(lambda: [step()])
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
