@@ -21,7 +21,8 @@
  *     pool is skipped by the stores, and attention clamps block ids into the
  *     pool so that no access leaves it.
  *   - Thread-safe and reentrant: no mutable global state beyond the per-thread
- *     error message.
+ *     error message, except the static scratch of npd_paged_attention_noalloc
+ *     (one per device, set up once under a lock; see there).
  * Citations are relative to the reference tree; PA/ = nanoPD/paged_attention/.
  */
 #ifndef NANOPD_H
@@ -143,6 +144,36 @@ int npd_paged_attention(void* out, const void* query,
                         int64_t out_stride_seq, int64_t out_stride_head,
                         void* workspace, int64_t workspace_bytes,
                         int32_t dtype, void* stream);
+
+/* Size of the static device scratch of npd_paged_attention_noalloc (64 MiB). */
+#define NPD_NOALLOC_SCRATCH_BYTES (64LL << 20)
+
+/*
+ * npd_paged_attention without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, serving loops that forbid
+ * hipMalloc). No counterpart in the reference (its decode op allocates
+ * nothing because it has no split-context path).
+ * Same arguments, semantics and results as npd_paged_attention; it calls no
+ * hipMalloc / hipFree. Its workspace is a static device array of
+ * NPD_NOALLOC_SCRATCH_BYTES that each GPU the library runs on holds until the
+ * process ends; shapes whose npd_paged_attention_workspace_size exceeds it
+ * fail with NPD_E_WORKSPACE (e.g. 64 sequences of up to 4096 tokens need
+ * 17.3 MiB, 8 of up to 32768 need 18.3 MiB). The first call on a device looks
+ * up the array's address and enqueues the clear of its counter region on
+ * `stream`. All calls on one GPU share the array: calls that overlap on one
+ * GPU (concurrent streams or threads) race and must be serialised by the
+ * caller; stream-ordered calls are safe, since every call leaves the counters
+ * at zero.
+ */
+int npd_paged_attention_noalloc(void* out, const void* query,
+                                const void* key_cache, const void* value_cache,
+                                const int32_t* block_tables, const int32_t* seq_lens,
+                                int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads,
+                                int64_t head_dim, int64_t num_blocks, int64_t block_size,
+                                int64_t max_blocks_per_seq, float scale,
+                                int64_t q_stride_seq, int64_t q_stride_head,
+                                int64_t out_stride_seq, int64_t out_stride_head,
+                                int32_t dtype, void* stream);
 
 /*
  * Bytes of device workspace npd_paged_prefill_attention needs.

@@ -14,6 +14,8 @@ LIB_PATH = Path(__file__).resolve().parent / "lib" / "libnanopd_hip.so"
 
 NPD_DTYPE_F16 = 0
 NPD_DTYPE_BF16 = 1
+# size of the static scratch of npd_paged_attention_noalloc (NPD_NOALLOC_SCRATCH_BYTES)
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 # name -> (restype, argtypes)
 _P = ctypes.c_void_p
@@ -33,6 +35,9 @@ SIGNATURES = {
     "npd_paged_attention": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
                                            _I64, _I64, _F, _I64, _I64, _I64, _I64, _P, _I64, _I32,
                                            _P]),
+    "npd_paged_attention_noalloc": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
+                                                   _I64, _I64, _I64, _F, _I64, _I64, _I64, _I64,
+                                                   _I32, _P]),
     "npd_paged_attention_fp8": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64,
                                                _I64, _I64, _I64, _I64, _F, _I64, _I64, _I64, _I64,
                                                _P, _I64, _I32, _P]),

@@ -1544,3 +1544,83 @@ extern "C" int npd_paged_attention_fp8(void* out, const void* query, const void*
                         out_stride_head, k_scale, v_scale, workspace, workspace_bytes, dtype,
                         stream, true, "npd_paged_attention_fp8");
 }
+
+// ---------------------------------------------------------------------------
+// No-allocation variant of npd_paged_attention: the workspace is `scratch`, a
+// static device array that every GPU the library runs on holds until the
+// process ends. Calls on one GPU share it (calls that overlap on one GPU
+// race); every call leaves its merge counters at zero, as with a caller's
+// workspace, and the counter region is cleared once per device at set-up.
+// ---------------------------------------------------------------------------
+#include <mutex>
+
+namespace {
+
+constexpr int64_t kScratchBytes = NPD_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchDevices];   // device address of `scratch`, per device
+
+__global__ __launch_bounds__(256) void clear_counters_kernel(u32x4* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = u32x4{0, 0, 0, 0};
+}
+
+// The device address of the current device's `scratch` (nullptr and an error
+// message on failure). The first call on a device looks the address up and
+// enqueues the clear of its counter region on `st`, ahead of the caller's
+// kernels.
+void* scratch_of_current_device(hipStream_t st, const char* name) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices) {
+    npd::fail(NPD_E_LAUNCH, "%s: no usable current device (%d)", name, dev);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev]) return g_scratch_ptr[dev];
+  void* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !ptr) {
+    npd::fail(NPD_E_LAUNCH, "%s: hipGetSymbolAddress(scratch): %s", name, hipGetErrorString(e));
+    return nullptr;
+  }
+  const int64_t n = npd::kCounterBytes / 16;
+  hipLaunchKernelGGL(clear_counters_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                     static_cast<u32x4*>(ptr), n);
+  if (npd::check_launch(name) != NPD_OK) return nullptr;
+  g_scratch_ptr[dev] = ptr;
+  return ptr;
+}
+
+}  // namespace
+
+extern "C" int npd_paged_attention_noalloc(void* out, const void* query, const void* key_cache,
+                                           const void* value_cache, const int32_t* block_tables,
+                                           const int32_t* seq_lens, int64_t num_seqs,
+                                           int64_t num_heads, int64_t num_kv_heads,
+                                           int64_t head_dim, int64_t num_blocks,
+                                           int64_t block_size, int64_t max_blocks_per_seq,
+                                           float scale, int64_t q_stride_seq,
+                                           int64_t q_stride_head, int64_t out_stride_seq,
+                                           int64_t out_stride_head, int32_t dtype, void* stream) {
+  const char* name = "npd_paged_attention_noalloc";
+  const int64_t need = npd_paged_attention_workspace_size(num_seqs, num_heads, num_kv_heads,
+                                                          head_dim, block_size, max_blocks_per_seq);
+  if (need > kScratchBytes)
+    return npd::fail(NPD_E_WORKSPACE,
+                     "%s: these shapes need %lld bytes of workspace, above the %lld-byte static "
+                     "scratch; call npd_paged_attention with a workspace", name, (long long)need,
+                     (long long)kScratchBytes);
+  void* ws = nullptr;
+  if (num_seqs > 0 && need > 0) {
+    ws = scratch_of_current_device(npd::as_stream(stream), name);
+    if (!ws) return NPD_E_LAUNCH;
+  }
+  return attention_impl(out, query, key_cache, value_cache, block_tables, seq_lens, num_seqs,
+                        num_heads, num_kv_heads, head_dim, num_blocks, block_size,
+                        max_blocks_per_seq, scale, q_stride_seq, q_stride_head, out_stride_seq,
+                        out_stride_head, nullptr, nullptr, ws, ws ? kScratchBytes : 0, dtype,
+                        stream, false, name);
+}

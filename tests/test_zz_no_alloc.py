@@ -1,0 +1,90 @@
+"""GPU test of npd_paged_attention_noalloc (the decode entry point that
+allocates nothing: its workspace is a static device array) against
+npd_paged_attention with a caller workspace, both called through the C-ABI.
+
+Two calls in a row on the same GPU share the static array; the second has a
+smaller input (fewer sequences, shorter contexts, another dtype), so it runs
+over what the first left there. Outputs must be bit-identical to the existing
+entry point's (same kernels, same partition and merge order), and within the
+attention tolerance of the float64 oracle. Shapes beyond the scratch size are
+refused before any launch."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from nanopd_amd import _lib
+from nanopd_amd import paged_kernels as pk
+from tests.helpers import ATOL, bits, max_abs, oracle_decode
+
+pytestmark = pytest.mark.gpu
+
+_CODE = {torch.float16: _lib.NPD_DTYPE_F16, torch.bfloat16: _lib.NPD_DTYPE_BF16}
+
+
+def _inputs(num_seqs, heads, kv_heads, ctx_max, dtype, device, seed):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    bs, d = 16, 128
+    lens = torch.randint(1, ctx_max + 1, (num_seqs,), generator=g)
+    lens[0] = ctx_max
+    nbs = [(int(s) + bs - 1) // bs for s in lens]
+    mb, total = max(nbs), sum(nbs)
+    q = (torch.randn(num_seqs, heads, d, generator=g) * 0.5).to(dtype)
+    kc = (torch.randn(total, kv_heads, bs, d, generator=g) * 0.5).to(dtype)
+    vc = (torch.randn(total, kv_heads, bs, d, generator=g) * 0.5).to(dtype)
+    order = torch.randperm(total, generator=g)
+    bt = torch.zeros(num_seqs, mb, dtype=torch.int32)
+    o = 0
+    for i, n in enumerate(nbs):
+        bt[i, :n] = order[o:o + n]
+        o += n
+    sl = lens.to(torch.int32)
+    return [t.to(device) for t in (q, kc, vc, bt, sl)] + [mb]
+
+
+def _noalloc(out, q, kc, vc, bt, sl, mb):
+    s, h, d = q.shape
+    nb, kvh, bs, _ = kc.shape
+    return _lib.load().npd_paged_attention_noalloc(
+        out.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(), sl.data_ptr(),
+        s, h, kvh, d, nb, bs, mb, d ** -0.5, q.stride(0), q.stride(1), out.stride(0),
+        out.stride(1), _CODE[q.dtype], ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+
+
+def _with_workspace(q, kc, vc, bt, sl, mb):
+    out = torch.full_like(q, float("nan"))
+    pk.paged_attention_forward(out, q, kc, vc, bt, sl, q.size(2) ** -0.5, kc.size(2), mb)
+    return out
+
+
+@pytest.mark.parametrize("first,second", [
+    # (num_seqs, heads, kv_heads, ctx_max, dtype, seed)
+    ((96, 32, 8, 4096, torch.bfloat16, 1), (8, 32, 8, 2000, torch.float16, 2)),
+    ((8, 32, 8, 32768, torch.bfloat16, 3), (4, 12, 2, 511, torch.float16, 4)),
+])
+def test_noalloc_matches_workspace_entry_point(device, first, second):
+    for num_seqs, heads, kvh, ctx_max, dtype, seed in (first, second):
+        print(f"noalloc case: seqs {num_seqs} heads {heads}/{kvh} ctx {ctx_max} {dtype}",
+              flush=True)
+        q, kc, vc, bt, sl, mb = _inputs(num_seqs, heads, kvh, ctx_max, dtype, device, seed)
+        want = _with_workspace(q, kc, vc, bt, sl, mb)
+        got = torch.full_like(q, float("nan"))
+        rc = _noalloc(got, q, kc, vc, bt, sl, mb)
+        assert rc == 0, _lib.load().npd_last_error()
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(got), bits(want)), "differs from npd_paged_attention"
+        err = max_abs(got, oracle_decode(q, kc, vc, bt, sl, q.size(2) ** -0.5))
+        assert err <= ATOL[dtype], f"max-abs {err} vs the oracle"
+
+
+def test_noalloc_refuses_shapes_beyond_scratch(device):
+    # 64 sequences with 65536-token tables need far more than the scratch:
+    # refused before any pointer is touched
+    need = pk.attention_workspace_bytes(64, 32, 8, 128, 16, 4096)
+    assert need > _lib.NOALLOC_SCRATCH_BYTES
+    fake = 0x1000
+    rc = _lib.load().npd_paged_attention_noalloc(fake, fake, fake, fake, fake, fake, 64, 32, 8,
+                                                 128, 1 << 16, 16, 4096, 0.088, 4096, 128, 4096,
+                                                 128, _lib.NPD_DTYPE_BF16, None)
+    assert rc == -4 and b"static scratch" in _lib.load().npd_last_error()
