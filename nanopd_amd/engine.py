@@ -184,7 +184,18 @@ class Engine:
         return batch
 
     def commit(self, plan: StepPlan, tokens: list, now: float = 0.0) -> None:
-        """Applies a step's sampled tokens (one per sample row, in order)."""
+        """Applies a step's sampled tokens (one per sample row, in order).
+        Raises if a token id is outside [0, vocab): argmax cannot produce one,
+        so it means memory that held the step's tokens was overwritten."""
+        vocab = self.model.cfg.vocab
+        for x in tokens:
+            if not 0 <= x < vocab:
+                shapes = {"step": self.steps, "prefill": None if plan.prefill is None else
+                          (plan.prefill.req.rid, plan.chunk, plan.is_last),
+                          "decodes": [(s.req.rid, s.num_computed) for s in plan.decodes],
+                          "tokens": tokens}
+                raise RuntimeError(f"token id {x} (0x{x & 0xffffffffffffffff:016x}) outside "
+                                   f"[0, {vocab}) in step {shapes}")
         k = 0
         t = self.clock() if tokens else now
         if plan.prefill is not None:

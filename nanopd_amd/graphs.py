@@ -11,10 +11,12 @@ inputs are static device buffers:
   -> pack_metadata kernel (inside the graph) -> positions, slots, tables, ...
   -> embedding, 36 layers, final norm, LM head, argmax -> tokens [B]
 
-A step fills a pinned host copy of `staging`, uploads it with one copy and
-replays the graph. Rows past the real batch are padding: position -1 and an
-all-zero table give slot -1 (nothing is stored) and a context of 0 (decode
-attention writes zeros), and their tokens are dropped. Every kernel argument
+A step fills a pinned host copy of `staging`, uploads it with one blocking
+copy and replays the graph; argmax writes the graph's token buffer directly,
+so the graph holds kernel nodes only, no memcpy node. Rows past the real
+batch are padding: position -1 and an all-zero table give slot -1 (nothing
+is stored) and a context of 0 (decode attention writes zeros), and their
+tokens are dropped. Every kernel argument
 (batch size, table width, workspace pointers) is fixed per graph, so the
 table width is bucketed (powers of two) and the decode workspace is
 allocated, zeroed, before capture; the graph records no memset.
@@ -31,7 +33,9 @@ BATCH_BUCKETS = (1, 2, 4, 8, 16)
 
 
 class _Graph:
-    def __init__(self, model: PagedQwen3, batch: int, width: int, pool=None):
+    def __init__(self, model: PagedQwen3, batch: int, width: int, pool=None, debug: bool = False):
+        """debug: keep the captured graph (its nodes can be listed through
+        CUDAGraph.raw_cuda_graph)."""
         dev = model.device
         cfg = model.cfg
         self.batch, self.width = batch, width
@@ -56,7 +60,7 @@ class _Graph:
         # the warm-up runs see padding rows only (no slot is written)
         self._fill([], [], [])
         self.staging.copy_(self.host)
-        self.graph = torch.cuda.CUDAGraph()
+        self.graph = torch.cuda.CUDAGraph(keep_graph=debug)
         side = torch.cuda.Stream(dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):
@@ -82,7 +86,10 @@ class _Graph:
         batch = StepBatch(input_ids=st[:b].long(), meta=meta, num_prefill_seqs=0,
                           num_prefill_tokens=0, sample_rows=None, max_prefill_q=0,
                           decode_workspace=self.workspace)
-        self.tokens.copy_(self.model.forward(batch).argmax(dim=-1))
+        # argmax writes the token buffer itself: no device-to-device copy node
+        # follows it in the graph (the argmax result of a separate tensor would
+        # sit in the shared graph pool, over other graphs' bf16 intermediates)
+        torch.argmax(self.model.forward(batch), dim=-1, out=self.tokens)
 
     def _fill(self, positions: list, tables: list, last_tokens: list) -> None:
         """Writes a step's staging image into the pinned host buffer: real rows
@@ -105,7 +112,8 @@ class _Graph:
         """One decode step of len(positions) <= batch sequences."""
         n = len(positions)
         self._fill(positions, tables, last_tokens)
-        self.staging.copy_(self.host, non_blocking=True)
+        # a blocking upload: the replay starts from a complete staging image
+        self.staging.copy_(self.host)
         self.graph.replay()
         return self.tokens[:n].tolist()   # synchronises: `host` is free again
 

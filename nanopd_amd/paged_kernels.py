@@ -21,6 +21,7 @@ There is no CPU or PyTorch fallback: without the built library every op raises.
 """
 from __future__ import annotations
 
+import threading
 from typing import NamedTuple, Sequence
 
 import torch
@@ -217,17 +218,20 @@ def paged_kv_store_slots_fp8(k_cache: torch.Tensor, v_cache: torch.Tensor, k_src
 # decode path keeps per-(sequence, kv-head) merge counters in the workspace and
 # leaves them zero after every call, so zeroing once is enough.
 _workspaces: dict = {}
+_workspaces_lock = threading.Lock()
 
 
 def _decode_workspace(dev: torch.device, stream: int, need: int, kind: str = "decode") -> torch.Tensor:
     """A zero-filled workspace cached per (device, stream, op): the kernels
-    leave their merge counters at zero, so it is cleared only when allocated."""
+    leave their merge counters at zero, so it is cleared only when allocated.
+    The lookup and the insert hold a lock (callers on several host threads)."""
     key = (dev.index, stream, kind)
-    ws = _workspaces.get(key)
-    if ws is None or ws.numel() < need:
-        ws = torch.zeros(need, dtype=torch.uint8, device=dev)
-        _workspaces[key] = ws
-    return ws
+    with _workspaces_lock:
+        ws = _workspaces.get(key)
+        if ws is None or ws.numel() < need:
+            ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+            _workspaces[key] = ws
+        return ws
 
 
 def attention_workspace_bytes(num_seqs: int, num_heads: int, num_kv_heads: int, head_dim: int,

@@ -246,13 +246,10 @@ def test_config4_long_context_with_cow_fork(device):
         assert torch.equal(w.k_cache[src], w.k_cache[dst]) and torch.equal(w.v_cache[src], w.v_cache[dst])
     # children (rows 8, 9) read a copied last block: identical to their parents
     assert torch.equal(out[8], out[6]) and torch.equal(out[9], out[7])
-    # oracle on a subset (the two shortest and the two longest parents)
-    idx = [0, 1, 6, 7]
-    sub = lambda t: t[idx]  # noqa: E731
-    want = oracle_decode(sub(w.query), w.k_cache, w.v_cache, sub(w.block_tables),
-                         sub(w.seq_lens), w.scale)
-    err = max_abs(out[idx], want)
-    print(f"cfg4 max-abs {err:.2e}")
+    # every row (8 parents of 8k-32k tokens, 2 children) against the oracle
+    want = oracle_decode(w.query, w.k_cache, w.v_cache, w.block_tables, w.seq_lens, w.scale)
+    err = max_abs(out, want)
+    print(f"cfg4 max-abs {err:.2e} over all {out.size(0)} rows")
     assert err <= ATOL[torch.bfloat16]
 
 

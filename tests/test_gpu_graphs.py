@@ -97,3 +97,38 @@ def test_steps_without_a_graph_fall_back(device):
     assert graphs.bucket(3, 17) is None and graphs.bucket(17, 4) is None
     assert graphs.decode([5], [[1] * 17], [0]) is None
     assert graphs.bucket(3, 5) == (4, 16)
+
+
+
+def _node_types(graph_handle: int) -> list:
+    """hipGraphNodeType of every node of a captured graph (HIP runtime API)."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    n = ctypes.c_size_t(0)
+    assert hip.hipGraphGetNodes(ctypes.c_void_p(graph_handle), None, ctypes.byref(n)) == 0
+    nodes = (ctypes.c_void_p * n.value)()
+    assert hip.hipGraphGetNodes(ctypes.c_void_p(graph_handle), nodes, ctypes.byref(n)) == 0
+    types = []
+    for i in range(n.value):
+        t = ctypes.c_int(-1)
+        assert hip.hipGraphNodeGetType(ctypes.c_void_p(nodes[i]), ctypes.byref(t)) == 0
+        types.append(t.value)
+    return types
+
+
+def test_decode_graph_holds_kernel_nodes_only(device):
+    """The captured decode step is kernel nodes only: no memcpy node (argmax
+    writes the token buffer itself; the staging upload happens before the
+    replay) and no memset node."""
+    from nanopd_amd.graphs import _Graph
+    model = _model(device)
+    g = _Graph(model, 4, 32, debug=True)
+    types = _node_types(g.graph.raw_cuda_graph())
+    kinds = {t: types.count(t) for t in set(types)}
+    print(f"decode graph nodes by hipGraphNodeType: {kinds}")
+    assert types and set(types) == {0}, kinds   # hipGraphNodeTypeKernel only
+    # and the replay (instantiated on first use) gives the eager step's tokens
+    for _ in range(2):
+        got = g.run([20, 40], [[1, 2], [3, 4, 5]], [7, 8])
+        want = _eager_tokens(model, [20, 40], [[1, 2], [3, 4, 5]], [7, 8], 4, 32)
+        assert got == want
