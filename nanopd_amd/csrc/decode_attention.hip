@@ -99,7 +99,10 @@ struct DecodeArgs {
   const float* v_scale;
   int num_seqs;
   int2* items;       // fast path: (unit, partition) work list
-  int num_kv_heads;
+  int num_kv_heads;  // kv heads of the work units: pool_kv_heads * kv_split
+  int kv_split;      // work units per pool kv head: a group of G > 8 query
+                     // heads is served as kv_split groups of G / kv_split
+  int pool_kv_heads; // kv heads of the cache layout
   int block_size;
   int num_blocks;
   int max_bps;
@@ -210,14 +213,15 @@ __global__ __launch_bounds__(64) void decode_partition_kernel(DecodeArgs a) {
   for (int h = 0; h < G; ++h) qv[h] = *reinterpret_cast<const u32x4*>(qbase + h * a.q_stride_head);
   __syncthreads();
 
-  const int64_t head_off = (int64_t)kh * bs;  // rows of kv-head kh inside a block
+  // rows of the unit's pool kv head inside a block
+  const int64_t head_off = (int64_t)(kh / a.kv_split) * bs;
   auto row_index = [&](int tl) -> int64_t {
     // 16-byte index of chunk j of token tl (clamped to the last valid token)
     const int t = t0 + (tl < ntok ? tl : ntok - 1);
     const int lb = t / bs;
     const int off = t - lb * bs;
     const int blk = s_blk[lb - b0];
-    return (((int64_t)blk * a.num_kv_heads * bs) + head_off + off) * LPT + j;
+    return (((int64_t)blk * a.pool_kv_heads * bs) + head_off + off) * LPT + j;
   };
 
   // ---------------- pass 1: scores ----------------
@@ -682,11 +686,12 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
   }
   const int voff = (r * 16) + j;   // offset (in lane chunks) of the lane's chunk: slot i is token i*4 + r
   // scores in log2 units (times the K scale of an fp8 pool); output scale
-  const float score_scale = kF8 ? a.scale_log2 * a.k_scale[kh] : a.scale_log2;
-  const float out_scale = kF8 ? a.v_scale[kh] : 1.f;
+  const int pkh = kh / a.kv_split;   // the unit's kv head in the pool
+  const float score_scale = kF8 ? a.scale_log2 * a.k_scale[pkh] : a.scale_log2;
+  const float out_scale = kF8 ? a.v_scale[pkh] : 1.f;
 
-  const int64_t head_rows = (int64_t)kh * BS;            // rows of head kh in a block
-  const int64_t blk_rows = (int64_t)a.num_kv_heads * BS; // rows per block
+  const int64_t head_rows = (int64_t)pkh * BS;            // rows of head pkh in a block
+  const int64_t blk_rows = (int64_t)a.pool_kv_heads * BS; // rows per block
   auto step_base = [&](int st) -> int64_t {              // chunk index of the step's first row
     const int bi = st / SPB;   // wave-uniform
     const int blk = __builtin_amdgcn_readlane(bi < 64 ? myblk0 : myblk1, bi & 63);
@@ -1052,6 +1057,16 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
     auto before = [&](int p) -> int { return wave_sum_i(full < p ? full : p) * kvh; };
     const int maxfull = wave_max_i(full);
     int id = blockIdx.x, seq = -1;
+    if (a.kv_split > 1) {
+      // The kv_split units of one pool kv head have consecutive item ids
+      // (every level and bucket starts at a multiple of the unit count).
+      // Their blockIdx values are made 8 apart -- the same XCD, as
+      // workgroups go to the 8 XCDs round-robin -- so the K/V rows the first
+      // unit reads are in that XCD's L2 for the others. The grid is a
+      // multiple of 8 * kv_split, so this permutes [0, grid).
+      const int span = 8 * a.kv_split, q = id / span, rem = id - q * span;
+      id = q * span + (rem & 7) * a.kv_split + (rem >> 3);
+    }
     part = 0;
     const int nfull = before(maxfull);
     if (id < nfull) {
@@ -1241,6 +1256,10 @@ int64_t fast_grid(const DecodeArgs& a, int64_t units) {
     h = h < 2 * kFastMinItemsActual ? h : 2 * kFastMinItemsActual;
     n = n > h ? n : h;
   }
+  if (a.kv_split > 1 && a.num_seqs <= kInlineSchedMax) {   // whole spans of the XCD permutation
+    const int64_t span = 8 * a.kv_split;
+    n = (n + span - 1) / span * span;
+  }
   return n;
 }
 
@@ -1340,6 +1359,17 @@ int dispatch_d(int64_t d, int g, const DecodeArgs& a, int64_t units, hipStream_t
   }
 }
 
+// Work units per pool kv head. The kernels keep a group's queries and
+// accumulators in registers for at most 8 query heads: a larger group is
+// served as kv_split equal groups of at most 8 heads (the smallest such
+// split), each reading the kv head's K/V once.
+int kv_split_of(int64_t num_heads, int64_t num_kv_heads) {
+  const int64_t g = num_kv_heads > 0 ? num_heads / num_kv_heads : 1;
+  int64_t k = 1;
+  while (k < g && (g / k > 8 || g % k != 0)) ++k;
+  return (int)k;
+}
+
 // Merge groups per unit of the fast path's two-level merge (0: one level):
 // used when a unit has more than one group of partitions and the counter
 // region holds a counter per unit and per group.
@@ -1357,6 +1387,7 @@ extern "C" int64_t npd_paged_attention_workspace_size(int64_t num_seqs, int64_t 
   if (num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
       max_blocks_per_seq <= 0)
     return 0;
+  num_kv_heads *= kv_split_of(num_heads, num_kv_heads);   // kv heads of the work units
   const int64_t max_ctx = block_size * max_blocks_per_seq;
   if (!use_fast_path(head_dim, block_size, num_seqs)) {
     const int ps =
@@ -1410,13 +1441,15 @@ int attention_impl(void* out, const void* query, const void* key_cache, const vo
   if (num_heads % num_kv_heads != 0)
     return fail(NPD_E_INVALID, "%s: num_heads %lld is not a multiple of num_kv_heads %lld", name,
                 (long long)num_heads, (long long)num_kv_heads);
+  // the work units' kv heads and group size (groups above 8 heads are split)
+  const int split = kv_split_of(num_heads, num_kv_heads);
+  const int64_t pool_kv_heads = num_kv_heads;
+  num_kv_heads *= split;
   const int64_t g = num_heads / num_kv_heads;
-  if (g > 8)
-    return fail(NPD_E_INVALID, "%s: query heads per kv head %lld > 8 is not supported", name,
-                (long long)g);
   if (head_dim != 64 && head_dim != 128 && head_dim != 256)
     return fail(NPD_E_INVALID, "%s: head_dim %lld not in {64, 128, 256}", name, (long long)head_dim);
-  if (num_blocks * block_size * num_kv_heads > INT32_MAX || max_blocks_per_seq * block_size > INT32_MAX)
+  if (num_blocks * block_size * pool_kv_heads > INT32_MAX ||
+      max_blocks_per_seq * block_size > INT32_MAX)
     return fail(NPD_E_INVALID, "%s: pool exceeds int32 row indexing", name);
   if (num_seqs * num_kv_heads > 0x7fffffff)
     return fail(NPD_E_INVALID, "%s: too many (seq, kv-head) units", name);
@@ -1453,7 +1486,7 @@ int attention_impl(void* out, const void* query, const void* key_cache, const vo
   // partial slots per unit: for the shortest partition the kernel may take
   const int64_t max_parts = (max_ctx + min_partition - 1) / min_partition;
   if (max_parts > 65535) return fail(NPD_E_INVALID, "%s: context too long", name);
-  const int64_t need = npd_paged_attention_workspace_size(num_seqs, num_heads, num_kv_heads,
+  const int64_t need = npd_paged_attention_workspace_size(num_seqs, num_heads, pool_kv_heads,
                                                           head_dim, block_size, max_blocks_per_seq);
   if (need > 0) {
     if (!workspace || workspace_bytes < need)
@@ -1486,6 +1519,8 @@ int attention_impl(void* out, const void* query, const void* key_cache, const vo
   a.max_groups = (int)merge_groups(fast_ws, units, max_parts);
   a.part_ml = wsb ? a.part_acc + units * (max_parts + a.max_groups) * g * head_dim : nullptr;
   a.num_kv_heads = (int)num_kv_heads;
+  a.kv_split = split;
+  a.pool_kv_heads = (int)pool_kv_heads;
   a.num_seqs = (int)num_seqs;
   a.block_size = (int)block_size;
   a.num_blocks = (int)num_blocks;

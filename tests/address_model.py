@@ -191,6 +191,16 @@ def fast_min_partition(ps: int, bs: int, fp8: bool) -> int:
     return min(lo, ps)
 
 
+def kv_split_of(H: int, KV: int) -> int:
+    """decode_attention.hip kv_split_of: groups of more than 8 query heads are
+    served as the smallest number of equal groups of at most 8."""
+    g = H // KV
+    k = 1
+    while k < g and (g // k > 8 or g % k):
+        k += 1
+    return k
+
+
 def merge_groups(units: int, parts: int) -> int:
     """decode_attention.hip:1346-1349 (fast path)."""
     ng = _ceil(parts, MERGE_GROUP)
@@ -201,10 +211,11 @@ def merge_groups(units: int, parts: int) -> int:
 class DecodeLaunch:
     S: int
     H: int
-    KV: int
+    KV: int                 # kv heads of the work units (pool kv heads * kv_split)
     bs: int
     max_bps: int
     fp8: bool
+    kv_split: int = 1
     partition: int = 0
     min_partition: int = 0
     max_parts: int = 0
@@ -227,7 +238,9 @@ class DecodeLaunch:
 def decode_host(S, H, KV, bs, max_bps, fp8, D=128) -> DecodeLaunch:
     """The host choices of attention_impl (decode_attention.hip:1441-1511)."""
     assert use_fast_path(D, bs, S), "model covers the D = 128 fast path"
-    L = DecodeLaunch(S, H, KV, bs, max_bps, fp8)
+    split = kv_split_of(H, KV)
+    KV *= split
+    L = DecodeLaunch(S, H, KV, bs, max_bps, fp8, split)
     max_ctx = bs * max_bps
     L.partition = choose_partition(S, H, KV, D, bs, max_ctx, fp8)
     L.min_partition = fast_min_partition(L.partition, bs, fp8)
@@ -241,6 +254,8 @@ def decode_host(S, H, KV, bs, max_bps, fp8, D=128) -> DecodeLaunch:
     if L.min_partition < L.partition:
         h = min(units * L.max_parts, 2 * FAST_MIN_ITEMS_ACTUAL)
         n = max(n, h)
+    if split > 1 and S <= INLINE_SCHED_MAX:
+        n = _ceil(n, 8 * split) * 8 * split
     L.grid = n
     gp = pow2ceil(G)
     t = L.partition + 16 * RING
@@ -295,6 +310,12 @@ def decode_items(L: DecodeLaunch, seq_lens: np.ndarray):
                       dtype=np.int64)
     nfull = int(before[maxfull]) if S else 0
     ids = np.arange(L.grid, dtype=np.int64)
+    if L.kv_split > 1:
+        # blockIdx -> item id: the units of one pool kv head 8 blockIdx apart
+        span = 8 * L.kv_split
+        q, rem = ids // span, ids % span
+        ids = q * span + (rem & 7) * L.kv_split + (rem >> 3)
+        assert np.array_equal(np.sort(ids), np.arange(L.grid)), "not a permutation"
     unit = np.full(ids.shape, -2, dtype=np.int64)   # -2: exits
     part = np.zeros(ids.shape, dtype=np.int64)
     # A: full partitions, level by level

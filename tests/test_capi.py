@@ -69,10 +69,13 @@ def test_c_validation_paths_need_no_gpu():
     rc = _rc("npd_paged_attention", fake, fake, fake, fake, fake, fake, 2, 12, 5, 128, 64, 16, 4,
              ctypes.c_float(0.1), 1536, 128, 1536, 128, None, 0, 1, None)
     assert rc == -1 and b"multiple" in lib.npd_last_error()
-    # group > 8
+    # a group of 16 q-heads per kv head is accepted (served as two groups of
+    # 8): validation gets as far as the missing workspace, sized for 4 units
+    need = lib.npd_paged_attention_workspace_size(2, 32, 2, 128, 16, 4)
+    assert need == lib.npd_paged_attention_workspace_size(2, 32, 4, 128, 16, 4)
     rc = _rc("npd_paged_attention", fake, fake, fake, fake, fake, fake, 2, 32, 2, 128, 64, 16, 4,
              ctypes.c_float(0.1), 4096, 128, 4096, 128, None, 0, 1, None)
-    assert rc == -1
+    assert rc == -4 and b"workspace" in lib.npd_last_error()
     # workspace required for a long context and missing
     rc = _rc("npd_paged_attention", fake, fake, fake, fake, fake, fake, 2, 32, 8, 128, 4096, 16,
              256, ctypes.c_float(0.1), 4096, 128, 4096, 128, None, 0, 1, None)

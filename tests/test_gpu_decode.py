@@ -101,6 +101,37 @@ def test_group_sizes_and_head_dims(device, dtype, D, G):
     check(run(*args, 16), q, kc, vc, bt, sl, scale)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("G,kvh", [(12, 2), (16, 4), (16, 1), (9, 1), (11, 1)])
+def test_group_sizes_above_8(device, dtype, G, kvh):
+    """More than 8 query heads per kv head (e.g. 64 q / 4 kv heads): the kv
+    head of q-head h is still h // G (PA/csrc/attention/
+    paged_attention_kernel.cu:62); the op serves the group as equal
+    sub-groups of at most 8 heads. Contexts up to 32k tokens (two-level
+    merges), an empty sequence and a one-token one."""
+    lens = [1, 17, 300, 4097, 32768, 0]
+    args = make_inputs(len(lens), G * kvh, kvh, 128, lens, 16, dtype, device, seed=G * 10 + kvh)
+    q, kc, vc, bt, sl, scale, mb = args
+    check(run(*args, 16), q, kc, vc, bt, sl, scale)
+
+
+@pytest.mark.parametrize("D,bs", [(64, 16), (256, 8), (128, 8)])
+def test_group_of_16_generic_path(device, D, bs):
+    """G = 16 on the generic kernel (head dims 64 / 256, block size 8)."""
+    args = make_inputs(3, 32, 2, D, [1, 700, 3000], bs, torch.bfloat16, device, seed=D + bs)
+    q, kc, vc, bt, sl, scale, mb = args
+    check(run(*args, bs), q, kc, vc, bt, sl, scale)
+
+
+def test_group_of_16_scheduled_path(device):
+    """G = 16 with more than 64 sequences (the schedule kernel's work list)."""
+    g = torch.Generator().manual_seed(16)
+    lens = torch.randint(0, 6000, (70,), generator=g).tolist()
+    args = make_inputs(70, 32, 2, 128, lens, 16, torch.bfloat16, device, seed=160)
+    q, kc, vc, bt, sl, scale, mb = args
+    check(run(*args, 16), q, kc, vc, bt, sl, scale)
+
+
 @pytest.mark.parametrize("lens", [[1024], [1025], [2048], [2049], [100, 1025, 3000, 5000, 17]])
 def test_two_level_merge_group_boundaries(device, lens):
     """A (sequence, kv-head) with more than 16 partitions merges in two

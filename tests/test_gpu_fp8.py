@@ -89,7 +89,7 @@ def _run_and_check(device, q, kc, vc, bt, sl, ks, vs, mb, bs, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("G", [1, 2, 4, 6, 8])
+@pytest.mark.parametrize("G", [1, 2, 4, 6, 8, 12, 16])
 def test_decode_group_sizes(device, dtype, G):
     kvh = 2
     args = _fp8_case(device, [1, 17, 300, 777, 0], G * kvh, kvh, 16, dtype, seed=G)
@@ -100,6 +100,12 @@ def test_decode_group_sizes(device, dtype, G):
 def test_decode_block_sizes_and_long_context(device, bs):
     args = _fp8_case(device, [4097, 64, 2500], 32, 8, bs, torch.bfloat16, seed=bs)
     _run_and_check(device, *args, bs, torch.bfloat16)
+
+
+def test_decode_group_of_16_long_context(device):
+    """16 query heads per kv head over an FP8 pool, up to 32k tokens."""
+    args = _fp8_case(device, [32768, 1, 4097, 0], 64, 4, 16, torch.bfloat16, seed=16)
+    _run_and_check(device, *args, 16, torch.bfloat16)
 
 
 def test_decode_long_context_merge_groups(device):
