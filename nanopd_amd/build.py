@@ -29,7 +29,10 @@ COMMON_FLAGS = [
 ]
 # Per-file additions. prefill_attention: attention scores are finite or -inf
 # (masked keys), so the row maxima need no NaN quieting (v_max_f32 x, x, x
-# before every max).
+# before every max); and MFMA accumulators in VGPRs: prefill_dma_kernel's 64-row
+# waves hold 128 O accumulators plus Q, S and P, and with O in the
+# accumulation registers the rare rescale branch made the allocator spill to
+# scratch; in VGPR form the few values over 256 go to accumulation registers.
 FILE_FLAGS = {
     "prefill_attention.hip": ["-fno-honor-nans"],
 }

@@ -150,26 +150,17 @@ __device__ __forceinline__ u32x2 lds_read_tr(const uint16_t* p) {
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p)));
 }
 
-// kOff32: every K/V element of the pool lies within 4 GiB of the cache base,
-// so gather offsets are 32-bit. kF8: the pool holds OCP e4m3 bytes; a K/V
-// chunk is 8 bytes, converted exactly to four TT pairs when copied into LDS,
-// and the per-kv-head scales go into the score scale and the output.
-template <class TT, int HW, bool kOff32, bool kF8>
-__global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
-  constexpr int RT = kPairs / HW;                      // row tiles of 64 per workgroup
-  constexpr int TR = 64 * RT;                          // query rows per workgroup
-  constexpr int MB = kWaveRows / 16;                   // 16-row query blocks per wave
-  __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kKT * kRow];
-  __shared__ __attribute__((aligned(16))) uint16_t s_v[3][kKT * kRow];
-  __shared__ int s_blk[kMaxBlocksLds];
-  __shared__ int s_ticket;
-
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int g = lane >> 4, r = lane & 15;
-
+// The work item of this workgroup (every wave derives the same one): the
+// sequence s, its query tile t of TR rows, key split j of split length ks
+// steps, kv head kh and head group hg, and the sequence's first query row,
+// chunk length and context. false: no item, the workgroup exits.
+struct Item {
+  int s, t, j, kh, hg, ks, q0, qlen, ctx;
+};
+template <int TR>
+__device__ __forceinline__ bool prefill_item(const PrefillArgs& a, int lane, Item& it) {
   int s, t, j, kh, hg, ks = a.ks_steps;
-  int q0, qlen, ctx;   // the sequence's first query row, chunk length, context
+  int q0, qlen, ctx;
   const int cap = a.max_bps * a.block_size;
   if (a.num_seqs * a.tiles_max <= 64) {
     // Work list in longest-processing-time order, derived by every wave from
@@ -235,7 +226,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
       // items in buckets >= b, non-increasing in b; item id is in the last
       // bucket b with from(b) > id (binary search over ballot counts)
       auto from = [&](int b) -> int { return __popcll(__ballot(last >= b)) * per_item; };
-      if (id >= from(0)) return;   // past the last item
+      if (id >= from(0)) return false;   // past the last item
       int lo = 0, hi = ks;
       while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
@@ -264,7 +255,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     const int gunits = a.tiles_max * a.hgroups;
     const int xcd = blockIdx.x & 7, p = blockIdx.x >> 3;
     const int gi = (p / gunits) * 8 + xcd;
-    if (gi >= a.num_groups) return;
+    if (gi >= a.num_groups) return false;
     const int u = p - (p / gunits) * gunits;
     t = a.tiles_max - 1 - u / a.hgroups;
     hg = u - (u / a.hgroups) * a.hgroups;
@@ -274,10 +265,37 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     j = js / a.num_seqs;
     q0 = a.cu_seqlens_q[s];
     qlen = a.cu_seqlens_q[s + 1] - q0;
-    if (t * TR >= qlen) return;
+    if (t * TR >= qlen) return false;
     ctx = a.context_lens[s];
     ctx = ctx < 0 ? 0 : (ctx < cap ? ctx : cap);
   }
+
+  it = Item{s, t, j, kh, hg, ks, q0, qlen, ctx};
+  return true;
+}
+
+// kOff32: every K/V element of the pool lies within 4 GiB of the cache base,
+// so gather offsets are 32-bit. kF8: the pool holds OCP e4m3 bytes; a K/V
+// chunk is 8 bytes, converted exactly to four TT pairs when copied into LDS,
+// and the per-kv-head scales go into the score scale and the output.
+template <class TT, int HW, bool kOff32, bool kF8>
+__global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
+  constexpr int RT = kPairs / HW;                      // row tiles of 64 per workgroup
+  constexpr int TR = 64 * RT;                          // query rows per workgroup
+  constexpr int MB = kWaveRows / 16;                   // 16-row query blocks per wave
+  __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kKT * kRow];
+  __shared__ __attribute__((aligned(16))) uint16_t s_v[3][kKT * kRow];
+  __shared__ int s_blk[kMaxBlocksLds];
+  __shared__ int s_ticket;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int g = lane >> 4, r = lane & 15;
+
+  Item it;
+  if (!prefill_item<TR>(a, lane, it)) return;
+  const int s = it.s, t = it.t, j = it.j, kh = it.kh, hg = it.hg, ks = it.ks;
+  const int q0 = it.q0, qlen = it.qlen, ctx = it.ctx;
 
   const int prefix = ctx - qlen;                       // position of query row 0
   const int rows = (qlen - t * TR) < TR ? (qlen - t * TR) : TR;
