@@ -236,6 +236,35 @@ class PagedQwen3:
         xs = F.rms_norm(x, (E,), self.final_norm, cfg.rms_eps)
         return (xs @ self.lm_head.t()).float()
 
+    @torch.no_grad()
+    def load_hf_state_dict(self, sd: dict) -> None:
+        """Takes the weights of a Hugging Face Qwen3ForCausalLM state dict (the
+        model the reference's ModelRunner wraps, nanoPD/engine/model_runner.py:
+        8-13): q/k/v projections fused into one [(H + 2 KV) * D, E] matrix,
+        gate/up into one [2 I, E], the rest as they are. An untied LM head
+        (lm_head.weight) is used when present, else the embedding."""
+        def get(name):
+            t = sd[name]
+            return t.to(device=self.device, dtype=self.dtype)
+
+        self.embed.copy_(get("model.embed_tokens.weight"))
+        for i, w in enumerate(self.layers):
+            p = f"model.layers.{i}."
+            w["in_norm"].copy_(get(p + "input_layernorm.weight"))
+            w["qkv"].copy_(torch.cat([get(p + "self_attn.q_proj.weight"),
+                                      get(p + "self_attn.k_proj.weight"),
+                                      get(p + "self_attn.v_proj.weight")], dim=0))
+            w["q_norm"].copy_(get(p + "self_attn.q_norm.weight"))
+            w["k_norm"].copy_(get(p + "self_attn.k_norm.weight"))
+            w["o"].copy_(get(p + "self_attn.o_proj.weight"))
+            w["post_norm"].copy_(get(p + "post_attention_layernorm.weight"))
+            w["gate_up"].copy_(torch.cat([get(p + "mlp.gate_proj.weight"),
+                                          get(p + "mlp.up_proj.weight")], dim=0))
+            w["down"].copy_(get(p + "mlp.down_proj.weight"))
+        self.final_norm.copy_(get("model.norm.weight"))
+        self.lm_head.copy_(get("lm_head.weight" if "lm_head.weight" in sd
+                               else "model.embed_tokens.weight"))
+
     def copy_blocks(self, pairs) -> None:
         """Copy-on-write copies (old, new) in every layer's cache."""
         if not pairs:
