@@ -350,7 +350,7 @@ def bench_e2e(args, dev) -> int:
         t_graphs = time.perf_counter() - t0
     eng = Engine(model, max_batch_size=16, budget=1024, chunk=512, graphs=graphs)
     reqs = make_requests(args.requests, seed=5)
-    res = serve(eng, reqs)
+    res = serve(eng, reqs, progress_every=32)
     print(json.dumps({
         "metric": "Collocated continuous-batching output tok/s, Qwen3-8B (random init)",
         "value": round(res["tok_per_s"], 1),

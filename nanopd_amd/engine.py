@@ -25,6 +25,7 @@ from __future__ import annotations
 
 import math
 import random
+import sys
 import time
 from dataclasses import dataclass, field
 from typing import Optional
@@ -260,16 +261,20 @@ def make_requests(n: int, seed: int = 5, rate: float = 8.0, prompt_median: int =
     return reqs
 
 
-def serve(engine: Engine, requests: list, time_scale: float = 1.0) -> dict:
+def serve(engine: Engine, requests: list, time_scale: float = 1.0,
+          progress_every: int = 0) -> dict:
     """Runs requests arriving at their `arrival` times (wall clock, scaled by
     time_scale) through the engine until all finish. Reports output tokens per
     second over (last finish - first arrival), and the reference's formula
-    (output tokens / arrival window, benchmark_poisson.py:93-99)."""
+    (output tokens / arrival window, benchmark_poisson.py:93-99).
+    progress_every > 0: a line on stderr each time that many more requests
+    have finished."""
     pending = sorted(requests, key=lambda r: r.arrival)
     seqs = []
     t0 = time.perf_counter()
     engine.clock = lambda: time.perf_counter() - t0
     i = 0
+    reported = 0
     while i < len(pending) or engine.sched.has_work():
         now = time.perf_counter() - t0
         while i < len(pending) and pending[i].arrival * time_scale <= now:
@@ -279,6 +284,12 @@ def serve(engine: Engine, requests: list, time_scale: float = 1.0) -> dict:
             time.sleep(max(0.0, pending[i].arrival * time_scale - now))
             continue
         engine.step(now)
+        if progress_every > 0:
+            done = sum(1 for s in seqs if s.finished >= 0)
+            if done >= reported + progress_every:
+                reported = done - done % progress_every
+                print(f"serve: {done}/{len(pending)} requests finished, {engine.steps} steps, "
+                      f"{now:.1f} s", file=sys.stderr, flush=True)
     torch.cuda.synchronize()
     t_end = time.perf_counter() - t0
     for s in seqs:
