@@ -70,13 +70,16 @@ def _settle(step, seconds: float = 0.3) -> None:
 
 def _launch_avg_ms(fn, iters: int = 50) -> float:
     """Average duration (ms) of one launch of fn, HIP events around `iters`
-    back-to-back launches on the current stream. A spin kernel queued first
-    keeps the GPU behind the host, so host-side call overhead does not show;
+    back-to-back launches on the current stream. A spin kernel queued first,
+    sized to outlast the host's enqueueing of all `iters` calls, keeps the GPU
+    behind the host, so host-side call overhead does not show;
     what remains between launches is the dispatch gap of dependent kernels.
     A per-call event pair adds one more such gap per call, which is why the
     in-step figures read a few microseconds longer."""
     torch.cuda.synchronize()
-    torch.cuda._sleep(2_000_000)
+    # about 0.4 ms + 40 us per launch at 2.4 GHz: longer than the host takes
+    # to enqueue the launches (up to ~20 us per call through the Python layer)
+    torch.cuda._sleep(1_000_000 + 100_000 * iters)
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
     a.record()
@@ -163,8 +166,11 @@ def bench_decode(args, w) -> dict:
     flush_buf = torch.ones(1 << 28, dtype=torch.int32, device=dev)
     cold = statistics.mean(_events_ms(attend, 10, pre=lambda: flush_buf.max()))
     del flush_buf
-    step_bytes = w.attention_bytes() + w.store_bytes()
-    achieved = w.attention_bytes() / (attn_avg * 1e-3) / 1e9
+    # the roofline counts the bytes the call must move from HBM at least: a
+    # block shared by two tables (config 4's copy-on-write forks) counts once
+    uniq = w.attention_unique_bytes()
+    step_bytes = uniq + w.store_bytes()
+    achieved = uniq / (attn_avg * 1e-3) / 1e9
     return {
         "ms_per_step": ms_step,
         "value": step_bytes / (ms_step * 1e-3) / 1e9,
@@ -176,10 +182,11 @@ def bench_decode(args, w) -> dict:
             "attention_us_in_step_mean": round(statistics.mean(attn_ms) * 1e3, 2),
             "attention_us_in_step_median": round(statistics.median(attn_ms) * 1e3, 2),
             "attention_us_cold_l2_flushed": round(cold * 1e3, 2),
-            "attention_gbs_cold": round(w.attention_bytes() / (cold * 1e-3) / 1e9, 1),
+            "attention_gbs_cold": round(uniq / (cold * 1e-3) / 1e9, 1),
             "store_us_mean": round(store_ms * 1e3, 2),
             "store_gbs": round(w.store_bytes() / (store_ms * 1e-3) / 1e9, 1),
-            "attention_bytes": w.attention_bytes(),
+            "attention_bytes": uniq,
+            "attention_bytes_per_sequence_sum": w.attention_bytes(),
             "store_bytes": w.store_bytes(),
             "kv_tokens": sum(w.seq_lens_list),
             "kernels": "decode_d128_kernel (partitions + fused log-sum-exp merge)",
@@ -524,6 +531,78 @@ def bench_transfer(args, dev) -> int:
     return 0
 
 
+def cpu_baseline_store(w, reps: int = 5) -> dict:
+    """The reference's Python scatter loop (restated in oracle/torch_ref.py
+    from nanoPD/docs/en/03-cuda_kernels_en.md:69-78) on host cores, over the
+    whole workload: per token, K and V of every kv head into the pool at its
+    slot (a one-entry table per token: block = slot // bs, position = slot %
+    bs)."""
+    from oracle.torch_ref import ref_kv_store_loop
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    kc, vc = w.k_cache.cpu(), w.v_cache.cpu()
+    ks, vs = w.new_k.cpu().transpose(0, 1), w.new_v.cpu().transpose(0, 1)   # [kvh, T, D]
+    sl = w.slot_mapping.cpu().long()
+    tables, pos = (sl // w.block_size)[:, None], sl % w.block_size
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        ref_kv_store_loop(kc, vc, ks, vs, tables, pos)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": round(w.store_bytes() / med / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"ref_kv_store_loop (torch CPU, per-token slice assignment) over all "
+                      f"{w.new_k.size(0)} tokens of the step, median of {reps} runs = "
+                      f"{med * 1e3:.1f} ms; CPU: {_cpu_model()}"}
+
+
+def bench_store(args, w) -> int:
+    """The KV store of configuration 3's mixed step: every new token's K and V
+    (2096 tokens x 8 kv heads x 128, bf16) scattered into the pool at its slot
+    (npd_paged_kv_store_slots, kv_store_kernel). One step = one store.
+    Roofline: HBM, the K/V rows read once and written once plus the slots."""
+    from nanopd_amd import paged_kernels as pk
+
+    def store():
+        pk.paged_kv_store_slots(w.k_cache, w.v_cache, w.new_k, w.new_v, w.slot_mapping)
+
+    _settle(store)
+    for _ in range(args.warmup):
+        store()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        store()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    launch_ms = _launch_avg_ms(store, max(args.steps, 50))
+    call_ms = statistics.mean(_events_ms(store, args.steps))
+    byt = w.store_bytes()
+    gbs = byt / (launch_ms * 1e-3) / 1e9
+    line = {
+        "metric": "Paged KV store achieved HBM GB/s (% peak)",
+        "value": round(byt / (ms * 1e-3) / 1e9, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)*0.5 values, shuffled block tables)",
+        "config": {"workload": w.name + "_store", "tokens": int(w.new_k.size(0)),
+                   "num_kv_heads": w.num_kv_heads, "head_dim": w.head_dim,
+                   "block_size": w.block_size,
+                   "step": "paged_kv_store_slots of every new token of the mixed step"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": _profiled_traffic(f"kv_store_kernel/{w.name}")},
+        "detail": {"store_us_launch_avg": round(launch_ms * 1e3, 3),
+                   "store_us_per_call_events": round(call_ms * 1e3, 3),
+                   "store_bytes": byt, "kernels": "kv_store_kernel<16, slots>"},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline_store(w)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def emit_prefill(args, w) -> int:
     from nanopd_amd import paged_kernels as pk
     pk.paged_kv_store_slots(w.k_cache, w.v_cache, w.new_k, w.new_v, w.slot_mapping)
@@ -561,11 +640,12 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=["decode", "decode-fp8", "long", "prefill", "copy", "e2e",
-                                           "transfer"],
+    ap.add_argument("--workload", choices=["decode", "decode-fp8", "long", "prefill", "store",
+                                           "copy", "e2e", "transfer"],
                     default="decode",
                     help="decode: config 2 (default); long: config 4 (8 seqs, 8k-32k); "
                          "prefill: config 3 (4 chunks of 512 on paged prefixes + 48 decodes); "
+                         "store: config 3's KV store (2096 tokens into the pool by slot); "
                          "e2e: config 5 (Qwen3-8B collocated serving, tok/s); "
                          "decode-fp8: config 2 over an FP8 (e4m3) pool; "
                          "transfer: KV transfer pack + unpack of a 4096-token Qwen3-8B sequence; "
@@ -599,6 +679,8 @@ def main() -> int:
         return bench_decode_fp8(args, workloads.config2(dev))
     if args.workload == "prefill":
         return emit_prefill(args, workloads.config3(dev))
+    if args.workload == "store":
+        return bench_store(args, workloads.config3(dev))
     if args.workload == "decode":
         w = workloads.config2(dev)
     else:

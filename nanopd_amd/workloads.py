@@ -58,13 +58,38 @@ class DecodeWorkload:
         elt = torch.finfo(self.dtype).bits // 8
         return sum(self.seq_lens_list) * self.num_kv_heads * self.head_dim * 2 * elt
 
-    def attention_bytes(self) -> int:
-        """Algorithmic HBM bytes of one decode-attention call: KV rows + Q + O
-        + block-table rows + seq_lens."""
+    def unique_kv_bytes(self) -> int:
+        """KV bytes of the distinct pool rows the call reads: a block shared by
+        several tables (a copy-on-write fork's prefix) counts once, with the
+        most tokens any sequence uses from it."""
+        elt = torch.finfo(self.dtype).bits // 8
+        used: dict = {}
+        tables = self.block_tables.cpu().numpy()
+        for s, n in enumerate(self.seq_lens_list):
+            nb = (n + self.block_size - 1) // self.block_size
+            for j in range(nb):
+                b = int(tables[s, j])
+                used[b] = max(used.get(b, 0), min(self.block_size, n - j * self.block_size))
+        return sum(used.values()) * self.num_kv_heads * self.head_dim * 2 * elt
+
+    def _qo_meta_bytes(self) -> int:
         elt = torch.finfo(self.dtype).bits // 8
         qo = 2 * self.num_seqs * self.num_heads * self.head_dim * elt
         meta = self.num_seqs * self.max_blocks_per_seq * 4 + self.num_seqs * 4
-        return self.kv_bytes() + qo + meta
+        return qo + meta
+
+    def attention_bytes(self) -> int:
+        """Algorithmic bytes of one decode-attention call, per sequence: its KV
+        rows + Q + O + block-table row + seq_len (a shared block counts once
+        per sequence that reads it)."""
+        return self.kv_bytes() + self._qo_meta_bytes()
+
+    def attention_unique_bytes(self) -> int:
+        """Bytes one decode-attention call must move from HBM at least: the
+        distinct KV rows (unique_kv_bytes) + Q + O + tables + seq_lens. The
+        roofline counts these; they equal attention_bytes when no block is
+        shared."""
+        return self.unique_kv_bytes() + self._qo_meta_bytes()
 
     def store_bytes(self) -> int:
         """Algorithmic bytes of the store: K/V rows read + written, plus the
@@ -229,6 +254,13 @@ class MixedWorkload:
         for c, p in zip(self.chunk_lens[: self.num_prefill_seqs], self.ctx_before):
             tot += c * p + c * (c + 1) // 2
         return 4 * self.num_heads * self.head_dim * tot
+
+    def store_bytes(self) -> int:
+        """Algorithmic bytes of the step's slot store: every new token's K/V
+        rows read + written, plus its int32 slot."""
+        elt = torch.finfo(self.dtype).bits // 8
+        t = self.new_k.size(0)
+        return 4 * t * self.num_kv_heads * self.head_dim * elt + 4 * t
 
 
 def config3(device="cpu", seed: int = 3, chunk: int = 512, prefixes=(0, 512, 1536, 3072),
