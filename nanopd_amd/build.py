@@ -3,6 +3,11 @@
 hipcc compiles every source under nanopd_amd/csrc/ to an object in
 nanopd_amd/_build/ (in parallel) and links them into nanopd_amd/lib/. Run as
 ``python -m nanopd_amd.build`` or call :func:`build`.
+
+:func:`build_asan` builds the same sources with AddressSanitizer on the host
+pass into libnanopd_hip_asan.so, for the CPU tests of the C-ABI's
+argument validation (tests/test_asan_capi.py), under _build/asan/. The
+product path never loads it.
 """
 from __future__ import annotations
 
@@ -29,10 +34,7 @@ COMMON_FLAGS = [
 ]
 # Per-file additions. prefill_attention: attention scores are finite or -inf
 # (masked keys), so the row maxima need no NaN quieting (v_max_f32 x, x, x
-# before every max); and MFMA accumulators in VGPRs: prefill_dma_kernel's 64-row
-# waves hold 128 O accumulators plus Q, S and P, and with O in the
-# accumulation registers the rare rescale branch made the allocator spill to
-# scratch; in VGPR form the few values over 256 go to accumulation registers.
+# before every max).
 FILE_FLAGS = {
     "prefill_attention.hip": ["-fno-honor-nans"],
 }
@@ -88,6 +90,64 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     return LIB_PATH
 
 
+ASAN_DIR = BUILD_DIR / "asan"
+ASAN_LIB_PATH = ASAN_DIR / "libnanopd_hip_asan.so"   # a test artefact: stays out of lib/
+# The sanitizer applies to the host pass only; the device code is compiled
+# (the host objects register it) but never launched from this library.
+ASAN_FLAGS = ["-std=c++17", "-fPIC", "-O1", "-gline-tables-only", "-fno-omit-frame-pointer",
+              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+              "-Xarch_host", "-fsanitize=address"]
+
+
+def build_asan(verbose: bool = False) -> Path:
+    """AddressSanitizer build (host pass) of every C-ABI source; always rebuilds.
+    The library leaves the sanitizer runtime to the process that loads it
+    (asan_runtime() names the one matching hipcc's compiler)."""
+    hipcc = _hipcc()
+    ASAN_DIR.mkdir(parents=True, exist_ok=True)
+    LIB_DIR.mkdir(exist_ok=True)
+
+    def one(src: Path) -> Path:
+        obj = ASAN_DIR / (src.stem + ".o")
+        cmd = [hipcc, f"--offload-arch={ARCH}", *ASAN_FLAGS, *FILE_FLAGS.get(src.name, []),
+               "-c", str(src), "-o", str(obj)]
+        if src.suffix == ".cpp":
+            cmd[1:1] = ["-x", "hip"]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc (asan) failed on {src.name}:\n{res.stdout}{res.stderr}")
+        return obj
+
+    srcs = sources()
+    with cf.ThreadPoolExecutor(max_workers=min(len(srcs), os.cpu_count() or 4)) as ex:
+        objs = list(ex.map(one, srcs))
+    tmp = ASAN_LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Xarch_host", "-fsanitize=address",
+           "-o", str(tmp), *map(str, objs)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link (asan) failed:\n{res.stdout}{res.stderr}")
+    os.replace(tmp, ASAN_LIB_PATH)
+    return ASAN_LIB_PATH
+
+
+def asan_runtime() -> Path | None:
+    """The AddressSanitizer runtime of hipcc's clang, or None."""
+    clang = Path(_hipcc()).resolve().parent.parent / "lib" / "llvm" / "bin" / "clang++"
+    for cand in (clang, Path("/opt/rocm/llvm/bin/clang++")):
+        if cand.exists():
+            res = subprocess.run([str(cand), "-print-file-name=libclang_rt.asan-x86_64.so"],
+                                 capture_output=True, text=True)
+            p = Path(res.stdout.strip())
+            if res.returncode == 0 and p.is_absolute() and p.exists():
+                return p
+    return None
+
+
 if __name__ == "__main__":
     p = build(verbose="-v" in sys.argv)
     print(p)
+    if "--asan" in sys.argv:
+        print(build_asan(verbose="-v" in sys.argv))
