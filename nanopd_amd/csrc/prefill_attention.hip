@@ -678,6 +678,184 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   }
 }
 
+// Head dims other than 128 (64 and 256). One workgroup of 4 waves per
+// (sequence, query head, 64-row query tile); wave w owns query rows
+// 16w .. 16w + 15 of the tile. Per step of 64 keys the workgroup copies the kv
+// head's K and V rows into LDS (keys past the visible range clamped to the
+// last visible key, as in prefill_kernel), then every wave computes
+//   S^T = K . Q^T     (v_mfma_f32_16x16x32, D/32 chunks of the head dim x
+//                      4 blocks of 16 keys; Q rows held in registers),
+//   a causal mask and an online softmax in fp32 (log2 units; O and the row
+//   sum rescaled whenever a row's running max grows),
+//   O^T += V^T . P^T  (D/16 blocks of 16 dims x 2 chunks of 32 keys; V^T via
+//                      the transposing LDS read, P^T from the S^T layout).
+// The operand layouts, the P packing and the normalisation (the row sum adds
+// the rounded P values) are those of prefill_kernel. No key splits and no
+// GQA sharing of the K/V tile: these head dims are served correctly, not
+// tuned. Rows with no visible key are written as zeros.
+template <class TT, int D, bool kF8>
+__global__ __launch_bounds__(256) void prefill_generic_kernel(PrefillArgs a) {
+  constexpr int kGT = 256;                      // threads
+  constexpr int RW = D + (D == 64 ? 8 : 16);    // LDS row (elements); 16-byte multiple
+  constexpr int CPR = D / 8;                    // 8-element chunks per K/V row
+  constexpr int KPP = kGT / CPR;                // keys per load pass
+  constexpr int NPASS = kKT / KPP;
+  constexpr int NC = D / 32;                    // head-dim chunks of QK
+  constexpr int NB = D / 16;                    // 16-dim blocks of O
+  static_assert(kKT % KPP == 0 && RW % 8 == 0, "tile shape");
+  __shared__ __attribute__((aligned(16))) uint16_t s_k[kKT * RW];
+  __shared__ __attribute__((aligned(16))) uint16_t s_v[kKT * RW];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int g = lane >> 4, r = lane & 15;
+  const int H = a.num_kv_heads * a.group;
+  const int h = (int)(blockIdx.x % (unsigned)H);
+  const int st = (int)(blockIdx.x / (unsigned)H);
+  const int s = st / a.tiles_max, t = st - (st / a.tiles_max) * a.tiles_max;
+  if (s >= a.num_seqs) return;
+  const int q0 = a.cu_seqlens_q[s];
+  const int qlen = a.cu_seqlens_q[s + 1] - q0;
+  if (t * 64 >= qlen) return;
+  const int cap = a.max_bps * a.block_size;
+  int ctx = a.context_lens[s];
+  ctx = ctx < 0 ? 0 : (ctx < cap ? ctx : cap);
+  const int kh = h / a.group;
+  const int prefix = ctx - qlen;                 // position of query row 0
+  const int rows = (qlen - t * 64) < 64 ? (qlen - t * 64) : 64;
+  int nkeys = prefix + t * 64 + rows;            // keys 0 .. the tile's last position
+  nkeys = nkeys < 0 ? 0 : nkeys;
+  const int nsteps = (nkeys + kKT - 1) / kKT;
+  const int bs = a.block_size;
+  const int row = t * 64 + wave * 16 + r;        // this lane's query row (S^T column r)
+  const int pos = prefix + row;
+
+  u32x4 qb[NC];   // B operand: Q[row][c*32 + 8g .. +8]; rows past the chunk read its last row
+  {
+    const int rq = row < qlen ? row : qlen - 1;
+    const uint16_t* qp = a.q + (int64_t)(q0 + rq) * a.q_stride_token +
+                         (int64_t)h * a.q_stride_head + g * 8;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) qb[c] = *reinterpret_cast<const u32x4*>(qp + c * 32);
+  }
+  f32x4 oacc[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) oacc[nb] = f32x4{0, 0, 0, 0};
+  float m = -INFINITY, l = 0.f;
+  const float c2 = kF8 ? a.scale_log2 * a.k_scale[kh] : a.scale_log2;
+  const float oscale = kF8 ? a.v_scale[kh] : 1.f;
+
+  for (int step = 0; step < nsteps; ++step) {
+    __syncthreads();   // every wave is done with the previous tile
+#pragma unroll
+    for (int e = 0; e < NPASS; ++e) {
+      const int kk = tid / CPR + KPP * e;
+      const int col = tid - (tid / CPR) * CPR;
+      int tok = step * kKT + kk;
+      tok = tok < nkeys ? tok : nkeys - 1;
+      const int lb = a.bs_shift >= 0 ? tok >> a.bs_shift : tok / bs;
+      int blk = a.block_tables[(int64_t)s * a.max_bps + lb];
+      blk = blk < 0 ? 0 : (blk >= a.num_blocks ? a.num_blocks - 1 : blk);
+      const int64_t ri = ((int64_t)blk * a.num_kv_heads + kh) * bs + (tok - lb * bs);
+      u32x4 kw, vw;
+      if constexpr (kF8) {   // D-byte rows, 8-byte chunks
+        const char* kb = reinterpret_cast<const char*>(a.k_cache);
+        const char* vb = reinterpret_cast<const char*>(a.v_cache);
+        const u32x2 k8 = *reinterpret_cast<const u32x2*>(kb + ri * D + col * 8);
+        const u32x2 v8 = *reinterpret_cast<const u32x2*>(vb + ri * D + col * 8);
+        kw = u32x4{npd::e4m3x2_to<TT, false>(k8.x), npd::e4m3x2_to<TT, true>(k8.x),
+                   npd::e4m3x2_to<TT, false>(k8.y), npd::e4m3x2_to<TT, true>(k8.y)};
+        vw = u32x4{npd::e4m3x2_to<TT, false>(v8.x), npd::e4m3x2_to<TT, true>(v8.x),
+                   npd::e4m3x2_to<TT, false>(v8.y), npd::e4m3x2_to<TT, true>(v8.y)};
+      } else {
+        const int64_t idx = ri * CPR + col;   // 16-byte units
+        kw = a.k_cache[idx];
+        vw = a.v_cache[idx];
+      }
+      *reinterpret_cast<u32x4*>(&s_k[kk * RW + col * 8]) = kw;
+      *reinterpret_cast<u32x4*>(&s_v[kk * RW + col * 8]) = vw;
+    }
+    __syncthreads();
+
+    // S^T[key n*16 + 4g + i][query r]
+    f32x4 sacc[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) sacc[n] = f32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const u32x4 ka = *reinterpret_cast<const u32x4*>(&s_k[(n * 16 + r) * RW + c * 32 + g * 8]);
+        sacc[n] = Mfma<TT>::mma(ka, qb[c], sacc[n]);
+      }
+    const int key0 = step * kKT;
+    float v[16];
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = key0 + n * 16 + 4 * g + i;
+        v[n * 4 + i] = key <= pos ? sacc[n][i] : -INFINITY;
+      }
+    float mx = v[0];
+#pragma unroll
+    for (int e = 1; e < 16; ++e) mx = fmaxf(mx, v[e]);
+    mx = row_max4(mx);
+    const float mnew = fmaxf(m, mx * c2);
+    const float mref = mnew == -INFINITY ? 0.f : mnew;
+    const float alpha = __builtin_amdgcn_exp2f(m - mref);   // 0 from the initial -inf
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) oacc[nb] *= alpha;
+    l *= alpha;
+    m = mnew;
+    uint32_t packed[8];
+#pragma unroll
+    for (int e = 0; e < 16; e += 2) {
+      const float p0 = __builtin_amdgcn_exp2f(fmaf(v[e], c2, -mref));
+      const float p1 = __builtin_amdgcn_exp2f(fmaf(v[e + 1], c2, -mref));
+      const uint32_t u = TT::pack2(p0, p1);
+      l = TT::dot2(u, TT::kOne2, l);
+      packed[e / 2] = u;
+    }
+    // B operand of keys kc*32 .. +32: slots e < 4 -> key 4g + e, e >= 4 -> 16 + 4g + e - 4
+    const u32x4 pb[2] = {u32x4{packed[0], packed[1], packed[2], packed[3]},
+                         u32x4{packed[4], packed[5], packed[6], packed[7]}};
+    const uint16_t* vlane = s_v + (g * 4 + (r >> 2)) * RW + 4 * (r & 3);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        const u32x2 lo = lds_read_tr(vlane + (kc * 32) * RW + nb * 16);
+        const u32x2 hi = lds_read_tr(vlane + (kc * 32 + 16) * RW + nb * 16);
+        oacc[nb] = Mfma<TT>::mma(u32x4{lo.x, lo.y, hi.x, hi.y}, pb[kc], oacc[nb]);
+      }
+  }
+  l = row_sum4(l);
+  if (row >= qlen) return;
+  const float inv = (l > 0.f && pos >= 0) ? oscale / l : 0.f;
+  uint16_t* op = a.out + (int64_t)(q0 + row) * a.out_stride_token + (int64_t)h * a.out_stride_head;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const f32x4 o = oacc[nb];
+    u32x2 w;
+    w.x = TT::pack2(o[0] * inv, o[1] * inv);
+    w.y = TT::pack2(o[2] * inv, o[3] * inv);
+    *reinterpret_cast<u32x2*>(op + nb * 16 + g * 4) = w;
+  }
+}
+
+template <class TT, bool kF8>
+int launch_generic(int64_t head_dim, const PrefillArgs& a, int64_t grid, hipStream_t st,
+                   const char* name) {
+  if (head_dim == 64)
+    hipLaunchKernelGGL((prefill_generic_kernel<TT, 64, kF8>), dim3((unsigned)grid), dim3(256), 0,
+                       st, a);
+  else
+    hipLaunchKernelGGL((prefill_generic_kernel<TT, 256, kF8>), dim3((unsigned)grid), dim3(256), 0,
+                       st, a);
+  return npd::check_launch(name);
+}
+
 template <class TT, bool kOff32, bool kF8>
 int launch(int hw, const PrefillArgs& a, int64_t grid, hipStream_t st, const char* name) {
   switch (hw) {
@@ -734,7 +912,7 @@ extern "C" int64_t npd_paged_prefill_workspace_size(int64_t num_seqs, int64_t to
                                                     int64_t num_heads, int64_t head_dim,
                                                     int64_t max_q_len, int64_t max_context_len) {
   (void)total_q;
-  (void)head_dim;
+  if (head_dim != kD) return 0;   // the head dims of prefill_generic_kernel need no workspace
   return prefill_layout(num_seqs, num_heads, max_q_len, max_context_len).total;
 }
 
@@ -758,8 +936,8 @@ int prefill_impl(void* out, const void* query, const void* key_cache, const void
   if (num_seqs < 0 || total_q < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_blocks <= 0 ||
       block_size <= 0 || max_blocks_per_seq <= 0 || max_q_len < 0)
     return fail(NPD_E_INVALID, "%s: bad sizes", name);
-  if (head_dim != kD)
-    return fail(NPD_E_INVALID, "%s: head_dim %lld not supported (128 only)", name,
+  if (head_dim != 64 && head_dim != kD && head_dim != 256)
+    return fail(NPD_E_INVALID, "%s: head_dim %lld not in {64, 128, 256}", name,
                 (long long)head_dim);
   if (num_heads % num_kv_heads != 0)
     return fail(NPD_E_INVALID, "%s: num_heads %lld is not a multiple of num_kv_heads %lld", name,
@@ -768,7 +946,7 @@ int prefill_impl(void* out, const void* query, const void* key_cache, const void
   const int hw = (g % 4 == 0) ? 4 : (g % 2 == 0 ? 2 : 1);   // gcd(g, 4)
   if (num_blocks * block_size * num_kv_heads > INT32_MAX || max_blocks_per_seq * block_size > INT32_MAX)
     return fail(NPD_E_INVALID, "%s: pool exceeds int32 row indexing", name);
-  if (max_blocks_per_seq > kMaxBlocksLds)
+  if (head_dim == kD && max_blocks_per_seq > kMaxBlocksLds)
     return fail(NPD_E_INVALID, "%s: block tables wider than %d blocks are not supported", name,
                 kMaxBlocksLds);
   if (q_stride_token % 8 || q_stride_head % 8 || out_stride_token % 4 || out_stride_head % 4 ||
@@ -787,6 +965,40 @@ int prefill_impl(void* out, const void* query, const void* key_cache, const void
       (reinterpret_cast<uintptr_t>(out) & 7u) != 0)
     return fail(NPD_E_ALIGN, "%s: query pointer must be 16-byte aligned, caches %d-byte, out 8-byte",
                 name, fp8 ? 8 : 16);
+  if (head_dim != kD) {
+    const int64_t tiles = (max_q_len + 63) / 64;
+    const int64_t grid = num_seqs * tiles * num_heads;
+    if (grid > INT32_MAX) return fail(NPD_E_INVALID, "%s: too many tiles", name);
+    PrefillArgs a{};
+    a.out = static_cast<uint16_t*>(out);
+    a.q = static_cast<const uint16_t*>(query);
+    a.k_cache = static_cast<const u32x4*>(key_cache);
+    a.v_cache = static_cast<const u32x4*>(value_cache);
+    a.block_tables = block_tables;
+    a.cu_seqlens_q = cu_seqlens_q;
+    a.context_lens = context_lens;
+    a.k_scale = k_scale;
+    a.v_scale = v_scale;
+    a.num_seqs = (int)num_seqs;
+    a.num_kv_heads = (int)num_kv_heads;
+    a.group = (int)g;
+    a.block_size = (int)block_size;
+    a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctzll((unsigned long long)block_size) : -1;
+    a.num_blocks = (int)num_blocks;
+    a.max_bps = (int)max_blocks_per_seq;
+    a.tiles_max = (int)tiles;
+    a.scale_log2 = scale * kLog2e;
+    a.q_stride_token = q_stride_token;
+    a.q_stride_head = q_stride_head;
+    a.out_stride_token = out_stride_token;
+    a.out_stride_head = out_stride_head;
+    hipStream_t st = as_stream(stream);
+    if (dtype == NPD_DTYPE_BF16)
+      return fp8 ? launch_generic<BF16, true>(head_dim, a, grid, st, name)
+                 : launch_generic<BF16, false>(head_dim, a, grid, st, name);
+    return fp8 ? launch_generic<F16, true>(head_dim, a, grid, st, name)
+               : launch_generic<F16, false>(head_dim, a, grid, st, name);
+  }
   const Layout L = prefill_layout(num_seqs, num_heads, max_q_len, max_context_len);
   if (L.total > 0) {
     if (!workspace || workspace_bytes < L.total)

@@ -7,12 +7,16 @@
 // and apply_rotary_pos_emb (nanoPD/engine/model_runner.py:97-115), transposes
 // and copies k / v (.contiguous(), :142-143, :191-192) and calls
 // paged_kv_store (:146, :189): about a dozen elementwise launches plus the
-// copies. Here one wave handles one (token, head) row of the QKV output:
+// copies. Here a group of lanes handles one (token, head) row of the QKV
+// output:
 //   rows [0, H)           q heads: normalise, rotate, write q_out
 //   rows [H, H + KV)      k heads: normalise, rotate, store to k_cache[slot]
 //   rows [H + KV, H + 2KV) v heads: store to v_cache[slot]
-// Lane l holds elements l and l + 64 of the 128-wide row: exactly a
-// rotate-half pair, so RoPE needs no data exchange.
+// A row of D elements takes LW = min(D / 2, 64) lanes (head dims 64, 128,
+// 256: 32, 64, 64 lanes; a wave holds two rows of 64). Lane l holds the
+// rotate-half pairs (i, i + D/2) for i = l, l + LW, ... (one pair for D 64 and
+// 128, two for D 256), so RoPE needs no data exchange; the RMS statistic is
+// a reduction over the row's LW lanes.
 // RMSNorm rounds as HF Qwen3RMSNorm does (transformers modeling_qwen3):
 // n = half(half(x * rsqrt(mean(x^2) + eps)) * w), with the mean in fp32.
 // RoPE then rotates n in fp32 with cos / sin of pos * inv_freq[l] (inv_freq
@@ -27,8 +31,7 @@
 
 namespace {
 
-constexpr int kThreads = 256;   // 4 rows per workgroup
-constexpr int kD = 128;
+constexpr int kThreads = 256;   // 4 waves per workgroup
 
 struct RopeArgs {
   uint16_t* q_out;
@@ -48,9 +51,11 @@ struct RopeArgs {
   float eps;
 };
 
-__device__ __forceinline__ float wave_sum(float x) {
+// Sum over aligned groups of LW lanes (the lanes of one row).
+template <int LW>
+__device__ __forceinline__ float group_sum(float x) {
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
+  for (int m = LW / 2; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
   return x;
 }
 
@@ -59,16 +64,27 @@ __device__ __forceinline__ float ld(const uint16_t* p) {
   return TT::lo((uint32_t)*p);
 }
 
-template <class TT, bool kF8>
+template <class TT, bool kF8, int D>
 __global__ __launch_bounds__(kThreads) void qk_norm_rope_store_kernel(RopeArgs a) {
-  const int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  constexpr int HALF = D / 2;
+  constexpr int LW = HALF < 64 ? HALF : 64;   // lanes per row
+  constexpr int P = HALF / LW;                // rotate-half pairs per lane
+  constexpr int RPW = 64 / LW;                // rows per wave
+  const int lane = threadIdx.x & 63;
+  const int64_t row =
+      ((int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6)) * RPW + lane / LW;
   if (row >= a.rows) return;
-  const int l = threadIdx.x & 63;
+  const int l = lane % LW;
   const int per = a.heads + 2 * a.kv_heads;
   const int64_t t = row / per;
   const int hh = (int)(row - t * per);
-  const uint16_t* src = a.qkv + t * a.qkv_stride + (int64_t)hh * kD;
-  const float x0 = ld<TT>(src + l), x1 = ld<TT>(src + l + 64);
+  const uint16_t* src = a.qkv + t * a.qkv_stride + (int64_t)hh * D;
+  float x0[P], x1[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    x0[p] = ld<TT>(src + l + p * LW);
+    x1[p] = ld<TT>(src + l + p * LW + HALF);
+  }
 
   const int slot = a.slots[t];
   const bool store = slot >= 0 && slot < a.num_blocks * a.block_size;
@@ -78,46 +94,86 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_store_kernel(RopeArgs a
   if (hh >= a.heads + a.kv_heads) {   // v: plain store
     if (!store) return;
     const int kh = hh - a.heads - a.kv_heads;
-    const int64_t e = ((blk * a.kv_heads + kh) * a.block_size + off) * kD;
+    const int64_t e = ((blk * a.kv_heads + kh) * a.block_size + off) * D;
     if constexpr (kF8) {
       uint8_t* dst = static_cast<uint8_t*>(a.v_cache) + e;
       const float sc = a.v_scale[kh];
-      dst[l] = (uint8_t)npd::e4m3_byte(x0, sc);
-      dst[l + 64] = (uint8_t)npd::e4m3_byte(x1, sc);
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        dst[l + p * LW] = (uint8_t)npd::e4m3_byte(x0[p], sc);
+        dst[l + p * LW + HALF] = (uint8_t)npd::e4m3_byte(x1[p], sc);
+      }
     } else {
       uint16_t* dst = static_cast<uint16_t*>(a.v_cache) + e;
-      dst[l] = src[l];
-      dst[l + 64] = src[l + 64];
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        dst[l + p * LW] = src[l + p * LW];
+        dst[l + p * LW + HALF] = src[l + p * LW + HALF];
+      }
     }
     return;
   }
   const bool is_q = hh < a.heads;
   const uint16_t* w = is_q ? a.q_w : a.k_w;
-  const float r = rsqrtf(wave_sum(x0 * x0 + x1 * x1) * (1.f / kD) + a.eps);
-  const float n0 = TT::lo(TT::from_float(TT::lo(TT::from_float(x0 * r)) * ld<TT>(w + l)));
-  const float n1 = TT::lo(TT::from_float(TT::lo(TT::from_float(x1 * r)) * ld<TT>(w + l + 64)));
-  float s, c;
-  sincosf((float)a.positions[t] * a.inv_freq[l], &s, &c);
-  const uint16_t y0 = (uint16_t)TT::from_float(n0 * c - n1 * s);
-  const uint16_t y1 = (uint16_t)TT::from_float(n1 * c + n0 * s);
+  float ss = 0.f;
+#pragma unroll
+  for (int p = 0; p < P; ++p) ss += x0[p] * x0[p] + x1[p] * x1[p];
+  const float r = rsqrtf(group_sum<LW>(ss) * (1.f / D) + a.eps);
+  const float pos = (float)a.positions[t];
+  uint16_t y0[P], y1[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int i = l + p * LW;
+    const float n0 = TT::lo(TT::from_float(TT::lo(TT::from_float(x0[p] * r)) * ld<TT>(w + i)));
+    const float n1 =
+        TT::lo(TT::from_float(TT::lo(TT::from_float(x1[p] * r)) * ld<TT>(w + i + HALF)));
+    float s, c;
+    sincosf(pos * a.inv_freq[i], &s, &c);
+    y0[p] = (uint16_t)TT::from_float(n0 * c - n1 * s);
+    y1[p] = (uint16_t)TT::from_float(n1 * c + n0 * s);
+  }
   uint16_t* dst;
   if (is_q) {
-    dst = a.q_out + t * a.q_stride + (int64_t)hh * kD;
+    dst = a.q_out + t * a.q_stride + (int64_t)hh * D;
   } else {
     if (!store) return;
     const int kh = hh - a.heads;
-    const int64_t e = ((blk * a.kv_heads + kh) * a.block_size + off) * kD;
+    const int64_t e = ((blk * a.kv_heads + kh) * a.block_size + off) * D;
     if constexpr (kF8) {
       uint8_t* d8 = static_cast<uint8_t*>(a.k_cache) + e;
       const float sc = a.k_scale[kh];
-      d8[l] = (uint8_t)npd::e4m3_byte(TT::lo(y0), sc);
-      d8[l + 64] = (uint8_t)npd::e4m3_byte(TT::lo(y1), sc);
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        d8[l + p * LW] = (uint8_t)npd::e4m3_byte(TT::lo(y0[p]), sc);
+        d8[l + p * LW + HALF] = (uint8_t)npd::e4m3_byte(TT::lo(y1[p]), sc);
+      }
       return;
     }
     dst = static_cast<uint16_t*>(a.k_cache) + e;
   }
-  dst[l] = y0;
-  dst[l + 64] = y1;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    dst[l + p * LW] = y0[p];
+    dst[l + p * LW + HALF] = y1[p];
+  }
+}
+
+template <class TT, bool kF8>
+void launch_rope(int64_t head_dim, int64_t grid, hipStream_t st, const RopeArgs& a) {
+  switch (head_dim) {
+    case 64:
+      hipLaunchKernelGGL((qk_norm_rope_store_kernel<TT, kF8, 64>), dim3((unsigned)grid),
+                         dim3(kThreads), 0, st, a);
+      break;
+    case 128:
+      hipLaunchKernelGGL((qk_norm_rope_store_kernel<TT, kF8, 128>), dim3((unsigned)grid),
+                         dim3(kThreads), 0, st, a);
+      break;
+    default:
+      hipLaunchKernelGGL((qk_norm_rope_store_kernel<TT, kF8, 256>), dim3((unsigned)grid),
+                         dim3(kThreads), 0, st, a);
+      break;
+  }
 }
 
 }  // namespace
@@ -136,8 +192,8 @@ int rope_impl(void* q_out, void* k_cache, void* v_cache, const void* qkv,
   using namespace npd;
   if (dtype != NPD_DTYPE_F16 && dtype != NPD_DTYPE_BF16)
     return fail(NPD_E_DTYPE, "%s: unsupported dtype code %d (fp16/bf16 only)", name, dtype);
-  if (head_dim != kD)
-    return fail(NPD_E_INVALID, "%s: head_dim %lld not supported (128 only)", name,
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(NPD_E_INVALID, "%s: head_dim %lld not in {64, 128, 256}", name,
                 (long long)head_dim);
   if (num_tokens < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_blocks <= 0 || block_size <= 0)
     return fail(NPD_E_INVALID, "%s: bad sizes", name);
@@ -152,7 +208,8 @@ int rope_impl(void* q_out, void* k_cache, void* v_cache, const void* qkv,
       !q_norm_weight || !k_norm_weight || (fp8 && (!k_scale || !v_scale)))
     return fail(NPD_E_INVALID, "%s: null pointer", name);
   const int64_t rows = num_tokens * (num_heads + 2 * num_kv_heads);
-  const int64_t grid = (rows + 3) / 4;
+  const int64_t rows_per_block = (kThreads / 64) * (head_dim == 64 ? 2 : 1);
+  const int64_t grid = (rows + rows_per_block - 1) / rows_per_block;
   if (grid > INT32_MAX) return fail(NPD_E_INVALID, "%s: too many rows", name);
   RopeArgs a;
   a.q_out = static_cast<uint16_t*>(q_out);
@@ -176,15 +233,11 @@ int rope_impl(void* q_out, void* k_cache, void* v_cache, const void* qkv,
   a.eps = eps;
   hipStream_t st = as_stream(stream);
   if (dtype == NPD_DTYPE_BF16) {
-    if (fp8)
-      hipLaunchKernelGGL((qk_norm_rope_store_kernel<BF16, true>), dim3((unsigned)grid), dim3(kThreads), 0, st, a);
-    else
-      hipLaunchKernelGGL((qk_norm_rope_store_kernel<BF16, false>), dim3((unsigned)grid), dim3(kThreads), 0, st, a);
+    if (fp8) launch_rope<BF16, true>(head_dim, grid, st, a);
+    else launch_rope<BF16, false>(head_dim, grid, st, a);
   } else {
-    if (fp8)
-      hipLaunchKernelGGL((qk_norm_rope_store_kernel<F16, true>), dim3((unsigned)grid), dim3(kThreads), 0, st, a);
-    else
-      hipLaunchKernelGGL((qk_norm_rope_store_kernel<F16, false>), dim3((unsigned)grid), dim3(kThreads), 0, st, a);
+    if (fp8) launch_rope<F16, true>(head_dim, grid, st, a);
+    else launch_rope<F16, false>(head_dim, grid, st, a);
   }
   return check_launch(name);
 }

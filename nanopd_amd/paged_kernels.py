@@ -442,7 +442,8 @@ def paged_prefill_attention_fp8(out: torch.Tensor, query: torch.Tensor, key_cach
     """:func:`paged_prefill_attention` over an FP8 pool written by
     :func:`paged_kv_store_slots_fp8` (no reference counterpart): K =
     e4m3(byte) * k_scale[kv head], V likewise, converted exactly to the
-    query's type before the MFMAs. query/out fp16 or bf16; head_dim 128."""
+    query's type before the MFMAs. query/out fp16 or bf16; head_dim 64, 128
+    or 256."""
     _prefill(out, query, key_cache, value_cache, block_tables, cu_seqlens_q, context_lens, scale,
              block_size, max_num_blocks_per_seq, max_q_len, max_context_len, workspace,
              (k_scale, v_scale))
@@ -565,7 +566,7 @@ def qk_norm_rope_store(q_out: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     contiguous; slot_mapping / positions: int32 [T]; inv_freq: fp32 [D / 2];
     norm weights: [D] in the cache dtype. Writes normalised + rotated q to
     q_out, normalised + rotated k and raw v to the caches at slot_mapping
-    (negative slots are not stored). D = 128.
+    (negative slots are not stored). D in {64, 128, 256}.
     With ``k_scale`` / ``v_scale`` (fp32 [num_kv_heads]) the caches are an FP8
     pool (torch.float8_e4m3fn or uint8): k and v are stored as the e4m3 bytes
     of value / scale, as :func:`paged_kv_store_slots_fp8` rounds them.

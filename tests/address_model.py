@@ -644,6 +644,41 @@ def prefill(W: Writes, L: PrefillLaunch, out: Buf, ws: Buf, cu: np.ndarray, ctx_
             W.index([cidx], K_MAX_COUNTERS, "prefill merge counter")
 
 
+def prefill_generic(W: Writes, S: int, H: int, KV: int, bs: int, max_bps: int, num_blocks: int,
+                    max_q_len: int, out: Buf, cu: np.ndarray, ctx_lens: np.ndarray,
+                    out_stride_token: int, out_stride_head: int, tables: np.ndarray,
+                    D: int) -> None:
+    """prefill_generic_kernel (head dims 64 / 256): one workgroup per
+    (sequence, head, 64-row tile); every K/V row it reads and every output
+    row it writes."""
+    tiles = _ceil(max_q_len, 64)
+    cap = max_bps * bs
+    G = H // KV
+    for bid in range(S * tiles * H):
+        h = bid % H
+        st = bid // H
+        s, t = st // tiles, st % tiles
+        q0 = int(cu[s])
+        qlen = int(cu[s + 1]) - q0
+        if t * 64 >= qlen:
+            continue
+        ctx = min(max(int(ctx_lens[s]), 0), cap)
+        prefix = ctx - qlen
+        rows = min(qlen - t * 64, 64)
+        nkeys = max(prefix + t * 64 + rows, 0)
+        if nkeys:
+            tok = np.arange(nkeys)
+            lb = tok // bs
+            W.index(lb, max_bps, "prefill_generic block-table column")
+            blk = np.clip(tables[s, lb], 0, num_blocks - 1)
+            ri = (blk * KV + h // G) * bs + (tok - lb * bs)
+            W.index(ri, num_blocks * KV * bs, "prefill_generic K/V row")
+        r = np.arange(t * 64, t * 64 + 64)
+        r = r[r < qlen]
+        lo = ((q0 + r) * out_stride_token + h * out_stride_head) * 2
+        W.add(out, lo, lo + 2 * D, "prefill_generic output rows")
+
+
 # ---------------------------------------------------------------------------
 # Block copy (copy_blocks.hip:15-29)
 # ---------------------------------------------------------------------------

@@ -272,3 +272,36 @@ def test_planted_mistakes_are_reported():
                True)
     with pytest.raises(A.OutOfBounds, match="prologue cache"):
         W.check()
+
+
+def test_head_dims_64_and_256():
+    """The fused prologue (two rows per wave at D 64, two rotate-half pairs
+    per lane at D 256) and the generic prefill kernel of those head dims:
+    every K/V row read and every store inside its buffer, over ragged chunks
+    on paged prefixes, an empty chunk, a chunk longer than its context (rows
+    before position 0) and block tables at their full width; a planted wrong
+    row stride is caught."""
+    rng = np.random.default_rng(64)
+    for d in (64, 256):
+        W = A.Writes()
+        h, kv, bs, nblk = 6, 2, 16, 400
+        # prologue: 37 tokens, every 7th slot skipped, q rows with a padded stride
+        T = 37
+        slots = rng.permutation(nblk * bs)[:T]
+        slots[::7] = -1
+        A.prologue(W, A.Buf("q_out", T * (h * d + 64) * 2), A.Buf("k", nblk * kv * bs * d * 2),
+                   A.Buf("v", nblk * kv * bs * d * 2), slots, T, h, kv, nblk, bs, h * d + 64,
+                   False, D=d)
+        q = np.array([300, 1, 0, 129, 64])
+        cu = np.concatenate([[0], np.cumsum(q)])
+        mb = 100
+        ctx = np.array([1300, 1, 0, mb * bs, 20])   # full-width table; 64 rows on 20 keys
+        tables = np.stack([rng.permutation(nblk)[:mb] for _ in q]).astype(np.int64)
+        A.prefill_generic(W, len(q), h, kv, bs, mb, nblk, int(q.max()),
+                          A.Buf("out", int(cu[-1]) * h * d * 2), cu, ctx, h * d, d, tables, d)
+        W.check()
+        bad = A.Writes()   # planted: output rows addressed with twice the row stride
+        A.prefill_generic(bad, len(q), h, kv, bs, mb, nblk, int(q.max()),
+                          A.Buf("out", int(cu[-1]) * h * d * 2), cu, ctx, 2 * h * d, d, tables, d)
+        with pytest.raises(A.OutOfBounds):
+            bad.check()

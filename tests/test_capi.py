@@ -97,7 +97,7 @@ def test_c_validation_paths_need_no_gpu():
     rope = lambda d, stride, code, t=4: _rc(  # noqa: E731
         "npd_qk_norm_rope_store", fake, fake, fake, fake, fake, fake, fake, fake, fake, t, 32, 8, d,
         64, 16, stride, 32 * d, ctypes.c_float(1e-6), code, None)
-    assert rope(64, 48 * 64, 1) == -1 and b"head_dim" in lib.npd_last_error()
+    assert rope(96, 48 * 96, 1) == -1 and b"head_dim" in lib.npd_last_error()
     assert rope(128, 40 * 128, 1) == -1 and b"stride" in lib.npd_last_error()
     assert rope(128, 48 * 128, 5) == -2
     assert rope(128, 48 * 128, 1, t=0) == 0
@@ -169,6 +169,9 @@ def test_prefill_workspace_size():
     assert lib.npd_paged_prefill_workspace_size(4, 2048, 32, 128, 512, 3584) == split(4, 32, 512, 4)
     assert lib.npd_paged_prefill_workspace_size(1, 100, 32, 128, 100, 1025) == split(1, 32, 100, 2)
     assert lib.npd_paged_prefill_workspace_size(2, 1024, 32, 128, 512, 32768) == split(2, 32, 512, 8)
+    # head dims 64 and 256 run unsplit (prefill_generic_kernel): no workspace
+    assert lib.npd_paged_prefill_workspace_size(4, 2048, 32, 64, 512, 3584) == 0
+    assert lib.npd_paged_prefill_workspace_size(2, 1024, 32, 256, 512, 32768) == 0
 
 
 def test_python_mirror_raises_like_torch_check():

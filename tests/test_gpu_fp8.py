@@ -177,14 +177,14 @@ def test_argument_checks(device):
                                        torch.ones(3, device=device), sc)
 
 
-def _fp8_prefill_case(device, prefixes, chunks, H, kvh, dtype, seed, bs=16):
+def _fp8_prefill_case(device, prefixes, chunks, H, kvh, dtype, seed, bs=16, D=128):
     """Random e4m3 pool (no NaN codes) with per-head scales, shuffled tables
     of prefix + chunk blocks, and the chunks' queries packed varlen."""
     g = torch.Generator().manual_seed(seed)
     ctx = [p + c for p, c in zip(prefixes, chunks)]
     nbs = [(n + bs - 1) // bs for n in ctx]
     total = sum(nbs) + 3
-    codes = torch.randint(0, 0x7E, (2, total, kvh, bs, 128), generator=g, dtype=torch.int32)
+    codes = torch.randint(0, 0x7E, (2, total, kvh, bs, D), generator=g, dtype=torch.int32)
     codes = codes | (torch.randint(0, 2, codes.shape, generator=g, dtype=torch.int32) << 7)
     kc, vc = codes[0].to(torch.uint8), codes[1].to(torch.uint8)
     order = torch.randperm(total, generator=g)
@@ -193,7 +193,7 @@ def _fp8_prefill_case(device, prefixes, chunks, H, kvh, dtype, seed, bs=16):
     for s, n in enumerate(nbs):
         bt[s, :n] = order[o:o + n]
         o += n
-    q = (torch.randn(sum(chunks), H, 128, generator=g) * 0.5).to(dtype)
+    q = (torch.randn(sum(chunks), H, D, generator=g) * 0.5).to(dtype)
     cu = torch.tensor([0] + list(np.cumsum(chunks)), dtype=torch.int32)
     ks = (0.5 + torch.rand(kvh, generator=g)) / 448
     vs = (0.5 + torch.rand(kvh, generator=g)) / 448
@@ -201,7 +201,7 @@ def _fp8_prefill_case(device, prefixes, chunks, H, kvh, dtype, seed, bs=16):
 
 
 def _prefill_run_and_check(device, q, kc, vc, bt, cu, ctx, ks, vs, max_q, dtype):
-    scale = 1 / math.sqrt(128)
+    scale = 1 / math.sqrt(q.size(-1))
     out = torch.full_like(q, float("nan")).to(device)
     pk.paged_prefill_attention_fp8(out, q.to(device), kc.to(device).view(torch.float8_e4m3fn),
                                    vc.to(device).view(torch.float8_e4m3fn), bt.to(device),
@@ -223,6 +223,16 @@ def test_prefill_group_sizes(device, dtype, G):
     empty prefix, a ragged chunk and a key range long enough to be split."""
     kvh = 2
     case = _fp8_prefill_case(device, [0, 100, 1500], [64, 37, 200], G * kvh, kvh, dtype, seed=G)
+    _prefill_run_and_check(device, *case, dtype)
+
+
+@pytest.mark.parametrize("hd", [64, 256])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_head_dims_64_and_256(device, hd, dtype):
+    """Head dims 64 and 256 over an FP8 pool (prefill_generic_kernel): empty
+    and paged prefixes, ragged chunks, a decode row."""
+    case = _fp8_prefill_case(device, [0, 100, 1500, 77], [64, 37, 200, 1], 8, 2, dtype,
+                             seed=hd, D=hd)
     _prefill_run_and_check(device, *case, dtype)
 
 
@@ -250,32 +260,34 @@ def test_prefill_fp8_argument_checks(device):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_fused_prologue_fp8_bytes(device, dtype):
+@pytest.mark.parametrize("hd", [64, 128, 256])
+def test_fused_prologue_fp8_bytes(device, dtype, hd):
     """The fused q/k-norm + RoPE prologue into an FP8 pool writes the same
     bytes as the 2-byte prologue followed by the FP8 store of its K/V rows,
-    and the same q; negative slots leave the pool untouched."""
-    g = torch.Generator(device=device).manual_seed(11)
+    and the same q; negative slots leave the pool untouched (head dims 64,
+    128, 256)."""
+    g = torch.Generator(device=device).manual_seed(11 + hd)
     T, H, KV, N, bs = 45, 16, 4, 32, 16
-    width = (H + 2 * KV) * 128
+    width = (H + 2 * KV) * hd
     qkv = (torch.randn(T, width + 8, generator=g, device=device) * 1.5).to(dtype)[:, :width]
-    qw = (1.0 + 0.2 * torch.randn(128, generator=g, device=device)).to(dtype)
-    kw = (1.0 + 0.2 * torch.randn(128, generator=g, device=device)).to(dtype)
+    qw = (1.0 + 0.2 * torch.randn(hd, generator=g, device=device)).to(dtype)
+    kw = (1.0 + 0.2 * torch.randn(hd, generator=g, device=device)).to(dtype)
     slots = torch.randperm(N * bs, generator=g, device=device)[:T].to(torch.int32)
     slots[::7] = -1
     pos = torch.randint(0, 40000, (T,), generator=g, device=device, dtype=torch.int32)
-    inv_freq = 1.0 / (1.0e6 ** (torch.arange(0, 128, 2, dtype=torch.float32, device=device) / 128))
+    inv_freq = 1.0 / (1.0e6 ** (torch.arange(0, hd, 2, dtype=torch.float32, device=device) / hd))
     ks = (0.01 + 0.05 * torch.rand(KV, generator=g, device=device)).float()
     vs = (0.01 + 0.05 * torch.rand(KV, generator=g, device=device)).float()
     # 2-byte prologue into a 2-byte pool, then the FP8 store of the stored rows
-    kc = torch.zeros(N, KV, bs, 128, dtype=dtype, device=device)
+    kc = torch.zeros(N, KV, bs, hd, dtype=dtype, device=device)
     vc = torch.zeros_like(kc)
-    q2 = torch.empty(T, H, 128, dtype=dtype, device=device)
+    q2 = torch.empty(T, H, hd, dtype=dtype, device=device)
     pk.qk_norm_rope_store(q2, kc, vc, qkv, slots, pos, inv_freq, qw, kw, 1e-6)
     keep = slots >= 0
     sl = slots[keep].long()
-    k_rows = kc.permute(0, 2, 1, 3).reshape(N * bs, KV, 128)[sl]
-    v_rows = vc.permute(0, 2, 1, 3).reshape(N * bs, KV, 128)[sl]
-    want_k = torch.full((N, KV, bs, 128), 0x5A, dtype=torch.uint8, device=device)
+    k_rows = kc.permute(0, 2, 1, 3).reshape(N * bs, KV, hd)[sl]
+    v_rows = vc.permute(0, 2, 1, 3).reshape(N * bs, KV, hd)[sl]
+    want_k = torch.full((N, KV, bs, hd), 0x5A, dtype=torch.uint8, device=device)
     want_v = want_k.clone()
     pk.paged_kv_store_slots_fp8(want_k.view(torch.float8_e4m3fn), want_v.view(torch.float8_e4m3fn),
                                 k_rows, v_rows, slots[keep].contiguous(), ks, vs)

@@ -194,3 +194,45 @@ def test_workspace_reuse_and_explicit_workspace(device):
     with pytest.raises(RuntimeError, match="workspace"):
         pk.paged_prefill_attention(torch.empty_like(q), q, kc, vc, bt, cu, ctx, scale, 16, mb, mq,
                                    workspace=ws[:64])
+
+
+@pytest.mark.parametrize("hd", [64, 256])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("prefixes,chunks,G,kvh,bs", [
+    ([0], [1], 4, 2, 16),
+    ([0, 70, 300], [130, 45, 64], 4, 2, 16),
+    ([5, 1000, 0], [1, 17, 65], 2, 4, 32),
+    ([1536, 0, 4000], [512, 200, 96], 1, 4, 8),
+    ([0, 512, 2000, 99], [300, 128, 1, 1], 6, 1, 16),
+])
+def test_head_dims_64_and_256(device, hd, dtype, prefixes, chunks, G, kvh, bs):
+    """Head dims 64 and 256 (prefill_generic_kernel): empty and paged
+    prefixes, ragged chunks and decode rows in one call, group sizes 1-6,
+    block sizes 8-32."""
+    print(f"prefill D={hd} {dtype} prefixes={prefixes} chunks={chunks} G={G} kvh={kvh} bs={bs}",
+          flush=True)
+    args = make_case(device, prefixes, chunks, H=G * kvh, kvh=kvh, D=hd, bs=bs, dtype=dtype,
+                     seed=hd + sum(chunks))
+    q, kc, vc, bt, cu, ctx, mb, mq = args
+    scale = 1 / math.sqrt(hd)
+    check(run(*args, scale), q, kc, vc, bt, cu, ctx, scale)
+
+
+@pytest.mark.parametrize("hd", [64, 256])
+def test_head_dims_64_and_256_zero_rows_and_decode(device, hd):
+    """Rows before position 0 are zeros; the last row of a chunk equals a
+    decode step over the same context (decode's generic path for D 64/256)."""
+    args = make_case(device, [0], [40], D=hd, seed=hd + 3)
+    q, kc, vc, bt, cu, ctx, mb, mq = args
+    short = torch.tensor([25], dtype=torch.int32, device=device)
+    out = run(q, kc, vc, bt, cu, short, mb, mq, 0.1)
+    assert torch.count_nonzero(out[:15]) == 0
+    check(out, q, kc, vc, bt, cu, short, 0.1)
+    scale = 1 / math.sqrt(hd)
+    args = make_case(device, [700], [300], D=hd, seed=hd + 11)
+    q, kc, vc, bt, cu, ctx, mb, mq = args
+    full = run(*args, scale)
+    dec = torch.empty(1, 32, hd, dtype=q.dtype, device=device)
+    pk.paged_attention_forward(dec, q[-1:].contiguous(), kc, vc, bt, ctx, scale, 16, mb)
+    torch.cuda.synchronize()
+    assert max_abs(full[-1:], f32(dec).astype(np.float64)) <= ATOL[torch.bfloat16]

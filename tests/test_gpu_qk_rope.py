@@ -44,7 +44,7 @@ def rope_hf(x, cos, sin):
     return x * c + rot * s
 
 
-def _case(device, dtype, T, H, KV, num_blocks, bs, pad=0, seed=0, max_pos=40000):
+def _case(device, dtype, T, H, KV, num_blocks, bs, pad=0, seed=0, max_pos=40000, D=D):
     g = torch.Generator(device=device).manual_seed(seed)
     width = (H + 2 * KV) * D
     base = torch.randn(T, width + pad, generator=g, device=device, dtype=torch.float32) * 1.5
@@ -59,8 +59,9 @@ def _case(device, dtype, T, H, KV, num_blocks, bs, pad=0, seed=0, max_pos=40000)
     return qkv, qw, kw, slots, pos, inv_freq
 
 
-def _run(device, dtype, T, H, KV, num_blocks=64, bs=16, pad=0, seed=0):
-    qkv, qw, kw, slots, pos, inv_freq = _case(device, dtype, T, H, KV, num_blocks, bs, pad, seed)
+def _run(device, dtype, T, H, KV, num_blocks=64, bs=16, pad=0, seed=0, D=D):
+    qkv, qw, kw, slots, pos, inv_freq = _case(device, dtype, T, H, KV, num_blocks, bs, pad, seed,
+                                              D=D)
     sentinel = torch.tensor(7.0, dtype=dtype)
     kc = torch.full((num_blocks, KV, bs, D), float(sentinel), dtype=dtype, device=device)
     vc = kc.clone()
@@ -93,12 +94,7 @@ def _ulp(ref, dtype):
     return torch.pow(2.0, e - mant)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("T,H,KV,pad", [(1, 32, 8, 0), (37, 32, 8, 0), (512, 32, 8, 256),
-                                        (300, 16, 4, 64), (64, 8, 8, 0)])
-def test_matches_composites(device, dtype, T, H, KV, pad):
-    print(f"qk_norm_rope_store dtype={dtype} T={T} H={H} KV={KV} pad={pad}", flush=True)
-    res, kc, vc, vref = _run(device, dtype, T, H, KV, pad=pad, seed=T + H)
+def _check(res, kc, vc, vref, dtype, D):
     assert torch.equal(vc, vref), "v cache differs"
     # unit roundoff of the storage dtype
     u = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
@@ -116,6 +112,27 @@ def test_matches_composites(device, dtype, T, H, KV, pad):
         d = (got.float() - whf.float()).abs()
         tol = 2.5 * u * mag + 1.5 * u * whf.float().abs() + 1e-6
         assert (d <= tol).all(), f"{nm}: {(d - tol).max().item():.3e} beyond the HF composite bound"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("T,H,KV,pad", [(1, 32, 8, 0), (37, 32, 8, 0), (512, 32, 8, 256),
+                                        (300, 16, 4, 64), (64, 8, 8, 0)])
+def test_matches_composites(device, dtype, T, H, KV, pad):
+    print(f"qk_norm_rope_store dtype={dtype} T={T} H={H} KV={KV} pad={pad}", flush=True)
+    res, kc, vc, vref = _run(device, dtype, T, H, KV, pad=pad, seed=T + H)
+    _check(res, kc, vc, vref, dtype, D)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("hd", [64, 256])
+@pytest.mark.parametrize("T,H,KV,pad", [(1, 5, 1, 0), (37, 5, 1, 0), (130, 16, 4, 32),
+                                        (257, 8, 2, 0)])
+def test_head_dims_64_and_256(device, dtype, hd, T, H, KV, pad):
+    """D 64: two rows per wave (an odd row count leaves the last wave half
+    idle); D 256: two rotate-half pairs per lane."""
+    print(f"qk_norm_rope_store D={hd} dtype={dtype} T={T} H={H} KV={KV} pad={pad}", flush=True)
+    res, kc, vc, vref = _run(device, dtype, T, H, KV, pad=pad, seed=T + H + hd, D=hd)
+    _check(res, kc, vc, vref, dtype, hd)
 
 
 def test_untouched_slots_and_empty(device):
