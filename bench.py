@@ -176,7 +176,7 @@ def bench_decode(args, w) -> dict:
         "value": step_bytes / (ms_step * 1e-3) / 1e9,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": _profiled_traffic(f"decode_d128_kernel/{w.name}")},
+                     "traffic": _profiled_traffic(f"decode_fast_kernel/{w.name}")},
         "detail": {
             "attention_us_mean": round(attn_avg * 1e3, 2),
             "attention_us_in_step_mean": round(statistics.mean(attn_ms) * 1e3, 2),
@@ -189,7 +189,7 @@ def bench_decode(args, w) -> dict:
             "attention_bytes_per_sequence_sum": w.attention_bytes(),
             "store_bytes": w.store_bytes(),
             "kv_tokens": sum(w.seq_lens_list),
-            "kernels": "decode_d128_kernel (partitions + fused log-sum-exp merge)",
+            "kernels": "decode_fast_kernel (partitions + fused log-sum-exp merge)",
         },
     }
 
@@ -310,7 +310,7 @@ def bench_prefill(args, w) -> dict:
             "prefill_flops": flops,
             "prefill_tokens": tp,
             "decode_seqs": len(w.chunk_lens) - npf,
-            "kernels": "prefill_kernel (MFMA 16x16x32) + kv_store_kernel + decode_d128_kernel",
+            "kernels": "prefill_kernel (MFMA 16x16x32) + kv_store_kernel + decode_fast_kernel",
         },
     }
 
@@ -469,10 +469,10 @@ def bench_decode_fp8(args, w) -> int:
                    "step": "fp8 kv store (1 token/seq) + fp8 paged decode attention"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": _profiled_traffic(f"decode_d128_kernel/{w.name}_fp8")},
+                     "traffic": _profiled_traffic(f"decode_fast_kernel/{w.name}_fp8")},
         "detail": {"attention_us_mean": round(attn_ms * 1e3, 2), "attention_bytes": attn_bytes,
                    "context_tokens_per_s": round(ctx / (attn_ms * 1e-3), 1),
-                   "kernels": "decode_d128_kernel<.., fp8> (e4m3 -> bf16 in registers)"},
+                   "kernels": "decode_fast_kernel<.., fp8> (e4m3 -> bf16 in registers)"},
     }), flush=True)
     return 0
 

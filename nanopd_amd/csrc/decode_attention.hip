@@ -42,6 +42,9 @@ constexpr int kStep = 16;            // tokens per step
 #define NPD_DECODE_NT 1
 #endif
 constexpr int kRing = NPD_DECODE_RING;   // fast path: K/V steps in flight per wave
+// head dim 64: rows of 128 bytes, half the bytes per step; twice the steps in
+// flight keep the same bytes in flight (and the same ring registers)
+constexpr int ring_of(int d) { return d == 64 ? 2 * kRing : kRing; }
 #ifndef NPD_FAST_MAX_PARTITION
 #define NPD_FAST_MAX_PARTITION 2048
 #endif
@@ -387,16 +390,20 @@ __global__ __launch_bounds__(64) void decode_partition_kernel(DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Fast path: head_dim 128, block_size a multiple of 16 (<= 256).
+// Fast path: head_dim 128 (any power-of-two block size from 16 to 256) and
+// head_dim 64 or 256 (block sizes 16 and 32).
 //
 // Same work unit and passes as decode_partition_kernel, with the per-step
 // cost cut down:
 //   * a step is 16 tokens inside one block, so the block id is one readlane
 //     per step and every lane's load offsets are loop constants;
-//   * the reduce-scatter of the q.k partial sums over the 16 lanes of a token
-//     row uses DPP: partners are lane^8 (row_ror:8), lane^7 (row_half_mirror),
-//     lane^2 and lane^1 (quad_perm). A lane's partial sums are indexed
-//     k = head_slot * 4 + token_slot. Stages on head bits need no selects: q
+//   * the reduce-scatter of the q.k partial sums over the LPT = D/8 lanes of
+//     a token row uses DPP: for D 128 the partners are lane^8 (row_ror:8),
+//     lane^7 (row_half_mirror), lane^2 and lane^1 (quad_perm); D 64 (8 lanes)
+//     takes the last three stages; D 256 (32 lanes) adds lane^16 with
+//     v_permlane16_swap (which hands each lane its kept value and its
+//     partner's sent one, no select). A lane's partial sums are indexed
+//     k = head_slot * NL + token_slot. Stages on head bits need no selects: q
 //     slot h of a lane holds head h ^ hmask(lane), chosen so that at every such
 //     stage the half a lane keeps is its lower half (one v_add_f32_dpp per
 //     value). Stages on token bits pick the kept half with v_cndmask, so the K
@@ -459,10 +466,53 @@ __device__ __forceinline__ void bfly_stage(float* v, bool upper) {
   }
 }
 
+// The lane^16 stage of D 256 (rows of 32 lanes): v_permlane16_swap(A, B)
+// exchanges A of the odd 16-lane rows with B of the even ones. With A = v[p]
+// and B = v[p + HALF], an even-row lane (keeping the lower half) ends with its
+// own v[p] and its partner's v[p], an odd-row lane with its partner's
+// v[p + HALF] and its own v[p + HALF]: their sum is kept + received either way.
+template <int CNT>
+__device__ __forceinline__ void bfly_swap16(float* v) {
+  constexpr int HALF = CNT >= 2 ? CNT / 2 : 1;
+#pragma unroll
+  for (int p = 0; p < HALF; ++p) {
+    const uint32_t lo = __float_as_uint(v[p]);
+    const uint32_t hi = __float_as_uint(CNT >= 2 ? v[p + HALF] : v[p]);
+    const auto sw = __builtin_amdgcn_permlane16_swap(lo, hi, false, false);
+    v[p] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
+}
+
+// Stage k (0-based) of the reduce-scatter over the D/8 lanes of a token row:
+// the coordinate of lane j in that stage's basis direction (which half it
+// keeps), and the DPP control of its partner.
+template <int D>
+__device__ __forceinline__ int stage_coord(int j, int k) {
+  if constexpr (D == 64) return bfly_coord(j, k + 2);
+  else if constexpr (D == 128) return bfly_coord(j, k + 1);
+  else return k < 4 ? bfly_coord(j & 15, k + 1) : (j >> 4) & 1;
+}
+template <int D>
+constexpr int stage_ctrl(int k) {
+  return D == 64 ? (k == 0 ? kDppHalfMirror : (k == 1 ? kDppXor2 : kDppXor1))
+                 : (k == 0 ? kDppRor8 : (k == 1 ? kDppHalfMirror : (k == 2 ? kDppXor2 : kDppXor1)));
+}
+// Stage K over NV values (halving while two or more remain, then all-reduce);
+// stages below LGP split head bits (free), the rest select by `upper`.
+template <int D, int NV, int LGP, int K>
+__device__ __forceinline__ void rs_stage(float* v, int j) {
+  constexpr int CNT = (NV >> K) >= 2 ? (NV >> K) : 1;
+  if constexpr (D == 256 && K == 4) {
+    bfly_swap16<CNT>(v);
+  } else {
+    bfly_stage<CNT, stage_ctrl<D>(K), (K < LGP)>(v, stage_coord<D>(j, K) != 0);
+  }
+}
+
 using npd::ld_coherent2;
 using npd::st_coherent2;
 
-// Merge of one (sequence, kv-head) by a single wave (fast path, D = 128), the
+// Merge of one (sequence, kv-head) by a single wave (fast path), the
 // same log-sum-exp merge as merge_unit but latency-bound work done in parallel:
 //   A: lane p loads (m, l) of partition p for every head; a wave reduction
 //      gives M (partitions past 64 are read in a second loop). The first
@@ -478,11 +528,11 @@ using npd::st_coherent2;
 // normalised rows of (sequence s, kv-head kh) go to the output.
 constexpr int kMergeFlight = 4;
 constexpr int kMergeGroup = 16;   // partitions per first-level merge (long contexts)
-template <class TT, int G>
+template <class TT, int D, int G>
 __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int64_t slot0, int nparts,
                                                 int64_t dst, int s, int kh, int lane, float* s_w,
                                                 float oscale) {
-  constexpr int D = 128, GP = pow2ceil(G), CH = D / 8;
+  constexpr int GP = pow2ceil(G), CH = D / 8;
   constexpr int OWN = (G * CH + 63) / 64;   // (head, chunk) pairs per lane
   auto slot = [&](int p) -> int64_t { return slot0 + p; };
   // the first batch of partial rows of the lane's first (head, chunk) pair is
@@ -497,7 +547,7 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int64_t slo
       const int pq = p0 + (q0 + q < n ? q0 + q : n - 1);
       const float* src = a.part_acc + (slot(pq) * G + h) * D + c * 2;
 #pragma unroll
-      for (int k2 = 0; k2 < 4; ++k2) ld_coherent2(src + k2 * 32, x[q][2 * k2], x[q][2 * k2 + 1]);
+      for (int k2 = 0; k2 < 4; ++k2) ld_coherent2(src + k2 * (2 * CH), x[q][2 * k2], x[q][2 * k2 + 1]);
     }
   };
   load_batch(0, n0, 0, h0, c0);
@@ -569,7 +619,7 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int64_t slo
         // same layout as a published partition: [dim pair][chunk][2]
         float* row = a.part_acc + (dst * G + h) * D + c * 2;
 #pragma unroll
-        for (int k2 = 0; k2 < 4; ++k2) st_coherent2(row + k2 * 32, o[k][2 * k2], o[k][2 * k2 + 1]);
+        for (int k2 = 0; k2 < 4; ++k2) st_coherent2(row + k2 * (2 * CH), o[k][2 * k2], o[k][2 * k2 + 1]);
       } else {
         store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + c * 8,
                        o[k], oscale / L[h]);
@@ -608,20 +658,27 @@ struct KvSrc<TT, true> {
   }
 };
 
-template <class TT, int G, int SPB, bool kF8 = false>
-__device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, int part,
+template <class TT, int D, int G, int SPB, bool kF8 = false>
+__device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, int part,
                                                  int ps, float* s_p, uint32_t* s_pp) {
   typedef KvSrc<TT, kF8> Src;
   typedef typename Src::raw raw_t;
-  constexpr int D = 128;
+  static_assert(D == 64 || D == 128 || D == 256, "head dims of the fast path");
+  static_assert(!kF8 || D == 128, "FP8 pools: head_dim 128");
+  constexpr int LPT = D / 8;            // lanes per token row (16-byte chunks)
+  constexpr int TPL = 64 / LPT;         // token rows per load
+  constexpr int NL = 16 / TPL;          // loads per 16-token step (token slots)
+  constexpr int NLB = ilog2(NL);
+  constexpr int NS = ilog2(LPT);        // reduce-scatter stages
   constexpr int GP = pow2ceil(G);
   constexpr int LGP = ilog2(GP);
-  constexpr int NV = 4 * GP;            // 4 token slots x GP head slots
+  constexpr int NV = NL * GP;           // NL token slots x GP head slots
   constexpr int NB = ilog2(NV);
-  constexpr int NH = NB < 4 ? NB : 4;   // halving stages
+  constexpr int NH = NB < NS ? NB : NS; // halving stages
   constexpr int HELD = NV >> NH;
+  constexpr int NTS = NH > LGP ? NH - LGP : 0;   // token bits split by stages
   constexpr int BS = 16 * SPB;
-  constexpr int NBUF = kRing;           // steps in flight per pass
+  constexpr int NBUF = ring_of(D);      // steps in flight per pass
   // pass 3 on packed 2-byte probabilities with v_dot2 (FP8 pools: their short
   // partitions leave LDS room for the packed copy), else on the fp32 ones
   constexpr bool kDot2 = kF8;
@@ -629,7 +686,7 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
 
   (void)MAXT;
   const int lane = threadIdx.x;
-  const int r = lane >> 4, j = lane & 15;
+  const int r = lane / LPT, j = lane % LPT;
   const int s = unit / a.num_kv_heads;
   const int kh = unit - s * a.num_kv_heads;
 
@@ -637,7 +694,7 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
   const int cap = a.max_bps * BS;
   ctx = ctx < cap ? ctx : cap;
   if (ctx <= 0) {
-    if (part == 0 && lane < 16) {
+    if (part == 0 && lane < LPT) {
       const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
       for (int h = 0; h < G; ++h)
         store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + j * 8, z, 0.f);
@@ -653,14 +710,15 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
   const int nsteps = (((ntok + 15) >> 4) + NBUF - 1) / NBUF * NBUF;
   const int b0 = t0 / BS;
 
-  // stages 1..LGP split head bits (q slots permuted by hmask), the next two
-  // split token bits (selects); see bfly_coord
+  // stages 0..LGP-1 split head bits (q slots permuted by hmask), the next
+  // NTS split token bits, high to low (selects); see stage_coord
   int hmask = 0;
 #pragma unroll
-  for (int st = 1; st <= LGP && st <= 4; ++st) hmask |= bfly_coord(j, st) << (LGP - st);
+  for (int k = 0; k < LGP && k < NS; ++k) hmask |= stage_coord<D>(j, k) << (LGP - 1 - k);
   const int headmask = hmask;
-  const bool tup1 = bfly_coord(j, LGP + 1) != 0;   // token bit 1 kept
-  const bool tup0 = bfly_coord(j, LGP + 2) != 0;   // token bit 0 kept
+  int tokhi = 0;   // the token-slot bits this lane keeps (the low NLB - NTS bits are held)
+#pragma unroll
+  for (int t = 0; t < NTS; ++t) tokhi |= stage_coord<D>(j, LGP + t) << (NLB - 1 - t);
 
   // q slot h holds head h ^ headmask of the group (zeros for padding heads)
   u32x4 qv[GP];
@@ -684,7 +742,7 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
     if (lane < nb) myblk0 = clamp_blk(row[lane]);
     if (lane + 64 < nb) myblk1 = clamp_blk(row[lane + 64]);
   }
-  const int voff = (r * 16) + j;   // offset (in lane chunks) of the lane's chunk: slot i is token i*4 + r
+  const int voff = lane;   // offset (in lane chunks) of the lane's chunk r * LPT + j: slot i is token i*TPL + r
   // scores in log2 units (times the K scale of an fp8 pool); output scale
   const int pkh = kh / a.kv_split;   // the unit's kv head in the pool
   const float score_scale = kF8 ? a.scale_log2 * a.k_scale[pkh] : a.scale_log2;
@@ -695,27 +753,27 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
   auto step_base = [&](int st) -> int64_t {              // chunk index of the step's first row
     const int bi = st / SPB;   // wave-uniform
     const int blk = __builtin_amdgcn_readlane(bi < 64 ? myblk0 : myblk1, bi & 63);
-    return ((int64_t)blk * blk_rows + head_rows + (st % SPB) * 16) * 16;
+    return ((int64_t)blk * blk_rows + head_rows + (st % SPB) * 16) * LPT;
   };
   // K/V rows are read once per call: nontemporal loads keep them from
   // displacing reusable lines in L2
   auto load_k = [&](raw_t* buf, int st) {
     const int64_t b = step_base(st) + voff;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) buf[i] = Src::load(a.k_cache, b + i * 64);
+    for (int i = 0; i < NL; ++i) buf[i] = Src::load(a.k_cache, b + i * 64);
   };
   auto load_v = [&](raw_t* buf, int st) {
     const int64_t b = step_base(st) + voff;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) buf[i] = Src::load(a.v_cache, b + i * 64);
+    for (int i = 0; i < NL; ++i) buf[i] = Src::load(a.v_cache, b + i * 64);
   };
 
   // ---------------- pass 1: scores ----------------
   float runmax = -INFINITY;   // max of the scores this lane stored (its head: headmask)
   auto score_step = [&](const raw_t* kraw, int st) {
-    float v[NV];   // v[h * 4 + i]: q slot h . token slot i
+    float v[NV];   // v[h * NL + i]: q slot h . token slot i
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NL; ++i) {
       const u32x4 kbi = Src::pairs(kraw[i]);
 #pragma unroll
       for (int h = 0; h < GP; ++h) {
@@ -723,25 +781,21 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
         d = TT::dot2(kbi.y, qv[h].y, d);
         d = TT::dot2(kbi.z, qv[h].z, d);
         d = TT::dot2(kbi.w, qv[h].w, d);
-        v[h * 4 + i] = d;
+        v[h * NL + i] = d;
       }
     }
     // head stages (free), then token stages (select), then all-reduce
-    constexpr int C1 = NV, C2 = NV / 2 > 0 ? NV / 2 : 1, C3 = NV / 4 > 0 ? NV / 4 : 1;
-    constexpr int C4 = NV / 8 > 0 ? NV / 8 : 1;
-    bfly_stage<C1, kDppRor8, (LGP >= 1)>(v, LGP == 0 ? tup1 : false);
-    bfly_stage<C2, kDppHalfMirror, (LGP >= 2)>(v, LGP == 1 ? tup1 : (LGP == 0 ? tup0 : false));
-    bfly_stage<(NV >= 8 ? C3 : 1), kDppXor2, (LGP >= 3)>(
-        v, LGP == 2 ? tup1 : (LGP == 1 ? tup0 : false));
-    bfly_stage<(NV >= 16 ? C4 : 1), kDppXor1, (LGP >= 4)>(
-        v, LGP == 3 ? tup1 : (LGP == 2 ? tup0 : false));
-    // held: head hmask, token bits (tup1, tup0) -- for GP = 8 two values,
-    // token bit 0 = e
+    rs_stage<D, NV, LGP, 0>(v, j);
+    rs_stage<D, NV, LGP, 1>(v, j);
+    rs_stage<D, NV, LGP, 2>(v, j);
+    if constexpr (NS >= 4) rs_stage<D, NV, LGP, 3>(v, j);
+    if constexpr (NS >= 5) rs_stage<D, NV, LGP, 4>(v, j);
+    // held: head hmask, token slot tokhi | e
 #pragma unroll
     for (int e = 0; e < HELD; ++e) {
       const int h = headmask;
-      const int ti = (tup1 ? 2 : 0) + (HELD == 2 ? e : (tup0 ? 1 : 0));
-      const int tl = st * 16 + ti * 4 + r;
+      const int ti = tokhi | e;
+      const int tl = st * 16 + ti * TPL + r;
       if (h < G) {
         const float sv = (tl < ntok) ? v[e] * score_scale : -INFINITY;
         s_p[tl * GP + h] = sv;
@@ -752,7 +806,7 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
   {
     // ring of NBUF steps in flight; the last round is peeled so the steady
     // loop has no branches and each wait leaves the newer loads pending
-    raw_t kb[NBUF][4];
+    raw_t kb[NBUF][NL];
 #pragma unroll
     for (int b = 0; b < NBUF; ++b) load_k(kb[b], b);
     auto round = [&](int st0) {
@@ -768,7 +822,7 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
     for (int b = 0; b < NBUF; ++b) score_step(kb[b], st0 + b);
   }
 
-  raw_t vb[NBUF][4];
+  raw_t vb[NBUF][NL];
 #pragma unroll
   for (int b = 0; b < NBUF; ++b) load_v(vb[b], b);
   __syncthreads();
@@ -818,13 +872,13 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[h][d] = 0.f;
   auto pv_step = [&](const raw_t* vraw, int st) {
-    u32x4 vbuf[4];
+    u32x4 vbuf[NL];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) vbuf[i] = Src::pairs(vraw[i]);
+    for (int i = 0; i < NL; ++i) vbuf[i] = Src::pairs(vraw[i]);
     if (st * 16 + 16 > ntok) {   // tail step: rows past the context may hold anything
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (st * 16 + i * 4 + r >= ntok) vbuf[i] = u32x4{0, 0, 0, 0};
+      for (int i = 0; i < NL; ++i)
+        if (st * 16 + i * TPL + r >= ntok) vbuf[i] = u32x4{0, 0, 0, 0};
     }
   if constexpr (kDot2) {
     // slots 2q and 2q+1 hold tokens 8q + r and 8q + 4 + r: pack their values
@@ -859,8 +913,8 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tl = st * 16 + i * 4 + r;
+    for (int i = 0; i < NL; ++i) {
+      const int tl = st * 16 + i * TPL + r;
       float p[GP];
       if constexpr (GP >= 4) {
 #pragma unroll
@@ -898,23 +952,28 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
 #pragma unroll
     for (int b = 0; b < NBUF; ++b) pv_step(vb[b], st0 + b);
   }
-  // sum over the 4 rows (lane, lane ^ 16, ^ 32, ^ 48) with the gfx950 row
-  // swaps: v_permlane16_swap / v_permlane32_swap with both operands x hand
-  // every lane {x, x of lane ^ 16} (^ 32) in some order
+  // sum over the TPL rows of the wave (lanes equal in j): lane ^ 8 by DPP
+  // (D 64), then the gfx950 row swaps: v_permlane16_swap / v_permlane32_swap
+  // with both operands x hand every lane {x, x of lane ^ 16} (^ 32) in some
+  // order
 #pragma unroll
   for (int h = 0; h < G; ++h)
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
-      const uint32_t x = __float_as_uint(acc[h][d]);
-      const auto p16 = __builtin_amdgcn_permlane16_swap(x, x, false, false);
-      const float y = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
+      float y = acc[h][d];
+      if constexpr (TPL >= 8) y += dpp<kDppRor8>(y);
+      if constexpr (TPL >= 4) {
+        const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y),
+                                                          false, false);
+        y = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
+      }
       const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y),
                                                         false, false);
       acc[h][d] = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
     }
 
   if (nparts == 1) {
-    if (lane < 16) {
+    if (lane < LPT) {
 #pragma unroll
       for (int h = 0; h < G; ++h)
         store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + j * 8,
@@ -929,9 +988,9 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
   // no L2 writeback or invalidate is needed; the store completion wait orders
   // them before the counter update.
   // Partial rows are stored transposed, [dim pair k][chunk j][2], so that the
-  // 16 lanes of a row write 128 contiguous bytes per store; after the row
+  // LPT lanes of a row write 8 * LPT contiguous bytes per store; after the row
   // reduction every row of the wave holds the sums, so row r stores heads
-  // r, r + 4, ...
+  // r, r + TPL, ...
   //
   // Long contexts (merge groups on) merge in two levels. The last of each
   // group of kMergeGroup partitions to arrive merges the group into the
@@ -951,12 +1010,12 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
     const int64_t base = grouped && gsize == 1 ? gbase + g : ubase + part;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      if ((h & 3) != r) continue;
+      if ((h % TPL) != r) continue;
       float* dst = a.part_acc + (base * G + h) * D + j * 2;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) st_coherent2(dst + k * 32, acc[h][2 * k], acc[h][2 * k + 1]);
+      for (int k = 0; k < 4; ++k) st_coherent2(dst + k * (2 * LPT), acc[h][2 * k], acc[h][2 * k + 1]);
     }
-    if (lane < 16 && j == 0) {
+    if (lane == 0) {
 #pragma unroll
       for (int h = 0; h < G; ++h) st_coherent2(a.part_ml + (base * G + h) * 2, m[h], l[h]);
     }
@@ -986,7 +1045,7 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
   }
   for (;;) {
     if (ticket_of(counter) != n - 1) return;
-    merge_unit_fast<TT, G>(a, slot0, n, dst, s, kh, lane, s_p, dst >= 0 ? 1.f : out_scale);
+    merge_unit_fast<TT, D, G>(a, slot0, n, dst, s, kh, lane, s_p, dst >= 0 ? 1.f : out_scale);
     if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (dst < 0) return;
     // second level: the group results
@@ -1004,13 +1063,13 @@ __device__ __forceinline__ void decode_d128_item(const DecodeArgs& a, int unit, 
 // short ones fill the tail. The grid is sized for the most items possible;
 // workgroups past the list (all at the end of the grid) exit at once.
 // LDS is dynamic, sized for the launch's partition (fast_lds_bytes).
-template <class TT, int G, int SPB, bool kF8>
-__global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
+template <class TT, int D, int G, int SPB, bool kF8>
+__global__ __launch_bounds__(64) void decode_fast_kernel(DecodeArgs a) {
   constexpr int GP = pow2ceil(G);
   extern __shared__ __attribute__((aligned(16))) float s_dyn[];
   float* s_p = s_dyn;   // [partition + ring padding][GP] scores
   uint32_t* s_pp =   // [(partition + ring padding) / 2][GP] packed probabilities (kDot2)
-      kF8 ? reinterpret_cast<uint32_t*>(s_dyn + (a.partition + 16 * kRing) * GP) : nullptr;
+      kF8 ? reinterpret_cast<uint32_t*>(s_dyn + (a.partition + 16 * ring_of(D)) * GP) : nullptr;
   int unit, part, ps = a.partition;
   if (a.num_seqs <= kInlineSchedMax) {
     // Small batch: every workgroup derives its item from seq_lens alone, in
@@ -1104,10 +1163,10 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(DecodeArgs a) {
     unit = it.x;
     part = it.y;
   }
-  decode_d128_item<TT, G, SPB, kF8>(a, unit, part, ps, s_p, s_pp);
+  decode_fast_item<TT, D, G, SPB, kF8>(a, unit, part, ps, s_p, s_pp);
 }
 
-// Builds the work list of decode_d128_kernel (one workgroup):
+// Builds the work list of decode_fast_kernel (one workgroup):
 //   - zeroes the merge counters (per unit and per merge group);
 //   - counting-sorts the sequences by partition count, descending;
 //   - lists the items of each sequence in that order, unit by unit
@@ -1200,8 +1259,10 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(DecodeArgs a) {
 }
 
 bool use_fast_path(int64_t head_dim, int64_t block_size, int64_t num_seqs) {
-  return head_dim == 128 && block_size % 16 == 0 && block_size <= 256 &&
-         (block_size & (block_size - 1)) == 0 && num_seqs <= kSchedMaxSeqs;
+  if (num_seqs > kSchedMaxSeqs) return false;
+  if (head_dim == 128)
+    return block_size % 16 == 0 && block_size <= 256 && (block_size & (block_size - 1)) == 0;
+  return (head_dim == 64 || head_dim == 256) && (block_size == 16 || block_size == 32);
 }
 
 // Partition length (tokens per wave). The fast path takes the longest of
@@ -1263,40 +1324,45 @@ int64_t fast_grid(const DecodeArgs& a, int64_t units) {
   return n;
 }
 
-// Dynamic LDS of decode_d128_kernel for a partition: scores (fp32) of every
+// Dynamic LDS of decode_fast_kernel for a partition: scores (fp32) of every
 // token of the partition plus the ring padding, and their packed bf16/fp16
 // probabilities when pass 3 uses v_dot2 (FP8 pools).
-int64_t fast_lds_bytes(int partition, int g, bool fp8) {
-  const int64_t t = partition + 16 * kRing;
+int64_t fast_lds_bytes(int partition, int g, bool fp8, int d) {
+  const int64_t t = partition + 16 * ring_of(d);
   const int64_t gp = pow2ceil(g);
   return t * gp * 4 + (fp8 ? t / 2 * gp * 4 : 0);
 }
 
-template <class TT, int G, int SPB, bool kF8 = false>
+template <class TT, int D, int G, int SPB, bool kF8 = false>
 int launch_fast_bs(const DecodeArgs& a, int num_seqs, int64_t max_items, hipStream_t st) {
   if (num_seqs > kInlineSchedMax)
     hipLaunchKernelGGL(decode_schedule_kernel, dim3(1), dim3(kSchedThreads), 0, st, a, num_seqs);
-  hipLaunchKernelGGL((decode_d128_kernel<TT, G, SPB, kF8>), dim3((unsigned)max_items), dim3(64),
-                     (unsigned)fast_lds_bytes(a.partition, G, kF8), st, a);
+  hipLaunchKernelGGL((decode_fast_kernel<TT, D, G, SPB, kF8>), dim3((unsigned)max_items), dim3(64),
+                     (unsigned)fast_lds_bytes(a.partition, G, kF8, D), st, a);
   return NPD_OK;
 }
 
-template <class TT, int G>
+template <class TT, int D, int G>
 int launch_fast(const DecodeArgs& a, int num_seqs, int64_t max_items, hipStream_t st) {
-  switch (a.block_size) {
-    case 16: return launch_fast_bs<TT, G, 1>(a, num_seqs, max_items, st);
-    case 32: return launch_fast_bs<TT, G, 2>(a, num_seqs, max_items, st);
-    case 64: return launch_fast_bs<TT, G, 4>(a, num_seqs, max_items, st);
-    case 128: return launch_fast_bs<TT, G, 8>(a, num_seqs, max_items, st);
-    default: return launch_fast_bs<TT, G, 16>(a, num_seqs, max_items, st);
+  if constexpr (D != 128) {   // block sizes 16 and 32 (use_fast_path)
+    if (a.block_size == 16) return launch_fast_bs<TT, D, G, 1>(a, num_seqs, max_items, st);
+    return launch_fast_bs<TT, D, G, 2>(a, num_seqs, max_items, st);
+  } else {
+    switch (a.block_size) {
+      case 16: return launch_fast_bs<TT, D, G, 1>(a, num_seqs, max_items, st);
+      case 32: return launch_fast_bs<TT, D, G, 2>(a, num_seqs, max_items, st);
+      case 64: return launch_fast_bs<TT, D, G, 4>(a, num_seqs, max_items, st);
+      case 128: return launch_fast_bs<TT, D, G, 8>(a, num_seqs, max_items, st);
+      default: return launch_fast_bs<TT, D, G, 16>(a, num_seqs, max_items, st);
+    }
   }
 }
 
-// FP8 pools: the fast path only, block sizes 16 and 32
+// FP8 pools: the fast path only, head_dim 128, block sizes 16 and 32
 template <class TT, int G>
 int launch_fast_fp8(const DecodeArgs& a, int num_seqs, int64_t max_items, hipStream_t st) {
-  if (a.block_size == 16) return launch_fast_bs<TT, G, 1, true>(a, num_seqs, max_items, st);
-  return launch_fast_bs<TT, G, 2, true>(a, num_seqs, max_items, st);
+  if (a.block_size == 16) return launch_fast_bs<TT, 128, G, 1, true>(a, num_seqs, max_items, st);
+  return launch_fast_bs<TT, 128, G, 2, true>(a, num_seqs, max_items, st);
 }
 
 template <class TT>
@@ -1318,19 +1384,13 @@ int dispatch_fp8(int g, const DecodeArgs& a, int64_t units, hipStream_t st) {
 
 template <class TT, int D, int G>
 int launch_decode(const DecodeArgs& a, int64_t units, hipStream_t st) {
-  if constexpr (D == 128) {
-    if (use_fast_path(D, a.block_size, units / a.num_kv_heads)) {
-      const int rc = launch_fast<TT, G>(a, (int)(units / a.num_kv_heads), fast_grid(a, units), st);
-      if (rc != NPD_OK) return rc;
-      return npd::check_launch("npd_paged_attention");
-    } else {
-      hipLaunchKernelGGL((decode_partition_kernel<TT, D, G>),
-                         dim3((unsigned)units, (unsigned)a.max_parts), dim3(64), 0, st, a);
-    }
-  } else {
-    hipLaunchKernelGGL((decode_partition_kernel<TT, D, G>),
-                       dim3((unsigned)units, (unsigned)a.max_parts), dim3(64), 0, st, a);
+  if (use_fast_path(D, a.block_size, units / a.num_kv_heads)) {
+    const int rc = launch_fast<TT, D, G>(a, (int)(units / a.num_kv_heads), fast_grid(a, units), st);
+    if (rc != NPD_OK) return rc;
+    return npd::check_launch("npd_paged_attention");
   }
+  hipLaunchKernelGGL((decode_partition_kernel<TT, D, G>),
+                     dim3((unsigned)units, (unsigned)a.max_parts), dim3(64), 0, st, a);
   if (a.max_parts > 1)
     hipLaunchKernelGGL((merge_partitions_kernel<TT, D, G>), dim3((unsigned)units), dim3(256), 0, st, a);
   return npd::check_launch("npd_paged_attention");

@@ -11,10 +11,10 @@ Kernels covered (the FP8 and 2-byte pools share their addressing):
 - qk_norm_rope_store_kernel (qk_norm_rope.hip:55-111): q_out rows, cache rows
   by slot;
 - pack_metadata_kernel (metadata.hip:24-98): its output arrays;
-- decode_d128_kernel with its inline work list or decode_schedule_kernel's
-  (decode_attention.hip:1003-1095, :1105-1172), decode_d128_item's output,
-  partial, group-slot, (m, l) and counter stores (:626-995), merge_unit_fast's
-  reads and stores (:476-597), and the dynamic LDS of pass 1-3;
+- decode_fast_kernel (head dims 64, 128, 256) with its inline work list or
+  decode_schedule_kernel's, decode_fast_item's output, partial, group-slot,
+  (m, l) and counter stores, merge_unit_fast's reads and stores, and the
+  dynamic LDS of pass 1-3;
 - prefill_kernel's work list / fixed grid (prefill_attention.hip:164-288),
   its zero rows, partial records, counters and output rows (:290-660);
 - copy_blocks_kernel (copy_blocks.hip:15-29).
@@ -42,6 +42,11 @@ INLINE_SCHED_MAX = 64
 SCHED_MAX_SEQS = 4096
 MERGE_GROUP = 16
 RING = 2
+
+
+def ring_of(D: int) -> int:
+    """decode_attention.hip ring_of: steps in flight per pass."""
+    return 2 * RING if D == 64 else RING
 
 # prefill_attention.hip constants
 KT = 64
@@ -157,11 +162,16 @@ def pack_metadata(W: Writes, out: dict, desc: np.ndarray, num_seqs: int, total_q
 
 
 # ---------------------------------------------------------------------------
-# Decode attention, fast path (D = 128)
+# Decode attention, fast path
 # ---------------------------------------------------------------------------
 
 def use_fast_path(D: int, bs: int, S: int) -> bool:
-    return D == 128 and bs % 16 == 0 and bs <= 256 and (bs & (bs - 1)) == 0 and S <= SCHED_MAX_SEQS
+    """decode_attention.hip use_fast_path."""
+    if S > SCHED_MAX_SEQS:
+        return False
+    if D == 128:
+        return bs % 16 == 0 and bs <= 256 and (bs & (bs - 1)) == 0
+    return D in (64, 256) and bs in (16, 32)
 
 
 def choose_partition(S, H, KV, D, bs, max_ctx, fp8) -> int:
@@ -237,7 +247,7 @@ class DecodeLaunch:
 
 def decode_host(S, H, KV, bs, max_bps, fp8, D=128) -> DecodeLaunch:
     """The host choices of attention_impl (decode_attention.hip:1441-1511)."""
-    assert use_fast_path(D, bs, S), "model covers the D = 128 fast path"
+    assert use_fast_path(D, bs, S), "model covers the fast path"
     split = kv_split_of(H, KV)
     KV *= split
     L = DecodeLaunch(S, H, KV, bs, max_bps, fp8, split)
@@ -258,7 +268,7 @@ def decode_host(S, H, KV, bs, max_bps, fp8, D=128) -> DecodeLaunch:
         n = _ceil(n, 8 * split) * 8 * split
     L.grid = n
     gp = pow2ceil(G)
-    t = L.partition + 16 * RING
+    t = L.partition + 16 * ring_of(D)
     L.lds_floats = t * gp + (t // 2 * gp if fp8 else 0)
     return L
 
@@ -397,11 +407,12 @@ def decode(W: Writes, L: DecodeLaunch, out: Buf, ws: Buf, seq_lens: np.ndarray,
     out_rows(single, "decode output rows")
     # LDS of the item's passes: scores s_p[tl * GP + h], packed s_pp[pi * GP + h]
     ntok = np.minimum(ctx - part * ps, ps)   # ps: per item
-    nsteps = _ceil(_ceil(np.maximum(ntok, 0), 16), RING) * RING
+    ring = ring_of(D)
+    nsteps = _ceil(_ceil(np.maximum(ntok, 0), 16), ring) * ring
     if run.any():
-        W.index(nsteps[run] * 16 * gp - 1, L.partition * gp + 16 * RING * gp, "decode LDS scores")
+        W.index(nsteps[run] * 16 * gp - 1, L.partition * gp + 16 * ring * gp, "decode LDS scores")
         if L.fp8:
-            W.index((L.partition + 16 * RING) * gp + nsteps[run] * 8 * gp - 1, L.lds_floats,
+            W.index((L.partition + 16 * ring) * gp + nsteps[run] * 8 * gp - 1, L.lds_floats,
                     "decode LDS packed probabilities")
         nb = _ceil(ntok[run], L.bs)
         W.index(nb - 1, 128, "decode block ids per lane")
@@ -438,7 +449,7 @@ def decode(W: Writes, L: DecodeLaunch, out: Buf, ws: Buf, seq_lens: np.ndarray,
         W.read(ws, r, r + G * D * 4, f"decode merge {what} partial")
         r = L.ml_off + sl * G * 2 * 4
         W.read(ws, r, r + G * 8, f"decode merge {what} (m, l)")
-    W.index([64 * gp - 1], (L.partition + 16 * RING) * gp, "decode merge weights in LDS")
+    W.index([64 * gp - 1], (L.partition + 16 * ring) * gp, "decode merge weights in LDS")
     dst = gbase + g
     if first_lvl.any():
         r = L.part_off + ((dst[first_lvl][:, None] * G + h[None, :]) * D) * 4

@@ -30,19 +30,21 @@ GRAPH_WIDTHS = (16, 32, 64, 128, 256, 512, MAX_WIDTH)
 NUM_BLOCKS = 12288                            # bench.py's config-5 pool
 
 
-def _decode_ws(S, max_bps, bs=BS, h=H, kv=KV):
-    return int(_lib.load().npd_paged_attention_workspace_size(S, h, kv, D, bs, max_bps))
+def _decode_ws(S, max_bps, bs=BS, h=H, kv=KV, d=D):
+    return int(_lib.load().npd_paged_attention_workspace_size(S, h, kv, d, bs, max_bps))
 
 
 def _prefill_ws(S, tq, mq, mctx, h=H):
     return int(_lib.load().npd_paged_prefill_workspace_size(S, tq, h, D, mq, mctx))
 
 
-def check_decode(W, S, max_bps, seq_lens, fp8, out_rows=None, ws_bytes=None, h=H, kv=KV, bs=BS):
-    L = A.decode_host(S, h, kv, bs, max_bps, fp8)
-    out = A.Buf("decode out", (out_rows if out_rows is not None else S) * h * D * 2)
-    ws = A.Buf("decode workspace", ws_bytes if ws_bytes is not None else _decode_ws(S, max_bps, bs, h, kv))
-    A.decode(W, L, out, ws, np.asarray(seq_lens), h * D, D)
+def check_decode(W, S, max_bps, seq_lens, fp8, out_rows=None, ws_bytes=None, h=H, kv=KV, bs=BS,
+                 d=D):
+    L = A.decode_host(S, h, kv, bs, max_bps, fp8, D=d)
+    out = A.Buf("decode out", (out_rows if out_rows is not None else S) * h * d * 2)
+    ws = A.Buf("decode workspace",
+               ws_bytes if ws_bytes is not None else _decode_ws(S, max_bps, bs, h, kv, d))
+    A.decode(W, L, out, ws, np.asarray(seq_lens), h * d, d, D=d)
     return L
 
 
@@ -305,3 +307,20 @@ def test_head_dims_64_and_256():
                           A.Buf("out", int(cu[-1]) * h * d * 2), cu, ctx, 2 * h * d, d, tables, d)
         with pytest.raises(A.OutOfBounds):
             bad.check()
+
+
+def test_decode_fast_path_head_dims_64_and_256():
+    """The fast path at head dims 64 and 256 (block sizes 16 and 32): output,
+    partial, group-slot and counter stores inside the workspace the library
+    sizes, over short and 32k contexts, both work-list forms and G up to 16."""
+    rng = np.random.default_rng(256)
+    W = A.Writes()
+    for d in (64, 256):
+        for bs in (16, 32):
+            for h, kv in ((32, 8), (16, 2), (14, 2), (64, 4)):
+                mb = 32768 // bs + 1
+                check_decode(W, 8, mb, [1, 17, 300, 4097, 32768, 0, 9000, 12], False, h=h, kv=kv,
+                             bs=bs, d=d)
+                check_decode(W, 70, 4096 // bs, rng.integers(0, 4097, 70), False, h=h, kv=kv,
+                             bs=bs, d=d)
+    W.check()

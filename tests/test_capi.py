@@ -149,8 +149,16 @@ def test_workspace_size():
     assert ws(1024, 32, 8, 128, 16, 16) == fast(1024, 32, 8, 1)
     # 1 seq x 8 kv heads x 4k tokens in blocks of 16: partitions of 64
     assert ws(1, 32, 8, 128, 16, 256) == fast(1, 32, 8, 64)
-    # generic path (head_dim 64): partitions of 256 below 4096 waves
-    n = lib.npd_paged_attention_workspace_size(2, 8, 8, 64, 16, 64)
+    # head dims 64 and 256 take the fast path for blocks of 16 and 32: the
+    # same layout with G*D + 2G floats per partition (1 seq x 8 kv heads x 1k
+    # tokens: partitions of 64, 16 slots)
+    def fast_d(S, H, kvh, P, d):
+        units = S * kvh
+        return (2**20 + 16 + units * P * 8 + 255) // 256 * 256 + S * H * P * (d + 2) * 4
+    assert ws(2, 8, 8, 64, 16, 64) == fast_d(2, 8, 8, 16, 64)
+    assert ws(2, 8, 8, 256, 32, 32) == fast_d(2, 8, 8, 16, 256)
+    # generic path (block size 8, any head dim): partitions of 256 below 4096 waves
+    n = lib.npd_paged_attention_workspace_size(2, 8, 8, 64, 8, 128)
     assert n == 2**20 + 2 * 8 * 4 * (64 + 2) * 4
 
 

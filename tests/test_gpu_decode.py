@@ -115,12 +115,39 @@ def test_group_sizes_above_8(device, dtype, G, kvh):
     check(run(*args, 16), q, kc, vc, bt, sl, scale)
 
 
-@pytest.mark.parametrize("D,bs", [(64, 16), (256, 8), (128, 8)])
+@pytest.mark.parametrize("D,bs", [(64, 8), (256, 8), (128, 8)])
 def test_group_of_16_generic_path(device, D, bs):
-    """G = 16 on the generic kernel (head dims 64 / 256, block size 8)."""
+    """G = 16 on the generic kernel (block size 8)."""
     args = make_inputs(3, 32, 2, D, [1, 700, 3000], bs, torch.bfloat16, device, seed=D + bs)
     q, kc, vc, bt, sl, scale, mb = args
     check(run(*args, bs), q, kc, vc, bt, sl, scale)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("D", [64, 256])
+@pytest.mark.parametrize("bs", [16, 32])
+@pytest.mark.parametrize("G", [1, 3, 4, 8, 16])
+def test_fast_path_head_dims_64_and_256(device, dtype, D, bs, G):
+    """The fast path at head dims 64 (8 lanes per row) and 256 (32 lanes):
+    contexts up to 32k (two-level merges), an empty and a one-token sequence,
+    block sizes 16 and 32, G = 16 as two sub-groups of 8."""
+    lens = [1, 17, 300, 4097, 32768, 0]
+    kvh = 2 if G <= 8 else 1
+    print(f"decode fast path D={D} bs={bs} G={G} {dtype}", flush=True)
+    args = make_inputs(len(lens), G * kvh, kvh, D, lens, bs, dtype, device, seed=D * 100 + bs + G)
+    q, kc, vc, bt, sl, scale, mb = args
+    check(run(*args, bs), q, kc, vc, bt, sl, scale)
+
+
+@pytest.mark.parametrize("D", [64, 256])
+def test_fast_path_head_dims_scheduled(device, D):
+    """More than 64 sequences at head dims 64 / 256: the schedule kernel's
+    work list, config 2's head shape (32 q / 8 kv heads)."""
+    g = torch.Generator().manual_seed(D)
+    lens = torch.randint(0, 6000, (70,), generator=g).tolist()
+    args = make_inputs(70, 32, 8, D, lens, 16, torch.bfloat16, device, seed=D + 1)
+    q, kc, vc, bt, sl, scale, mb = args
+    check(run(*args, 16), q, kc, vc, bt, sl, scale)
 
 
 def test_group_of_16_scheduled_path(device):
