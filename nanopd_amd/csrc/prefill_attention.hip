@@ -45,10 +45,10 @@
 //     D[m = 4*(lane/16) + i][n = lane%16].
 //
 // Key splits: a query tile whose key range is longer than ks_steps steps of 64
-// keys is cut at multiples of ks_steps into nsp <= splits_max ranges run by
-// separate workgroups (the tiles of a long prefix would otherwise run many
-// times longer than the rest). Cutting at the same keys for every tile lets the
-// tiles of a sequence share each K/V range through L2.
+// keys is cut into nsp <= splits_max ranges run by separate workgroups (the
+// tiles of a long prefix would otherwise run many times longer than the rest):
+// near-equal parts when the work list orders the items (at most 64 tiles),
+// else at multiples of ks_steps.
 // Each split publishes its unnormalised O, running max and row sum with
 // device-coherent stores, then takes a ticket from a per-tile counter; the last
 // of the nsp to arrive merges the others into its registers
@@ -153,9 +153,12 @@ __device__ __forceinline__ u32x2 lds_read_tr(const uint16_t* p) {
 // The work item of this workgroup (every wave derives the same one): the
 // sequence s, its query tile t of TR rows, key split j of split length ks
 // steps, kv head kh and head group hg, and the sequence's first query row,
-// chunk length and context. false: no item, the workgroup exits.
+// chunk length and context. eq: the tile's nsp = ceil(steps / ks) splits are
+// near-equal parts (the first steps % nsp one step longer) instead of ks-step
+// splits and a shorter last one. false: no item, the workgroup exits.
 struct Item {
   int s, t, j, kh, hg, ks, q0, qlen, ctx;
+  bool eq;
 };
 template <int TR>
 __device__ __forceinline__ bool prefill_item(const PrefillArgs& a, int lane, Item& it) {
@@ -168,8 +171,7 @@ __device__ __forceinline__ bool prefill_item(const PrefillArgs& a, int lane, Ite
     // i % tiles_max) with n_i key steps. The split length ks is chosen so that
     // the longest key range falls into equal parts no shorter than the
     // average work per compute unit (and no shorter than the host's split,
-    // which sized the workspace). Items: first every full split (ks steps),
-    // level by level, then the last split of every tile, longest first. The
+    // which sized the workspace); each tile's splits are near-equal parts. The
     // kv-head is the fastest-varying index and every count is a multiple of
     // the kv-head count, so with 8 kv-heads each XCD (workgroups go to XCDs
     // round-robin by blockIdx) serves one kv-head and its K/V stays in that
@@ -197,46 +199,41 @@ __device__ __forceinline__ bool prefill_item(const PrefillArgs& a, int lane, Ite
     parts = parts < 1 ? 1 : parts;
     const int ksd = __builtin_amdgcn_readfirstlane((nmax + parts - 1) / parts);
     ks = ksd > ks ? ksd : ks;
+    // a tile of n steps runs as nsp = ceil(n / ks) near-equal parts: no short
+    // tail part that would pay a whole item's prologue and merge for a few
+    // steps. Items in longest-processing-time order: by part length (bucket
+    // len = ceil(n / nsp)), longest first; within a bucket by tile, part and
+    // then (kv-head, head group).
     int nsp = (n + ks - 1) / ks;
     nsp = nsp < 1 ? 1 : (nsp > a.splits_max ? a.splits_max : nsp);
-    const int full = valid ? nsp - 1 : 0;
-    // steps of the last split, in buckets 0 .. ks (a split count capped at
-    // splits_max leaves a longer last split: it goes in the top bucket)
-    int last = valid ? n - (nsp - 1) * ks : -1;
-    last = last > ks ? ks : last;
-    auto nth = [&](uint64_t m, int k) -> int {   // lane of the k-th set bit of m
-      const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
-      return __builtin_ctzll(__ballot(((m >> lane) & 1) && rank == k));
-    };
-    int id = blockIdx.x, sel = -1;
-    j = 0;
-    for (int lvl = 0;; ++lvl) {
-      const uint64_t m = __ballot(full > lvl);
-      if (m == 0) break;
-      const int c = __popcll(m) * per_item;
-      if (id < c) {
-        sel = nth(m, id / per_item);
-        j = lvl;
-        break;
-      }
+    if (!valid) nsp = 0;
+    const int len = valid ? (n + nsp - 1) / nsp : -1;
+    const int lenmax = npd::wave_max_i(len);
+    // items in buckets >= b, non-increasing in b; item id is in the last
+    // bucket b with from(b) > id (binary search over DPP wave sums)
+    auto from = [&](int b) -> int { return npd::wave_sum_i(len >= b ? nsp : 0) * per_item; };
+    int id = blockIdx.x;
+    if (id >= from(0)) return false;   // past the last item
+    int lo = 0, hi = lenmax;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (from(mid) > id) lo = mid; else hi = mid - 1;
+    }
+    id -= from(lo + 1);
+    // the tile of the bucket holding item id: walk the bucket's tiles (a
+    // wave-uniform loop over at most 64 lanes)
+    uint64_t m = __ballot(len == lo);
+    int sel = __builtin_ctzll(m);
+    for (;;) {
+      const int c = __builtin_amdgcn_readlane(nsp, sel) * per_item;
+      if (id < c || (m & (m - 1)) == 0) break;
       id -= c;
+      m &= m - 1;
+      sel = __builtin_ctzll(m);
     }
-    if (sel < 0) {
-      // items in buckets >= b, non-increasing in b; item id is in the last
-      // bucket b with from(b) > id (binary search over ballot counts)
-      auto from = [&](int b) -> int { return __popcll(__ballot(last >= b)) * per_item; };
-      if (id >= from(0)) return false;   // past the last item
-      int lo = 0, hi = ks;
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (from(mid) > id) lo = mid; else hi = mid - 1;
-      }
-      id -= from(lo + 1);
-      sel = nth(__ballot(last == lo), id / per_item);
-      j = __builtin_amdgcn_readlane(full, sel);
-    }
-    const int rem = id % per_item;
+    j = id / per_item;
+    id -= j * per_item;
+    const int rem = id;
     kh = rem % a.num_kv_heads;
     hg = rem / a.num_kv_heads;
     s = __builtin_amdgcn_readfirstlane(sel / a.tiles_max);
@@ -270,7 +267,7 @@ __device__ __forceinline__ bool prefill_item(const PrefillArgs& a, int lane, Ite
     ctx = ctx < 0 ? 0 : (ctx < cap ? ctx : cap);
   }
 
-  it = Item{s, t, j, kh, hg, ks, q0, qlen, ctx};
+  it = Item{s, t, j, kh, hg, ks, q0, qlen, ctx, a.num_seqs * a.tiles_max <= 64};
   return true;
 }
 
@@ -303,13 +300,21 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   int nkeys = pos0 + rows;                             // keys 0 .. last row's position
   nkeys = nkeys < 0 ? 0 : nkeys;
   const int nsteps = (nkeys + kKT - 1) / kKT;
-  // split j covers steps [j*ks, (j+1)*ks) -- the same keys for every tile of
-  // the sequence -- the last split runs to the end of the tile's range
+  // grid order: split j covers steps [j*ks, (j+1)*ks) -- the same keys for
+  // every tile of the sequence -- the last split runs to the end of the
+  // tile's range; work list: near-equal parts
   int nsp = (nsteps + ks - 1) / ks;
   nsp = nsp < 1 ? 1 : (nsp > a.splits_max ? a.splits_max : nsp);
   if (j >= nsp) return;
-  const int st0 = j * ks;
-  const int st1 = j == nsp - 1 ? nsteps : st0 + ks;
+  int st0, st1;
+  if (it.eq) {   // near-equal parts, the first nsteps % nsp one step longer
+    const int base = nsteps / nsp, rem = nsteps - base * nsp;
+    st0 = j * base + (j < rem ? j : rem);
+    st1 = st0 + base + (j < rem ? 1 : 0);
+  } else {
+    st0 = j * ks;
+    st1 = j == nsp - 1 ? nsteps : st0 + ks;
+  }
 
   // wave -> (head of the group, row tile, half of the row tile)
   const int pair = wave >> 1, half = wave & 1;

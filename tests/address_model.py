@@ -519,7 +519,7 @@ def prefill_host(S, H, KV, bs, max_bps, max_q_len, max_ctx, num_cus=256) -> Pref
 
 
 def prefill_items(L: PrefillLaunch, cu: np.ndarray, ctx_lens: np.ndarray):
-    """(s, t, j, kh, hg, q0, qlen, ctx, ks) per running workgroup
+    """(s, t, j, kh, hg, q0, qlen, ctx, ks, eq) per running workgroup
     (prefill_attention.hip:170-288)."""
     TR = 64 * L.rt
     cap = L.max_bps * L.bs
@@ -547,42 +547,34 @@ def prefill_items(L: PrefillLaunch, cu: np.ndarray, ctx_lens: np.ndarray):
         avg = _ceil(tot * per_item, L.num_cus)
         parts = max(nmax // avg if avg > 0 else 1, 1)
         ks = max(_ceil(nmax, parts), L.ks_steps)
-        nsp = np.clip(_ceil(n, ks), 1, L.splits)
-        full = np.where(valid, nsp - 1, 0)
-        last = np.where(valid, n - (nsp - 1) * ks, -1)
-        last = np.minimum(last, ks)
+        # near-equal parts per tile; items by part length (longest first),
+        # then tile, part, (kv-head, head group)
+        nsp = np.where(valid, np.clip(_ceil(n, ks), 1, L.splits), 0)
+        ln = np.where(valid, _ceil(n, np.maximum(nsp, 1)), -1)
+        lenmax = int(ln.max())
+        frm = [int(nsp[ln >= b].sum()) * per_item for b in range(lenmax + 2)]
         for bid in range(L.grid):
-            idv, sel, j = bid, -1, 0
-            lvl = 0
-            while True:
-                m = full > lvl
-                if not m.any():
-                    break
-                cnum = int(m.sum()) * per_item
-                if idv < cnum:
-                    sel = int(_nth(m, np.array([idv // per_item]))[0])
-                    j = lvl
-                    break
-                idv -= cnum
-                lvl += 1
-            if sel < 0:
-                frm = [int((last >= b).sum()) * per_item for b in range(ks + 2)]
-                if idv >= frm[0]:
-                    continue
-                lo = max(b for b in range(ks + 1) if frm[b] > idv)
-                idv -= frm[lo + 1]
-                sel = int(_nth(last == lo, np.array([idv // per_item]))[0])
-                if sel < 0:
-                    items.append(None)
-                    continue
-                j = int(full[sel])
-            if sel < 0:
+            idv = bid
+            if idv >= frm[0]:
+                continue
+            lo = max(b for b in range(lenmax + 1) if frm[b] > idv)
+            idv -= frm[lo + 1]
+            lanes = np.flatnonzero(ln == lo)
+            if len(lanes) == 0:
                 items.append(None)
                 continue
-            rem = idv % per_item
+            sel = int(lanes[0])
+            for k, l in enumerate(lanes):
+                sel = int(l)
+                c = int(nsp[l]) * per_item
+                if idv < c or k == len(lanes) - 1:
+                    break
+                idv -= c
+            j = idv // per_item
+            rem = idv - j * per_item
             kh, hg = rem % L.KV, rem // L.KV
             items.append((sel // L.tiles, sel % L.tiles, j, kh, hg, int(c0[sel]), int(ql[sel]),
-                          int(cx[sel]), ks))
+                          int(cx[sel]), ks, True))
         return items
     gunits = L.tiles * L.hgroups
     for bid in range(L.grid):
@@ -602,7 +594,7 @@ def prefill_items(L: PrefillLaunch, cu: np.ndarray, ctx_lens: np.ndarray):
         if t * TR >= qlen:
             continue
         ctx = min(max(int(ctx_lens[s]), 0), cap)
-        items.append((s, t, j, kh, hg, q0, qlen, ctx, L.ks_steps))
+        items.append((s, t, j, kh, hg, q0, qlen, ctx, L.ks_steps, False))
     return items
 
 
@@ -614,7 +606,7 @@ def prefill(W: Writes, L: PrefillLaunch, out: Buf, ws: Buf, cu: np.ndarray, ctx_
         if it is None:
             W.errors.append("prefill: a workgroup derived no tile (empty ballot)")
             continue
-        s, t, j, kh, hg, q0, qlen, ctx, ks = it
+        s, t, j, kh, hg, q0, qlen, ctx, ks, eq = it
         W.index([s], L.S, "prefill sequence")
         prefix = ctx - qlen
         rows = min(qlen - t * TR, TR)
@@ -624,8 +616,13 @@ def prefill(W: Writes, L: PrefillLaunch, out: Buf, ws: Buf, cu: np.ndarray, ctx_
         nsp = min(max(_ceil(nsteps, ks), 1), L.splits)
         if j >= nsp:
             continue
-        st0 = j * ks
-        st1 = nsteps if j == nsp - 1 else st0 + ks
+        if eq:   # near-equal parts, the first nsteps % nsp one step longer
+            base, rm = divmod(nsteps, nsp)
+            st0 = j * base + min(j, rm)
+            st1 = st0 + base + (1 if j < rm else 0)
+        else:
+            st0 = j * ks
+            st1 = nsteps if j == nsp - 1 else st0 + ks
         kbeg = st0 * KT
         kend = min(st1 * KT, nkeys)
         blk0 = kbeg // L.bs

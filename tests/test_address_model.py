@@ -324,3 +324,62 @@ def test_decode_fast_path_head_dims_64_and_256():
                 check_decode(W, 70, 4096 // bs, rng.integers(0, 4097, 70), False, h=h, kv=kv,
                              bs=bs, d=d)
     W.check()
+
+
+@pytest.mark.parametrize("case", ["cfg3", "ragged", "long_prefix", "groups_2"])
+def test_prefill_work_list_covers_every_part_once(case):
+    """The in-kernel work list (<= 64 tiles): every (sequence, tile, key part,
+    kv head, head group) is run by exactly one workgroup, and each tile's parts
+    cut its key range [0, steps) into consecutive, non-empty pieces of near
+    equal length (prefill_attention.hip prefill_item and the part bounds of
+    prefill_kernel)."""
+    rng = np.random.default_rng(7)
+    if case == "cfg3":
+        S, h, kv, q, p = 4, H, KV, [512] * 4, [0, 512, 1536, 3072]
+    elif case == "ragged":
+        S, h, kv = 5, H, KV
+        q = [int(x) for x in rng.integers(1, 700, S)]
+        p = [int(x) for x in rng.integers(0, 5000, S)]
+    elif case == "long_prefix":
+        S, h, kv, q, p = 2, H, KV, [300, 64], [30000, 9000]
+    else:
+        S, h, kv, q, p = 3, 16, 8, [200, 130, 400], [100, 2000, 700]
+    cu = np.concatenate([[0], np.cumsum(q)])
+    ctx = np.array(q) + np.array(p)
+    max_bps = int(np.ceil(ctx.max() / BS))
+    L = A.prefill_host(S, h, kv, BS, max_bps, max(q), int(ctx.max()))
+    assert L.S * L.tiles <= 64
+    items = [it for it in A.prefill_items(L, cu, ctx) if it is not None]
+    TR = 64 * L.rt
+    seen = set()
+    parts = {}
+    for s, t, j, kh, hg, q0, qlen, cx, ks, eq in items:
+        assert eq
+        key = (s, t, j, kh, hg)
+        assert key not in seen, key
+        seen.add(key)
+        rows = min(qlen - t * TR, TR)
+        nsteps = -(-max(cx - qlen + t * TR + rows, 0) // 64)
+        nsp = min(max(-(-nsteps // ks), 1), L.splits)
+        assert j < nsp
+        base, rm = divmod(nsteps, nsp)
+        st0 = j * base + min(j, rm)
+        st1 = st0 + base + (1 if j < rm else 0)
+        parts.setdefault((s, t, kh, hg), []).append((st0, st1, nsteps, nsp))
+    expected = 0
+    for s in range(S):
+        for t in range(-(-q[s] // TR)):
+            for kh in range(kv):
+                for hg in range(L.hgroups):
+                    got = sorted(parts.get((s, t, kh, hg), []))
+                    assert got, (s, t, kh, hg)
+                    nsteps, nsp = got[0][2], got[0][3]
+                    assert len(got) == nsp
+                    expected += nsp
+                    assert got[0][0] == 0 and got[-1][1] == nsteps
+                    for (a0, a1, _, _), (b0, _, _, _) in zip(got, got[1:]):
+                        assert a1 == b0
+                    lens = [b - a for a, b, _, _ in got]
+                    assert max(lens) - min(lens) <= 1
+                    assert nsteps == 0 or min(lens) >= 1
+    assert len(items) == expected
