@@ -1116,6 +1116,17 @@ __global__ __launch_bounds__(64) void decode_fast_kernel(DecodeArgs a) {
     auto before = [&](int p) -> int { return wave_sum_i(full < p ? full : p) * kvh; };
     const int maxfull = wave_max_i(full);
     int id = blockIdx.x, seq = -1;
+    {
+      // Workgroups go to the 8 XCDs round-robin (blockIdx % 8) and, within
+      // an XCD, to its 32 CUs in turn, so in longest-first order the same
+      // CUs would take the longest item of every round of 256. Every other
+      // full round is reversed within each XCD (a "snake"), so each CU's
+      // items pair long with short. Only full rounds are permuted: the map
+      // stays a bijection of [0, grid).
+      const int xcd = id & 7, pos = id >> 3, rnd = pos >> 5;
+      if ((rnd & 1) != 0 && (rnd + 1) * 256 <= (int)gridDim.x)
+        id = ((rnd * 32 + (31 - (pos & 31))) << 3) | xcd;
+    }
     if (a.kv_split > 1) {
       // The kv_split units of one pool kv head have consecutive item ids
       // (every level and bucket starts at a multiple of the unit count).

@@ -320,6 +320,12 @@ def decode_items(L: DecodeLaunch, seq_lens: np.ndarray):
                       dtype=np.int64)
     nfull = int(before[maxfull]) if S else 0
     ids = np.arange(L.grid, dtype=np.int64)
+    # blockIdx -> item id: every other full round of 256 reversed within each XCD
+    xcd, pos = ids & 7, ids >> 3
+    rnd = pos >> 5
+    snake = ((rnd & 1) == 1) & ((rnd + 1) * 256 <= L.grid)
+    ids = np.where(snake, ((rnd * 32 + (31 - (pos & 31))) << 3) | xcd, ids)
+    assert np.array_equal(np.sort(ids), np.arange(L.grid)), "not a permutation"
     if L.kv_split > 1:
         # blockIdx -> item id: the units of one pool kv head 8 blockIdx apart
         span = 8 * L.kv_split
