@@ -195,9 +195,11 @@ int64_t npd_paged_prefill_workspace_size(int64_t num_seqs, int64_t total_q,
  * Rows with p < 0 (context shorter than the chunk) get zeros. scale must be
  * positive and finite.
  * max_q_len: host-known upper bound on the chunk lengths (grid size).
- * max_context_len: host-known upper bound on context_lens; key ranges longer
- * than 1024 keys are split over up to 8 workgroups when it allows (<= 0: no
- * split). It sizes the workspace: npd_paged_prefill_workspace_size(...) bytes,
+ * head_dim 64, 128 or 256.
+ * max_context_len: host-known upper bound on context_lens; at head dims 64
+ * and 128 key ranges longer than 1024 keys are split over up to 8 workgroups
+ * when it allows (<= 0: no split; head dim 256 never splits). It sizes the
+ * workspace: npd_paged_prefill_workspace_size(...) bytes,
  * 256-byte aligned, zero-filled before first use, with the same fixed 1 MiB
  * counter region as npd_paged_attention's (every call leaves its counters at
  * zero; partials follow the region), so any stream-ordered sequence of calls
@@ -225,8 +227,8 @@ int npd_paged_prefill_attention(void* out, const void* query,
  * prefill, nanoPD/engine/model_runner.py:152-168, reads fp16 K/V). K and V
  * elements are e4m3(byte) * k_scale[kv head] (v_scale for V), converted
  * exactly to the query's type (fp16/bf16, dtype) before the MFMAs; arithmetic
- * and workspace as in npd_paged_prefill_attention. head_dim 128; caches
- * 8-byte aligned.
+ * and workspace as in npd_paged_prefill_attention. head_dim 64, 128 or
+ * 256; caches 8-byte aligned.
  */
 int npd_paged_prefill_attention_fp8(void* out, const void* query,
                                     const void* key_cache, const void* value_cache,

@@ -10,6 +10,8 @@
 // them before attending, model_runner.py:146). For an empty prefix both agree.
 //
 // MI355X design (gfx950, v_mfma_f32_16x16x32_{bf16,f16}, wave64):
+//   head dim D = 64 or 128 (prefill_kernel<.., D, ..>; 256 has its own
+//   kernel below);
 //   workgroup = 8 waves = one (sequence, kv-head, head group, 64-row query
 //   tile, key split); wave w owns one query head and 32 query rows. Two waves
 //   per SIMD, 256 VGPRs each (MFMA operands stay in VGPRs). HW = gcd(G, 4)
@@ -66,24 +68,24 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kD = 128;          // head_dim of this kernel
 constexpr int kWaves = 8;        // waves per workgroup: 2 per SIMD
 constexpr int kThreads = 64 * kWaves;
 constexpr int kPairs = kWaves / 2;   // (head, 64-row tile) pairs, two 32-row waves each
 constexpr int kWaveRows = 32;    // query rows per wave
 constexpr int kKT = 64;          // keys per step
 constexpr int kDepth = 3;        // K/V tiles in flight per workgroup
-// LDS row of the K and V tiles (elements): 72 dwords, an 8-bank shift per row,
-// so 16 rows of K read at one column and 4 rows x 32 bytes of a transposing
-// V read both hit distinct banks
-constexpr int kRow = kD + 16;
+// LDS row of the K and V tiles (elements) at head dim d: 72 dwords at 128,
+// 40 at 64 -- an 8-bank shift per row either way, so 16 rows of K read at one
+// column and 4 rows x 32 bytes of a transposing V read both hit distinct banks
+constexpr int lds_row(int d) { return d + 16; }
 constexpr int kMaxBlocksLds = 16384;  // block ids of one workgroup's key range kept in LDS (64 KB)
 constexpr int kSplitSteps = 16;       // a key range longer than this many steps is split
 constexpr int kMaxSplits = 8;
 constexpr float kTau = 8.f;           // lazy-rescale threshold, log2 units
 constexpr float kLog2e = 1.4426950408889634f;
-// partial record of one wave (32 rows of one head, one split), floats
-constexpr int kRecO = 16 * 2 * 64 * 2;   // [nb*2 + mb][half][lane][2]
+// partial record of one wave (32 rows of one head, one split) at head dim d,
+// floats: [nb*2 + mb][half][lane][2], nb < d / 16
+constexpr int rec_o(int d) { return d / 8 * 2 * 64 * 2; }
 constexpr int kRecML = 2 * 64 * 2;       // [mb][lane][m, l]
 
 struct PrefillArgs {
@@ -275,11 +277,16 @@ __device__ __forceinline__ bool prefill_item(const PrefillArgs& a, int lane, Ite
 // so gather offsets are 32-bit. kF8: the pool holds OCP e4m3 bytes; a K/V
 // chunk is 8 bytes, converted exactly to four TT pairs when copied into LDS,
 // and the per-kv-head scales go into the score scale and the output.
-template <class TT, int HW, bool kOff32, bool kF8>
+template <class TT, int D, int HW, bool kOff32, bool kF8>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
+  static_assert(D == 64 || D == 128, "head dims of this kernel");
   constexpr int RT = kPairs / HW;                      // row tiles of 64 per workgroup
   constexpr int TR = 64 * RT;                          // query rows per workgroup
   constexpr int MB = kWaveRows / 16;                   // 16-row query blocks per wave
+  constexpr int NC = D / 32;                           // head-dim chunks of QK
+  constexpr int NB = D / 16;                           // 16-dim blocks of O
+  constexpr int kRow = lds_row(D);
+  constexpr int kRecO = rec_o(D);
   __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kKT * kRow];
   __shared__ __attribute__((aligned(16))) uint16_t s_v[3][kKT * kRow];
   __shared__ int s_blk[kMaxBlocksLds];
@@ -337,7 +344,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
       if (row >= qlen) continue;
       uint16_t* op = a.out + (int64_t)(q0 + row) * a.out_stride_token + (int64_t)h * a.out_stride_head;
 #pragma unroll
-      for (int nb = 0; nb < 8; ++nb) *reinterpret_cast<u32x2*>(op + nb * 16 + g * 4) = u32x2{0, 0};
+      for (int nb = 0; nb < NB; ++nb) *reinterpret_cast<u32x2*>(op + nb * 16 + g * 4) = u32x2{0, 0};
     }
     return;
   }
@@ -352,7 +359,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   // the wave's query rows as B operands: qb[mb][c] = Q[row mb*16 + r][c*32 + 8g .. +8].
   // Rows past the chunk read its last row (their outputs are never stored):
   // unconditional loads keep the compiler's count of loads in flight exact.
-  u32x4 qb[MB][4];
+  u32x4 qb[MB][NC];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     int row = wrow0 + mb * 16 + r;
@@ -360,18 +367,21 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     const uint16_t* qp = a.q + (int64_t)(q0 + row) * a.q_stride_token +
                          (int64_t)h * a.q_stride_head + g * 8;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) qb[mb][c] = *reinterpret_cast<const u32x4*>(qp + c * 32);
+    for (int c = 0; c < NC; ++c) qb[mb][c] = *reinterpret_cast<const u32x4*>(qp + c * 32);
   }
   __syncthreads();
 
-  // K/V tile loaders: chunk tid + 512e (16 bytes) of the 64 x 256-byte tile,
-  // i.e. key (tid >> 4) + 32e, column tid & 15. Loads run kDepth steps ahead
-  // through a register ring (slot = step % kDepth): one 32 KB tile in flight
+  // K/V tile loaders: chunk tid + 512e (8 elements) of the 64-key tile, i.e.
+  // key tid / CPR + KPP * e, column chunk tid % CPR. Loads run kDepth steps
+  // ahead through a register ring (slot = step % kDepth): one tile in flight
   // per CU leaves a step waiting on memory latency.
-  constexpr int kPer = kKT * kD / 8 / kThreads;        // 2
+  constexpr int CPR = D / 8;                           // 8-element chunks per row
+  constexpr int KPP = kThreads / CPR;                  // keys per load pass
+  constexpr int kPer = kKT / KPP;                      // 2 at D 128, 1 at D 64
+  static_assert(kPer * KPP == kKT, "tile shape");
   typedef typename std::conditional<kF8, u32x2, u32x4>::type raw_t;   // 8 elements
   raw_t kst[kDepth][kPer], vst[kDepth][kPer];
-  const int col = tid & 15;
+  const int col = tid % CPR;
   // Every fetch issues the same loads, so the compiler's count of loads in
   // flight stays exact and its waits cover only the slot being used: tokens
   // past the split's range are clamped to its last key. Such keys only occur
@@ -380,29 +390,29 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   auto fetch = [&](int step, raw_t* ks, raw_t* vs) {
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
-      int tok = step * kKT + (tid >> 4) + 32 * e;
+      int tok = step * kKT + tid / CPR + KPP * e;
       tok = tok < kend ? tok : kend - 1;
       const int lb = a.bs_shift >= 0 ? tok >> a.bs_shift : tok / bs;
       const int blk = s_blk[lb - blk0];
       const int row = (blk * a.num_kv_heads + kh) * bs + (tok - lb * bs);   // < 2^31 (host check)
-      if constexpr (kF8) {   // 128-byte rows, 8-byte chunks
+      if constexpr (kF8) {   // D-byte rows, 8-byte chunks
         const char* kb = reinterpret_cast<const char*>(a.k_cache);
         const char* vb = reinterpret_cast<const char*>(a.v_cache);
         if (kOff32) {
-          const uint32_t off = (uint32_t)row * 128u + (uint32_t)col * 8u;
+          const uint32_t off = (uint32_t)row * (uint32_t)D + (uint32_t)col * 8u;
           ks[e] = *reinterpret_cast<const u32x2*>(kb + off);
           vs[e] = *reinterpret_cast<const u32x2*>(vb + off);
         } else {
-          const int64_t off = (int64_t)row * 128 + col * 8;
+          const int64_t off = (int64_t)row * D + col * 8;
           ks[e] = *reinterpret_cast<const u32x2*>(kb + off);
           vs[e] = *reinterpret_cast<const u32x2*>(vb + off);
         }
       } else if (kOff32) {
-        const uint32_t off = (uint32_t)row * 256u + (uint32_t)col * 16u;
+        const uint32_t off = (uint32_t)row * (uint32_t)(2 * D) + (uint32_t)col * 16u;
         ks[e] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(a.k_cache) + off);
         vs[e] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(a.v_cache) + off);
       } else {
-        const int64_t idx = (int64_t)row * 16 + col;
+        const int64_t idx = (int64_t)row * CPR + col;
         ks[e] = a.k_cache[idx];
         vs[e] = a.v_cache[idx];
       }
@@ -418,15 +428,15 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   auto stash = [&](int kbuf, int vbuf, const raw_t* ks, const raw_t* vs) {
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
-      const int kk = (tid >> 4) + 32 * e;
+      const int kk = tid / CPR + KPP * e;
       *reinterpret_cast<u32x4*>(&s_k[kbuf][kk * kRow + col * 8]) = pairs(ks[e]);
       *reinterpret_cast<u32x4*>(&s_v[vbuf][kk * kRow + col * 8]) = pairs(vs[e]);
     }
   };
 
-  f32x4 oacc[8][MB];   // O^T[d = nb*16 + 4g + i][q = mb*16 + r]
+  f32x4 oacc[NB][MB];   // O^T[d = nb*16 + 4g + i][q = mb*16 + r]
 #pragma unroll
-  for (int nb = 0; nb < 8; ++nb)
+  for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) oacc[nb][mb] = f32x4{0, 0, 0, 0};
   float mrow[MB], nmref[MB], lrow[MB];   // running max (log2 units), -max or 0, row sum
@@ -456,7 +466,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) sacc[n][mb] = f32x4{0, 0, 0, 0};
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < NC; ++c) {
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
         const u32x4 ka = *reinterpret_cast<const u32x4*>(&kt[(n * 16 + r) * kRow + c * 32 + g * 8]);
@@ -509,7 +519,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
         const float mnew = nd ? mxs[mb] : mrow[mb];
         const float alpha = nd ? __builtin_amdgcn_exp2f(mrow[mb] - mnew) : 1.f;
 #pragma unroll
-        for (int nb = 0; nb < 8; ++nb) oacc[nb][mb] *= alpha;
+        for (int nb = 0; nb < NB; ++nb) oacc[nb][mb] *= alpha;
         lrow[mb] *= alpha;
         mrow[mb] = mnew;
         nmref[mb] = mnew == -INFINITY ? 0.f : -mnew;
@@ -538,7 +548,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     // dims nb*16 + 4*(r%4) .. +3, and receives dim nb*16 + r of keys +0..3
     const uint16_t* vlane = s_v[vbuf] + (g * 4 + (r >> 2)) * kRow + 4 * (r & 3);
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
+    for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
       for (int kc = 0; kc < 2; ++kc) {
         const u32x2 lo = lds_read_tr(vlane + (kc * 32) * kRow + nb * 16);
@@ -555,17 +565,17 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   // previous step first, then QK -> softmax, so that one wave's softmax (VALU)
   // runs while the other's MFMAs do. K tiles use two LDS buffers; V tiles
   // three, because group B still reads step j - 1's V in step j.
-  // Register ring slot D holds this step's tile (already in LDS); it is
-  // refilled with step + kDepth, and slot D + 1 (the next step's tile) is
+  // Register ring slot SL holds this step's tile (already in LDS); it is
+  // refilled with step + kDepth, and slot SL + 1 (the next step's tile) is
   // copied into LDS at the end of the step.
   const bool late = wave >= kWaves / 2;
   u32x4 pb[2][MB];
   bool pending = false;   // group B: pb holds the P of a step whose PV is due
   auto step_body = [&](int step, auto slot) {
-    constexpr int D = decltype(slot)::value;
-    constexpr int DN = (D + 1) % kDepth;
+    constexpr int SL = decltype(slot)::value;
+    constexpr int SN = (SL + 1) % kDepth;
     const int rel = step - st0;
-    fetch(step + kDepth, kst[D], vst[D]);   // past st1: clamped, never used
+    fetch(step + kDepth, kst[SL], vst[SL]);   // past st1: clamped, never used
     // some row of the wave sees a key here (always so with one row tile)
     const bool active = RT == 1 || step * kKT <= wpos0 + kWaveRows - 1;
     if (!late) {
@@ -587,7 +597,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     // before that step's barrier. Written even after the last step (nobody
     // reads it then): an unconditional copy keeps the compiler's load
     // accounting exact on every path.
-    stash((rel + 1) & 1, (rel + 1) % 3, kst[DN], vst[DN]);
+    stash((rel + 1) & 1, (rel + 1) % 3, kst[SN], vst[SN]);
     __syncthreads();
   };
   // full rounds of the ring in the loop; the 0-2 remaining steps after it, so
@@ -615,7 +625,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     {
       float* po = a.part_o + (rec + j) * kRecO + lane * 2;
 #pragma unroll
-      for (int nb = 0; nb < 8; ++nb)
+      for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
           const int idx = nb * MB + mb;
@@ -651,7 +661,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
       }
       const float* po = a.part_o + (rec + jj) * kRecO + lane * 2;
 #pragma unroll
-      for (int nb = 0; nb < 8; ++nb)
+      for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
           const int idx = nb * MB + mb;
@@ -673,7 +683,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     const float inv = (l > 0.f && wpos0 + mb * 16 + r >= 0) ? oscale / l : 0.f;
     uint16_t* op = a.out + (int64_t)(q0 + row) * a.out_stride_token + (int64_t)h * a.out_stride_head;
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
+    for (int nb = 0; nb < NB; ++nb) {
       const f32x4 o = oacc[nb][mb];
       u32x2 w;
       w.x = TT::pack2(o[0] * inv, o[1] * inv);
@@ -683,7 +693,8 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   }
 }
 
-// Head dims other than 128 (64 and 256). One workgroup of 4 waves per
+// Head dim 256 (the tiles and register ring of prefill_kernel would need
+// about 174 KB of LDS and 336 VGPRs at this D). One workgroup of 4 waves per
 // (sequence, query head, 64-row query tile); wave w owns query rows
 // 16w .. 16w + 15 of the tile. Per step of 64 keys the workgroup copies the kv
 // head's K and V rows into LDS (keys past the visible range clamped to the
@@ -696,12 +707,11 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 //                      the transposing LDS read, P^T from the S^T layout).
 // The operand layouts, the P packing and the normalisation (the row sum adds
 // the rounded P values) are those of prefill_kernel. No key splits and no
-// GQA sharing of the K/V tile: these head dims are served correctly, not
-// tuned. Rows with no visible key are written as zeros.
+// GQA sharing of the K/V tile. Rows with no visible key are written as zeros.
 template <class TT, int D, bool kF8>
 __global__ __launch_bounds__(256) void prefill_generic_kernel(PrefillArgs a) {
   constexpr int kGT = 256;                      // threads
-  constexpr int RW = D + (D == 64 ? 8 : 16);    // LDS row (elements); 16-byte multiple
+  constexpr int RW = D + 16;                    // LDS row (elements); 16-byte multiple
   constexpr int CPR = D / 8;                    // 8-element chunks per K/V row
   constexpr int KPP = kGT / CPR;                // keys per load pass
   constexpr int NPASS = kKT / KPP;
@@ -850,33 +860,31 @@ __global__ __launch_bounds__(256) void prefill_generic_kernel(PrefillArgs a) {
 }
 
 template <class TT, bool kF8>
-int launch_generic(int64_t head_dim, const PrefillArgs& a, int64_t grid, hipStream_t st,
-                   const char* name) {
-  if (head_dim == 64)
-    hipLaunchKernelGGL((prefill_generic_kernel<TT, 64, kF8>), dim3((unsigned)grid), dim3(256), 0,
-                       st, a);
-  else
-    hipLaunchKernelGGL((prefill_generic_kernel<TT, 256, kF8>), dim3((unsigned)grid), dim3(256), 0,
-                       st, a);
+int launch_generic(const PrefillArgs& a, int64_t grid, hipStream_t st, const char* name) {
+  hipLaunchKernelGGL((prefill_generic_kernel<TT, 256, kF8>), dim3((unsigned)grid), dim3(256), 0,
+                     st, a);
   return npd::check_launch(name);
 }
 
-template <class TT, bool kOff32, bool kF8>
+template <class TT, int D, bool kOff32, bool kF8>
 int launch(int hw, const PrefillArgs& a, int64_t grid, hipStream_t st, const char* name) {
   switch (hw) {
-    case 1: hipLaunchKernelGGL((prefill_kernel<TT, 1, kOff32, kF8>), dim3((unsigned)grid), dim3(kThreads), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((prefill_kernel<TT, 2, kOff32, kF8>), dim3((unsigned)grid), dim3(kThreads), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((prefill_kernel<TT, 4, kOff32, kF8>), dim3((unsigned)grid), dim3(kThreads), 0, st, a); break;
+    case 1: hipLaunchKernelGGL((prefill_kernel<TT, D, 1, kOff32, kF8>), dim3((unsigned)grid), dim3(kThreads), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((prefill_kernel<TT, D, 2, kOff32, kF8>), dim3((unsigned)grid), dim3(kThreads), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((prefill_kernel<TT, D, 4, kOff32, kF8>), dim3((unsigned)grid), dim3(kThreads), 0, st, a); break;
     default: return npd::fail(NPD_E_INVALID, "%s: heads per workgroup %d", name, hw);
   }
   return npd::check_launch(name);
 }
 
 template <class TT, bool kF8>
-int launch_dt(bool off32, int hw, const PrefillArgs& a, int64_t grid, hipStream_t st,
-              const char* name) {
-  return off32 ? launch<TT, true, kF8>(hw, a, grid, st, name)
-               : launch<TT, false, kF8>(hw, a, grid, st, name);
+int launch_dt(int64_t head_dim, bool off32, int hw, const PrefillArgs& a, int64_t grid,
+              hipStream_t st, const char* name) {
+  if (head_dim == 64)
+    return off32 ? launch<TT, 64, true, kF8>(hw, a, grid, st, name)
+                 : launch<TT, 64, false, kF8>(hw, a, grid, st, name);
+  return off32 ? launch<TT, 128, true, kF8>(hw, a, grid, st, name)
+               : launch<TT, 128, false, kF8>(hw, a, grid, st, name);
 }
 
 // Workspace: [counter region (kCounterBytes) | O partials | (m, l) partials].
@@ -888,7 +896,8 @@ struct Layout {
   int64_t o_off, ml_off, total;
 };
 
-Layout prefill_layout(int64_t num_seqs, int64_t num_heads, int64_t max_q_len, int64_t max_context_len) {
+Layout prefill_layout(int64_t num_seqs, int64_t num_heads, int64_t head_dim, int64_t max_q_len,
+                      int64_t max_context_len) {
   Layout L{1, kSplitSteps, 0, 0, 0};
   if (max_context_len > 0) {
     // splits of kSplitSteps steps, longer ones when that would exceed kMaxSplits
@@ -906,7 +915,7 @@ Layout prefill_layout(int64_t num_seqs, int64_t num_heads, int64_t max_q_len, in
   const int64_t units = num_seqs * t32 * num_heads;
   const int64_t nrec = units * L.splits;
   L.o_off = npd::kCounterBytes;
-  L.ml_off = L.o_off + nrec * kRecO * 4;
+  L.ml_off = L.o_off + nrec * rec_o((int)head_dim) * 4;
   L.total = L.ml_off + nrec * kRecML * 4;
   return L;
 }
@@ -917,8 +926,9 @@ extern "C" int64_t npd_paged_prefill_workspace_size(int64_t num_seqs, int64_t to
                                                     int64_t num_heads, int64_t head_dim,
                                                     int64_t max_q_len, int64_t max_context_len) {
   (void)total_q;
-  if (head_dim != kD) return 0;   // the head dims of prefill_generic_kernel need no workspace
-  return prefill_layout(num_seqs, num_heads, max_q_len, max_context_len).total;
+  // head dim 256 (prefill_generic_kernel) needs no workspace
+  if (head_dim != 64 && head_dim != 128) return 0;
+  return prefill_layout(num_seqs, num_heads, head_dim, max_q_len, max_context_len).total;
 }
 
 namespace {
@@ -941,7 +951,7 @@ int prefill_impl(void* out, const void* query, const void* key_cache, const void
   if (num_seqs < 0 || total_q < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_blocks <= 0 ||
       block_size <= 0 || max_blocks_per_seq <= 0 || max_q_len < 0)
     return fail(NPD_E_INVALID, "%s: bad sizes", name);
-  if (head_dim != 64 && head_dim != kD && head_dim != 256)
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
     return fail(NPD_E_INVALID, "%s: head_dim %lld not in {64, 128, 256}", name,
                 (long long)head_dim);
   if (num_heads % num_kv_heads != 0)
@@ -951,7 +961,7 @@ int prefill_impl(void* out, const void* query, const void* key_cache, const void
   const int hw = (g % 4 == 0) ? 4 : (g % 2 == 0 ? 2 : 1);   // gcd(g, 4)
   if (num_blocks * block_size * num_kv_heads > INT32_MAX || max_blocks_per_seq * block_size > INT32_MAX)
     return fail(NPD_E_INVALID, "%s: pool exceeds int32 row indexing", name);
-  if (head_dim == kD && max_blocks_per_seq > kMaxBlocksLds)
+  if (head_dim != 256 && max_blocks_per_seq > kMaxBlocksLds)
     return fail(NPD_E_INVALID, "%s: block tables wider than %d blocks are not supported", name,
                 kMaxBlocksLds);
   if (q_stride_token % 8 || q_stride_head % 8 || out_stride_token % 4 || out_stride_head % 4 ||
@@ -970,7 +980,7 @@ int prefill_impl(void* out, const void* query, const void* key_cache, const void
       (reinterpret_cast<uintptr_t>(out) & 7u) != 0)
     return fail(NPD_E_ALIGN, "%s: query pointer must be 16-byte aligned, caches %d-byte, out 8-byte",
                 name, fp8 ? 8 : 16);
-  if (head_dim != kD) {
+  if (head_dim == 256) {
     const int64_t tiles = (max_q_len + 63) / 64;
     const int64_t grid = num_seqs * tiles * num_heads;
     if (grid > INT32_MAX) return fail(NPD_E_INVALID, "%s: too many tiles", name);
@@ -999,12 +1009,12 @@ int prefill_impl(void* out, const void* query, const void* key_cache, const void
     a.out_stride_head = out_stride_head;
     hipStream_t st = as_stream(stream);
     if (dtype == NPD_DTYPE_BF16)
-      return fp8 ? launch_generic<BF16, true>(head_dim, a, grid, st, name)
-                 : launch_generic<BF16, false>(head_dim, a, grid, st, name);
-    return fp8 ? launch_generic<F16, true>(head_dim, a, grid, st, name)
-               : launch_generic<F16, false>(head_dim, a, grid, st, name);
+      return fp8 ? launch_generic<BF16, true>(a, grid, st, name)
+                 : launch_generic<BF16, false>(a, grid, st, name);
+    return fp8 ? launch_generic<F16, true>(a, grid, st, name)
+               : launch_generic<F16, false>(a, grid, st, name);
   }
-  const Layout L = prefill_layout(num_seqs, num_heads, max_q_len, max_context_len);
+  const Layout L = prefill_layout(num_seqs, num_heads, head_dim, max_q_len, max_context_len);
   if (L.total > 0) {
     if (!workspace || workspace_bytes < L.total)
       return fail(NPD_E_WORKSPACE, "%s: workspace of %lld bytes needed, %lld given", name,
@@ -1059,10 +1069,10 @@ int prefill_impl(void* out, const void* query, const void* key_cache, const void
   const int64_t elt = fp8 ? 1 : 2;
   const bool off32 = num_blocks * num_kv_heads * block_size * head_dim * elt <= (int64_t)UINT32_MAX;
   if (dtype == NPD_DTYPE_BF16)
-    return fp8 ? launch_dt<BF16, true>(off32, hw, a, grid, st, name)
-               : launch_dt<BF16, false>(off32, hw, a, grid, st, name);
-  return fp8 ? launch_dt<F16, true>(off32, hw, a, grid, st, name)
-             : launch_dt<F16, false>(off32, hw, a, grid, st, name);
+    return fp8 ? launch_dt<BF16, true>(head_dim, off32, hw, a, grid, st, name)
+               : launch_dt<BF16, false>(head_dim, off32, hw, a, grid, st, name);
+  return fp8 ? launch_dt<F16, true>(head_dim, off32, hw, a, grid, st, name)
+             : launch_dt<F16, false>(head_dim, off32, hw, a, grid, st, name);
 }
 
 }  // namespace

@@ -53,8 +53,12 @@ KT = 64
 SPLIT_STEPS = 16
 MAX_SPLITS = 8
 MAX_BLOCKS_LDS = 16384
-REC_O = 16 * 2 * 64 * 2
 REC_ML = 2 * 64 * 2
+
+
+def rec_o(d: int) -> int:
+    """Floats of one wave's partial O record at head dim d (rec_o)."""
+    return d // 8 * 2 * 64 * 2
 WAVE_ROWS = 32
 
 
@@ -497,8 +501,11 @@ class PrefillLaunch:
     num_cus: int = 256
 
 
-def prefill_host(S, H, KV, bs, max_bps, max_q_len, max_ctx, num_cus=256) -> PrefillLaunch:
-    """prefill_layout and prefill_impl (prefill_attention.hip:686-851)."""
+def prefill_host(S, H, KV, bs, max_bps, max_q_len, max_ctx, num_cus=256,
+                 D: int = 128) -> PrefillLaunch:
+    """prefill_layout and prefill_impl (prefill_attention.hip), head dims 64
+    and 128 (prefill_kernel)."""
+    assert D in (64, 128)
     L = PrefillLaunch(S, H, KV, bs, max_bps, max_q_len, max_ctx, num_cus=num_cus)
     g = H // KV
     L.hw = 4 if g % 4 == 0 else (2 if g % 2 == 0 else 1)
@@ -513,7 +520,7 @@ def prefill_host(S, H, KV, bs, max_bps, max_q_len, max_ctx, num_cus=256) -> Pref
         t32 = _ceil(max_q_len, WAVE_ROWS) + 7
         nrec = S * t32 * H * L.splits
         L.o_off = K_COUNTER_BYTES
-        L.ml_off = L.o_off + nrec * REC_O * 4
+        L.ml_off = L.o_off + nrec * rec_o(D) * 4
         L.total = L.ml_off + nrec * REC_ML * 4
     L.rt = 4 // L.hw
     L.tiles = _ceil(max_q_len, 64 * L.rt)
@@ -650,8 +657,8 @@ def prefill(W: Writes, L: PrefillLaunch, out: Buf, ws: Buf, cu: np.ndarray, ctx_
             rec = ((s * L.subtiles + wsub) * L.H + h) * L.splits
             W.index([wsub], L.subtiles, "prefill subtile")
             for jj in (j, 0, nsp - 1):
-                o = L.o_off + (rec + jj) * REC_O * 4
-                W.add(ws, o, o + REC_O * 4, "prefill partial O")
+                o = L.o_off + (rec + jj) * rec_o(D) * 4
+                W.add(ws, o, o + rec_o(D) * 4, "prefill partial O")
                 o = L.ml_off + (rec + jj) * REC_ML * 4
                 W.add(ws, o, o + REC_ML * 4, "prefill partial (m, l)")
             cidx = ((s * L.tiles + t) * L.KV + kh) * L.hgroups + hg
@@ -662,7 +669,7 @@ def prefill_generic(W: Writes, S: int, H: int, KV: int, bs: int, max_bps: int, n
                     max_q_len: int, out: Buf, cu: np.ndarray, ctx_lens: np.ndarray,
                     out_stride_token: int, out_stride_head: int, tables: np.ndarray,
                     D: int) -> None:
-    """prefill_generic_kernel (head dims 64 / 256): one workgroup per
+    """prefill_generic_kernel (head dim 256): one workgroup per
     (sequence, head, 64-row tile); every K/V row it reads and every output
     row it writes."""
     tiles = _ceil(max_q_len, 64)

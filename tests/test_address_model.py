@@ -278,11 +278,12 @@ def test_planted_mistakes_are_reported():
 
 def test_head_dims_64_and_256():
     """The fused prologue (two rows per wave at D 64, two rotate-half pairs
-    per lane at D 256) and the generic prefill kernel of those head dims:
-    every K/V row read and every store inside its buffer, over ragged chunks
-    on paged prefixes, an empty chunk, a chunk longer than its context (rows
-    before position 0) and block tables at their full width; a planted wrong
-    row stride is caught."""
+    per lane at D 256) and prefill at those head dims (prefill_kernel at 64,
+    with its partials in the workspace the library sizes; the generic kernel
+    at 256): every K/V row read and every store inside its buffer, over
+    ragged chunks on paged prefixes, an empty chunk, a chunk longer than its
+    context (rows before position 0) and block tables at their full width; a
+    planted wrong row stride is caught."""
     rng = np.random.default_rng(64)
     for d in (64, 256):
         W = A.Writes()
@@ -299,12 +300,24 @@ def test_head_dims_64_and_256():
         mb = 100
         ctx = np.array([1300, 1, 0, mb * bs, 20])   # full-width table; 64 rows on 20 keys
         tables = np.stack([rng.permutation(nblk)[:mb] for _ in q]).astype(np.int64)
-        A.prefill_generic(W, len(q), h, kv, bs, mb, nblk, int(q.max()),
-                          A.Buf("out", int(cu[-1]) * h * d * 2), cu, ctx, h * d, d, tables, d)
-        W.check()
-        bad = A.Writes()   # planted: output rows addressed with twice the row stride
-        A.prefill_generic(bad, len(q), h, kv, bs, mb, nblk, int(q.max()),
-                          A.Buf("out", int(cu[-1]) * h * d * 2), cu, ctx, 2 * h * d, d, tables, d)
+        out = A.Buf("out", int(cu[-1]) * h * d * 2)
+        if d == 64:
+            mctx = int(ctx.max())
+            L = A.prefill_host(len(q), h, kv, bs, mb, int(q.max()), mctx, D=d)
+            ws_bytes = int(_lib.load().npd_paged_prefill_workspace_size(
+                len(q), int(cu[-1]), h, d, int(q.max()), mctx))
+            assert ws_bytes == L.total > 0
+            A.prefill(W, L, out, A.Buf("ws", ws_bytes), cu, ctx, h * d, d, D=d)
+            W.check()
+            bad = A.Writes()   # planted: output rows addressed with twice the row stride
+            A.prefill(bad, L, out, A.Buf("ws", ws_bytes), cu, ctx, 2 * h * d, d, D=d)
+        else:
+            A.prefill_generic(W, len(q), h, kv, bs, mb, nblk, int(q.max()), out, cu, ctx, h * d,
+                              d, tables, d)
+            W.check()
+            bad = A.Writes()   # planted: output rows addressed with twice the row stride
+            A.prefill_generic(bad, len(q), h, kv, bs, mb, nblk, int(q.max()), out, cu, ctx,
+                              2 * h * d, d, tables, d)
         with pytest.raises(A.OutOfBounds):
             bad.check()
 

@@ -169,16 +169,19 @@ def test_prefill_workspace_size():
     assert lib.npd_paged_prefill_workspace_size(4, 2048, 32, 128, 512, 0) == 0
     # longer ranges are split (at most 8 ways): the 1 MiB counter region, then
     # per (sequence, row subtile of 32, head, split) an O record of 32 rows x
-    # 128 fp32 and an (m, l) record of 32 rows x 2 x 4 lanes
-    def split(S, H, max_q, splits):
+    # D fp32 and an (m, l) record of 32 rows x 2 x 4 lanes
+    def split(S, H, max_q, splits, D=128):
         t32 = (max_q + 31) // 32 + 7
         units = S * t32 * H
-        return 2**20 + units * splits * (16384 + 1024)
+        return 2**20 + units * splits * (32 * D * 4 + 1024)
     assert lib.npd_paged_prefill_workspace_size(4, 2048, 32, 128, 512, 3584) == split(4, 32, 512, 4)
     assert lib.npd_paged_prefill_workspace_size(1, 100, 32, 128, 100, 1025) == split(1, 32, 100, 2)
     assert lib.npd_paged_prefill_workspace_size(2, 1024, 32, 128, 512, 32768) == split(2, 32, 512, 8)
-    # head dims 64 and 256 run unsplit (prefill_generic_kernel): no workspace
-    assert lib.npd_paged_prefill_workspace_size(4, 2048, 32, 64, 512, 3584) == 0
+    # head dim 64 runs the same kernel with half-size O records
+    assert lib.npd_paged_prefill_workspace_size(4, 2048, 32, 64, 512, 3584) == \
+        split(4, 32, 512, 4, D=64)
+    assert lib.npd_paged_prefill_workspace_size(4, 2048, 32, 64, 512, 1024) == 0
+    # head dim 256 runs unsplit (prefill_generic_kernel): no workspace
     assert lib.npd_paged_prefill_workspace_size(2, 1024, 32, 256, 512, 32768) == 0
 
 

@@ -229,8 +229,9 @@ def test_prefill_group_sizes(device, dtype, G):
 @pytest.mark.parametrize("hd", [64, 256])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_prefill_head_dims_64_and_256(device, hd, dtype):
-    """Head dims 64 and 256 over an FP8 pool (prefill_generic_kernel): empty
-    and paged prefixes, ragged chunks, a decode row."""
+    """Head dims 64 (prefill_kernel, the 1700-key range in key splits) and
+    256 (prefill_generic_kernel) over an FP8 pool: empty and paged prefixes,
+    ragged chunks, a decode row."""
     case = _fp8_prefill_case(device, [0, 100, 1500, 77], [64, 37, 200, 1], 8, 2, dtype,
                              seed=hd, D=hd)
     _prefill_run_and_check(device, *case, dtype)

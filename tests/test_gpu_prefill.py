@@ -157,15 +157,17 @@ def test_config3_store_then_prefill_and_decode(device):
     assert err <= ATOL[torch.bfloat16]
 
 
+@pytest.mark.parametrize("hd", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_key_splits_match_whole_ranges(device, dtype):
+def test_key_splits_match_whole_ranges(device, dtype, hd):
     """Long prefixes are cut into key splits merged by the last split to
     arrive; splitting off (max_context_len=0) runs every range whole. Both
-    agree with the oracle and with each other."""
-    args = make_case(device, [3000, 1100, 0, 5000], [200, 64, 130, 33], dtype=dtype, seed=21)
+    agree with the oracle and with each other (head dims 64 and 128)."""
+    args = make_case(device, [3000, 1100, 0, 5000], [200, 64, 130, 33], D=hd, dtype=dtype,
+                     seed=21)
     q, kc, vc, bt, cu, ctx, mb, mq = args
-    scale = 1 / math.sqrt(128)
-    assert pk.prefill_workspace_bytes(4, int(q.size(0)), 32, 128, mq, mb * 16) > 0
+    scale = 1 / math.sqrt(hd)
+    assert pk.prefill_workspace_bytes(4, int(q.size(0)), 32, hd, mq, mb * 16) > 0
     split = run(*args, scale)
     whole = torch.full_like(q, float("nan"))
     pk.paged_prefill_attention(whole, q, kc, vc, bt, cu, ctx, scale, 16, mb, mq, max_context_len=0)
@@ -206,9 +208,9 @@ def test_workspace_reuse_and_explicit_workspace(device):
     ([0, 512, 2000, 99], [300, 128, 1, 1], 6, 1, 16),
 ])
 def test_head_dims_64_and_256(device, hd, dtype, prefixes, chunks, G, kvh, bs):
-    """Head dims 64 and 256 (prefill_generic_kernel): empty and paged
-    prefixes, ragged chunks and decode rows in one call, group sizes 1-6,
-    block sizes 8-32."""
+    """Head dims 64 (prefill_kernel) and 256 (prefill_generic_kernel): empty
+    and paged prefixes, ragged chunks and decode rows in one call, group
+    sizes 1-6, block sizes 8-32."""
     print(f"prefill D={hd} {dtype} prefixes={prefixes} chunks={chunks} G={G} kvh={kvh} bs={bs}",
           flush=True)
     args = make_case(device, prefixes, chunks, H=G * kvh, kvh=kvh, D=hd, bs=bs, dtype=dtype,
