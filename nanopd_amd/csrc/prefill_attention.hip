@@ -503,9 +503,10 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     }
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
-      float mx = fmaxf(v[mb][0], fmaxf(v[mb][1], v[mb][2]));
+      // a chain of three-operand maxima (v_max3_f32: two values per instruction)
+      float mx = fmaxf(fmaxf(v[mb][0], v[mb][1]), v[mb][2]);
 #pragma unroll
-      for (int e = 3; e < 15; e += 2) mx = fmaxf(mx, fmaxf(v[mb][e], v[mb][e + 1]));
+      for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, v[mb][e]), v[mb][e + 1]);
       mx = row_max4(fmaxf(mx, v[mb][15]));
       mxs[mb] = mx * c2;
       need = need || (mxs[mb] > mrow[mb] + kTau);
