@@ -707,10 +707,13 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 //   O^T += V^T . P^T  (D/16 blocks of 16 dims x 2 chunks of 32 keys; V^T via
 //                      the transposing LDS read, P^T from the S^T layout).
 // The operand layouts, the P packing and the normalisation (the row sum adds
-// the rounded P values) are those of prefill_kernel. No key splits and no
-// GQA sharing of the K/V tile. Rows with no visible key are written as zeros.
+// the rounded P values) are those of prefill_kernel. The next step's K/V
+// chunks load into registers during the step (two workgroups per CU at 254
+// VGPRs); the workgroups of one (sequence, kv head) share K/V through one
+// XCD's L2 rather than one LDS tile, and there are no key splits. Rows with no
+// visible key are written as zeros.
 template <class TT, int D, bool kF8>
-__global__ __launch_bounds__(256) void prefill_generic_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(256, 2) void prefill_generic_kernel(PrefillArgs a) {
   constexpr int kGT = 256;                      // threads
   constexpr int RW = D + 16;                    // LDS row (elements); 16-byte multiple
   constexpr int CPR = D / 8;                    // 8-element chunks per K/V row
@@ -725,15 +728,41 @@ __global__ __launch_bounds__(256) void prefill_generic_kernel(PrefillArgs a) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, r = lane & 15;
-  const int H = a.num_kv_heads * a.group;
-  const int h = (int)(blockIdx.x % (unsigned)H);
-  const int st = (int)(blockIdx.x / (unsigned)H);
-  const int s = st / a.tiles_max, t = st - (st / a.tiles_max) * a.tiles_max;
-  if (s >= a.num_seqs) return;
+  // Every workgroup of one (sequence, kv head) reads the same keys from 0 up:
+  // they all run on one XCD (workgroups go to XCDs round-robin by blockIdx),
+  // one after another in that XCD's order, so the K/V rows come from its L2
+  // after the first read. Groups go longest context first (up to 64
+  // sequences; more keep their order); within a group the last tile (the
+  // most keys) first, the group's query heads of a tile together.
+  const int per = a.tiles_max * a.group;        // workgroups per (sequence, kv head)
+  const int xcd = (int)(blockIdx.x & 7u), p = (int)(blockIdx.x >> 3);
+  const int gi = (p / per) * 8 + xcd;           // (sequence rank, kv head) index
+  if (gi >= a.num_seqs * a.num_kv_heads) return;
+  const int u = p - (p / per) * per;
+  const int rank = gi / a.num_kv_heads;
+  const int t = a.tiles_max - 1 - u / a.group;
+  const int h = (gi - rank * a.num_kv_heads) * a.group + (u - (u / a.group) * a.group);
+  const int cap = a.max_bps * a.block_size;
+  int s = rank;
+  if (a.num_seqs <= 64) {
+    // lane i stands for sequence i; its rank counts the sequences with a
+    // longer context (ties: the lower index first)
+    int n = -1;
+    if (lane < a.num_seqs) {
+      n = a.context_lens[lane];
+      n = n < 0 ? 0 : (n < cap ? n : cap);
+    }
+    int rk = 0;
+    for (int i = 0; i < a.num_seqs; ++i) {
+      const int ni = __builtin_amdgcn_readlane(n, i);
+      rk += (ni > n || (ni == n && i < lane)) ? 1 : 0;
+    }
+    const uint64_t m = __ballot(lane < a.num_seqs && rk == rank);
+    s = __builtin_amdgcn_readfirstlane(__builtin_ctzll(m));
+  }
   const int q0 = a.cu_seqlens_q[s];
   const int qlen = a.cu_seqlens_q[s + 1] - q0;
   if (t * 64 >= qlen) return;
-  const int cap = a.max_bps * a.block_size;
   int ctx = a.context_lens[s];
   ctx = ctx < 0 ? 0 : (ctx < cap ? ctx : cap);
   const int kh = h / a.group;
@@ -761,37 +790,50 @@ __global__ __launch_bounds__(256) void prefill_generic_kernel(PrefillArgs a) {
   const float c2 = kF8 ? a.scale_log2 * a.k_scale[kh] : a.scale_log2;
   const float oscale = kF8 ? a.v_scale[kh] : 1.f;
 
-  for (int step = 0; step < nsteps; ++step) {
-    __syncthreads();   // every wave is done with the previous tile
+  // K/V of the step's tile: raw chunks loaded into registers one step ahead
+  // (in flight during the previous step's MFMAs), converted and copied into
+  // LDS at the step's start. Keys past the visible range are clamped to the
+  // last visible key (a real, finite row; the causal mask removes them).
+  typedef typename std::conditional<kF8, u32x2, u32x4>::type raw_t;   // 8 elements
+  raw_t kr[NPASS], vr[NPASS];
+  const int col = tid - (tid / CPR) * CPR;
+  auto fetch = [&](int step) {
 #pragma unroll
     for (int e = 0; e < NPASS; ++e) {
-      const int kk = tid / CPR + KPP * e;
-      const int col = tid - (tid / CPR) * CPR;
-      int tok = step * kKT + kk;
+      int tok = step * kKT + tid / CPR + KPP * e;
       tok = tok < nkeys ? tok : nkeys - 1;
       const int lb = a.bs_shift >= 0 ? tok >> a.bs_shift : tok / bs;
       int blk = a.block_tables[(int64_t)s * a.max_bps + lb];
       blk = blk < 0 ? 0 : (blk >= a.num_blocks ? a.num_blocks - 1 : blk);
       const int64_t ri = ((int64_t)blk * a.num_kv_heads + kh) * bs + (tok - lb * bs);
-      u32x4 kw, vw;
       if constexpr (kF8) {   // D-byte rows, 8-byte chunks
-        const char* kb = reinterpret_cast<const char*>(a.k_cache);
-        const char* vb = reinterpret_cast<const char*>(a.v_cache);
-        const u32x2 k8 = *reinterpret_cast<const u32x2*>(kb + ri * D + col * 8);
-        const u32x2 v8 = *reinterpret_cast<const u32x2*>(vb + ri * D + col * 8);
-        kw = u32x4{npd::e4m3x2_to<TT, false>(k8.x), npd::e4m3x2_to<TT, true>(k8.x),
-                   npd::e4m3x2_to<TT, false>(k8.y), npd::e4m3x2_to<TT, true>(k8.y)};
-        vw = u32x4{npd::e4m3x2_to<TT, false>(v8.x), npd::e4m3x2_to<TT, true>(v8.x),
-                   npd::e4m3x2_to<TT, false>(v8.y), npd::e4m3x2_to<TT, true>(v8.y)};
+        kr[e] = *reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(a.k_cache) + ri * D + col * 8);
+        vr[e] = *reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(a.v_cache) + ri * D + col * 8);
       } else {
         const int64_t idx = ri * CPR + col;   // 16-byte units
-        kw = a.k_cache[idx];
-        vw = a.v_cache[idx];
+        kr[e] = a.k_cache[idx];
+        vr[e] = a.v_cache[idx];
       }
-      *reinterpret_cast<u32x4*>(&s_k[kk * RW + col * 8]) = kw;
-      *reinterpret_cast<u32x4*>(&s_v[kk * RW + col * 8]) = vw;
+    }
+  };
+  auto pairs = [](raw_t w) -> u32x4 {
+    if constexpr (kF8)
+      return u32x4{npd::e4m3x2_to<TT, false>(w.x), npd::e4m3x2_to<TT, true>(w.x),
+                   npd::e4m3x2_to<TT, false>(w.y), npd::e4m3x2_to<TT, true>(w.y)};
+    else
+      return w;
+  };
+  if (nsteps > 0) fetch(0);
+  for (int step = 0; step < nsteps; ++step) {
+    __syncthreads();   // every wave is done with the previous tile
+#pragma unroll
+    for (int e = 0; e < NPASS; ++e) {
+      const int kk = tid / CPR + KPP * e;
+      *reinterpret_cast<u32x4*>(&s_k[kk * RW + col * 8]) = pairs(kr[e]);
+      *reinterpret_cast<u32x4*>(&s_v[kk * RW + col * 8]) = pairs(vr[e]);
     }
     __syncthreads();
+    if (step + 1 < nsteps) fetch(step + 1);
 
     // S^T[key n*16 + 4g + i][query r]
     f32x4 sacc[4];
@@ -983,7 +1025,7 @@ int prefill_impl(void* out, const void* query, const void* key_cache, const void
                 name, fp8 ? 8 : 16);
   if (head_dim == 256) {
     const int64_t tiles = (max_q_len + 63) / 64;
-    const int64_t grid = num_seqs * tiles * num_heads;
+    const int64_t grid = (num_seqs * num_kv_heads + 7) / 8 * 8 * tiles * g;
     if (grid > INT32_MAX) return fail(NPD_E_INVALID, "%s: too many tiles", name);
     PrefillArgs a{};
     a.out = static_cast<uint16_t*>(out);

@@ -665,20 +665,45 @@ def prefill(W: Writes, L: PrefillLaunch, out: Buf, ws: Buf, cu: np.ndarray, ctx_
             W.index([cidx], K_MAX_COUNTERS, "prefill merge counter")
 
 
+def prefill_generic_units(S: int, H: int, KV: int, max_q_len: int, ctx_lens, cap: int):
+    """(blockIdx, sequence, tile, head) of every workgroup of
+    prefill_generic_kernel's grid that does not exit at once (prefill_attention.hip, the blockIdx
+    mapping of prefill_generic_kernel and its grid in prefill_impl). Up to 64
+    sequences go longest context first (ties: lower index first)."""
+    tiles = _ceil(max_q_len, 64)
+    G = H // KV
+    per = tiles * G
+    grid = _ceil(S * KV, 8) * 8 * per
+    if S <= 64:
+        n = [min(max(int(c), 0), cap) for c in ctx_lens[:S]]
+        order = sorted(range(S), key=lambda i: (-n[i], i))
+    else:
+        order = list(range(S))
+    out = []
+    for bid in range(grid):
+        xcd, p = bid & 7, bid >> 3
+        gi = (p // per) * 8 + xcd
+        if gi >= S * KV:
+            continue
+        u = p % per
+        s = order[gi // KV]
+        t = tiles - 1 - u // G
+        h = (gi % KV) * G + u % G
+        out.append((bid, s, t, h))
+    return out
+
+
 def prefill_generic(W: Writes, S: int, H: int, KV: int, bs: int, max_bps: int, num_blocks: int,
                     max_q_len: int, out: Buf, cu: np.ndarray, ctx_lens: np.ndarray,
                     out_stride_token: int, out_stride_head: int, tables: np.ndarray,
                     D: int) -> None:
     """prefill_generic_kernel (head dim 256): one workgroup per
-    (sequence, head, 64-row tile); every K/V row it reads and every output
-    row it writes."""
+    (sequence, head, 64-row tile), grouped by (sequence, kv head) on one XCD;
+    every K/V row it reads and every output row it writes."""
     tiles = _ceil(max_q_len, 64)
     cap = max_bps * bs
     G = H // KV
-    for bid in range(S * tiles * H):
-        h = bid % H
-        st = bid // H
-        s, t = st // tiles, st % tiles
+    for _, s, t, h in prefill_generic_units(S, H, KV, max_q_len, ctx_lens, cap):
         q0 = int(cu[s])
         qlen = int(cu[s + 1]) - q0
         if t * 64 >= qlen:

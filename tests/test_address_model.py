@@ -322,6 +322,35 @@ def test_head_dims_64_and_256():
             bad.check()
 
 
+@pytest.mark.parametrize("S,H,KV,mq", [(4, 32, 8, 512), (3, 12, 2, 130), (5, 6, 1, 64),
+                                        (1, 16, 16, 700), (64, 8, 2, 65), (70, 4, 4, 64)])
+def test_prefill_generic_grid_covers_every_tile_once(S, H, KV, mq):
+    """Head dim 256: the XCD-grouped grid of prefill_generic_kernel runs every
+    (sequence, 64-row tile, query head) exactly once (tied and clamped
+    contexts included), the workgroups of one (sequence, kv head) all go to
+    one XCD, and up to 64 sequences start longest context first."""
+    rng = np.random.default_rng(S * 100 + H)
+    cap = 4096
+    ctx = rng.integers(-5, 5000, size=S)
+    ctx[: S // 3] = ctx[0]                       # ties
+    units = A.prefill_generic_units(S, H, KV, mq, ctx, cap)
+    tiles = -(-mq // 64)
+    assert sorted(u[1:] for u in units) == \
+        [(s, t, h) for s in range(S) for t in range(tiles) for h in range(H)]
+    assert len({u[0] for u in units}) == len(units)
+    xcds = {}
+    for bid, s, t, h in units:   # blockIdx % 8 is the XCD
+        xcds.setdefault((s, h // (H // KV)), set()).add(bid % 8)
+    assert all(len(x) == 1 for x in xcds.values())
+    if S <= 64:   # first workgroup of each sequence in grid order: by clamped context, descending
+        first = {}
+        for bid, s, t, h in units:
+            first.setdefault(s, bid)
+        key = np.clip(ctx, 0, cap)
+        by_start = sorted(first, key=lambda s: first[s])
+        assert [int(key[s]) for s in by_start] == sorted((int(k) for k in key), reverse=True)
+
+
 def test_decode_fast_path_head_dims_64_and_256():
     """The fast path at head dims 64 and 256 (block sizes 16 and 32): output,
     partial, group-slot and counter stores inside the workspace the library
