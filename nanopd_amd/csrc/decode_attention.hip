@@ -21,8 +21,12 @@
 //           combined with shuffles at the end.
 // A sequence that fits in one partition writes its output directly; longer
 // ones write fp32 partials (acc, max, sum) and merge_partitions_kernel
-// combines them (log-sum-exp merge). No MFMA: at one query row per sequence
-// the op is HBM-bound.
+// combines them (log-sum-exp merge). 2-byte pools use no MFMA: at one query
+// row per sequence the op is HBM-bound. FP8 pools move half the bytes with
+// twice the conversions per byte, so their passes 1 and 3 stage each 16-token
+// step's converted K / V rows in LDS and run S = Q.K^T and O^T += V^T.P^T on
+// v_mfma_f32_16x16x16 (the G heads padded to 16): no reduce-scatter and no
+// per-element products on the VALU.
 #include <type_traits>
 
 #include "common.h"
@@ -32,6 +36,43 @@ namespace {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+// O^T += V^T . P^T of FP8 pools' pass 3 on v_mfma_f32_16x16x16_{bf16,f16}:
+// A[m = lane%16][k = 4*(lane/16) + e], B[k = 4*(lane/16) + e][n = lane%16],
+// D[m = 4*(lane/16) + i][n = lane%16].
+template <class TT>
+struct Mfma16;
+template <>
+struct Mfma16<npd::BF16> {
+  static __device__ __forceinline__ f32x4 mma(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                     __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma16<npd::F16> {
+  static __device__ __forceinline__ f32x4 mma(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
+                                                 __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+  }
+};
+// ds_read_b64_tr_b16 on an LDS address given as a generic pointer to LDS: in
+// a group of 16 lanes, lane j receives element j%4 of the 8-byte chunks
+// addressed by lanes 4e + j/4, e = 0..3
+__device__ __forceinline__ u32x2 lds_read_tr(const uint16_t* p) {
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p)));
+}
+// LDS row (elements) of the 16-token V tile that FP8 pools' pass 3 stages: an
+// 8-bank shift per row, so the 4 rows x 32 bytes of a transposing read hit
+// distinct banks
+constexpr int kVRow = 128 + 16;
+// LDS row (elements) of the 16-token K tile of FP8 pools' pass 1: a 4-bank
+// shift per row, so the 16 rows x 8 bytes that 16 lanes read at one column
+// (and the two column groups of 32 lanes) hit distinct banks
+constexpr int kKRow = 128 + 8;
 
 constexpr int kMaxPartition = 512;   // tokens per partition, upper bound (LDS sizing)
 constexpr int kStep = 16;            // tokens per step
@@ -632,6 +673,17 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int64_t slo
   }
 }
 
+// Floats of the fast path's score region for t tokens (incl. ring padding):
+// FP8 pools' pass 3 stages its 16 x kVRow V tile there.
+__host__ __device__ constexpr int fast_score_floats(int t, int gp, bool fp8) {
+  return fp8 && t * gp < 16 * kVRow / 2 ? 16 * kVRow / 2 : t * gp;
+}
+// Bytes of FP8 pools' probability region ([GP][t] 2-byte values): pass 1
+// stages its 16 x kKRow K tile there first.
+__host__ __device__ constexpr int fast_prob_bytes(int t, int gp) {
+  return t * gp * 2 < 16 * kKRow * 2 ? 16 * kKRow * 2 : t * gp * 2;
+}
+
 // Element source of the fast path. 2-byte pools: a lane's 8 elements are one
 // 16-byte load, used as 4 packed pairs. FP8 pools (kF8): 8 e4m3 bytes, one
 // 8-byte load (the same index arithmetic in 8-byte units, a head row being 128
@@ -660,7 +712,8 @@ struct KvSrc<TT, true> {
 
 template <class TT, int D, int G, int SPB, bool kF8 = false>
 __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, int part,
-                                                 int ps, float* s_p, uint32_t* s_pp) {
+                                                 int ps, float* s_p, uint16_t* s_pb,
+                                                 uint16_t* s_v) {
   typedef KvSrc<TT, kF8> Src;
   typedef typename Src::raw raw_t;
   static_assert(D == 64 || D == 128 || D == 256, "head dims of the fast path");
@@ -679,9 +732,11 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
   constexpr int NTS = NH > LGP ? NH - LGP : 0;   // token bits split by stages
   constexpr int BS = 16 * SPB;
   constexpr int NBUF = ring_of(D);      // steps in flight per pass
-  // pass 3 on packed 2-byte probabilities with v_dot2 (FP8 pools: their short
-  // partitions leave LDS room for the packed copy), else on the fp32 ones
-  constexpr bool kDot2 = kF8;
+  // pass 3 on the matrix cores for FP8 pools (2-byte probabilities, V staged
+  // in LDS as TT; their short partitions leave LDS room for both), else on
+  // the VALU with fp32 probabilities
+  constexpr bool kMma = kF8;
+  const int tmax = a.partition + 16 * NBUF;   // row of s_pb: tokens incl. ring padding
   constexpr int MAXT = kFastMaxPartition + 16 * NBUF;   // tokens incl. ring padding
 
   (void)MAXT;
@@ -720,9 +775,10 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
 #pragma unroll
   for (int t = 0; t < NTS; ++t) tokhi |= stage_coord<D>(j, LGP + t) << (NLB - 1 - t);
 
-  // q slot h holds head h ^ headmask of the group (zeros for padding heads)
+  // q slot h holds head h ^ headmask of the group (zeros for padding heads;
+  // VALU pass 1 only)
   u32x4 qv[GP];
-  {
+  if constexpr (!kF8) {
     const uint16_t* qb = a.q + s * a.q_stride_seq + (kh * G) * a.q_stride_head + j * 8;
 #pragma unroll
     for (int h = 0; h < GP; ++h) {
@@ -770,7 +826,46 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
 
   // ---------------- pass 1: scores ----------------
   float runmax = -INFINITY;   // max of the scores this lane stored (its head: headmask)
+  // FP8 pools: S = Q . K^T on the matrix cores. A = Q[head n16][dims c*16 +
+  // 4*g4 .. +3] (zeros past the group), B = K^T from the step's K rows staged
+  // in LDS (row = token of the step), D[head 4*g4 + i][token n16]: each lane
+  // ends with the scores of 4 heads of one token, no reduce-scatter.
+  const int g4 = lane >> 4, n16 = lane & 15;
+  constexpr int NQC = kMma ? D / 16 : 1;
+  u32x2 qa[NQC];
+  float runmax4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};   // heads 4*g4 + i
+  if constexpr (kMma) {
+    const uint16_t* qrow = a.q + s * a.q_stride_seq + (kh * G + n16) * a.q_stride_head + 4 * g4;
+#pragma unroll
+    for (int c = 0; c < NQC; ++c)
+      qa[c] = n16 < G ? *reinterpret_cast<const u32x2*>(qrow + c * 16) : u32x2{0, 0};
+  }
+  uint16_t* s_k = s_pb;   // pass 1's K tile (the probabilities come later)
+  auto score_step_mma = [&](const raw_t* kraw, int st) {
+#pragma unroll
+    for (int i = 0; i < NL; ++i)
+      *reinterpret_cast<u32x4*>(&s_k[(i * TPL + r) * kKRow + j * 8]) = Src::pairs(kraw[i]);
+    f32x4 sacc = f32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < NQC; ++c)
+      sacc = Mfma16<TT>::mma(qa[c], *reinterpret_cast<const u32x2*>(&s_k[n16 * kKRow + c * 16 + 4 * g4]),
+                             sacc);
+    const int tl = st * 16 + n16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * g4 + i;
+      if (h < G) {
+        // rows past the context may hold anything: select, not scale
+        const float sv = (tl < ntok) ? sacc[i] * score_scale : -INFINITY;
+        s_p[tl * GP + h] = sv;
+        runmax4[i] = fmaxf(runmax4[i], sv);
+      }
+    }
+  };
   auto score_step = [&](const raw_t* kraw, int st) {
+    if constexpr (kMma) {
+      score_step_mma(kraw, st);
+    } else {
     float v[NV];   // v[h * NL + i]: q slot h . token slot i
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
@@ -801,6 +896,7 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
         s_p[tl * GP + h] = sv;
         runmax = fmaxf(runmax, sv);
       }
+    }
     }
   };
   {
@@ -833,22 +929,22 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
   float m[GP], l[GP];
 #pragma unroll
   for (int h = 0; h < GP; ++h) {
-    m[h] = h < G ? wave_max_f(headmask == h ? runmax : -INFINITY) : -INFINITY;
+    if constexpr (kMma)
+      m[h] = h < G ? wave_max_f(g4 == h / 4 ? runmax4[h % 4] : -INFINITY) : -INFINITY;
+    else
+      m[h] = h < G ? wave_max_f(headmask == h ? runmax : -INFINITY) : -INFINITY;
     l[h] = 0.f;
   }
   const int ntl = nsteps * 16;
-  if constexpr (kDot2) {
-  // Probabilities of the token pair (8q + rr, 8q + 4 + rr) of each step, packed
-  // as two 2-byte values per head: the pair a pass-3 lane multiplies into one
-  // v_dot2 with V. l sums the rounded values, so the normalisation matches them.
-  for (int pi = lane; pi < ntl / 2; pi += 64) {
-    const int ta = (pi >> 3) * 16 + ((pi >> 2) & 1) * 8 + (pi & 3), tb = ta + 4;
+  if constexpr (kMma) {
+  // 2-byte probabilities, head-major (s_pb[h * tmax + t]): the B operand of
+  // pass 3's MFMAs. l sums the rounded values, so the normalisation matches.
+  for (int t = lane; t < ntl; t += 64) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      const uint32_t ua = TT::from_float(__builtin_amdgcn_exp2f(s_p[ta * GP + h] - m[h]));
-      const uint32_t ub = TT::from_float(__builtin_amdgcn_exp2f(s_p[tb * GP + h] - m[h]));
-      l[h] += TT::lo(ua) + TT::lo(ub);
-      s_pp[pi * GP + h] = ua | (ub << 16);
+      const uint32_t u = TT::from_float(__builtin_amdgcn_exp2f(s_p[t * GP + h] - m[h]));
+      l[h] += TT::lo(u);
+      s_pb[h * tmax + t] = (uint16_t)u;
     }
   }
   } else {
@@ -871,6 +967,10 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
   for (int h = 0; h < G; ++h)
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[h][d] = 0.f;
+  constexpr int NOB = kMma ? D / 16 : 1;   // 16-dim blocks of O^T (MFMA path)
+  f32x4 oacc[NOB];
+#pragma unroll
+  for (int nb = 0; nb < NOB; ++nb) oacc[nb] = f32x4{0, 0, 0, 0};
   auto pv_step = [&](const raw_t* vraw, int st) {
     u32x4 vbuf[NL];
 #pragma unroll
@@ -880,37 +980,19 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
       for (int i = 0; i < NL; ++i)
         if (st * 16 + i * TPL + r >= ntok) vbuf[i] = u32x4{0, 0, 0, 0};
     }
-  if constexpr (kDot2) {
-    // slots 2q and 2q+1 hold tokens 8q + r and 8q + 4 + r: pack their values
-    // per dim (v_perm) and take both products with one v_dot2
+  if constexpr (kMma) {
+    // the step's 16 rows into LDS (row = token of the step, TT elements)
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      uint32_t pp[GP];
-      const uint32_t* src = &s_pp[(st * 8 + q * 4 + r) * GP];
-      if constexpr (GP >= 4) {
+    for (int i = 0; i < NL; ++i)
+      *reinterpret_cast<u32x4*>(&s_v[(i * TPL + r) * kVRow + j * 8]) = vbuf[i];
+    // B: probabilities of tokens st*16 + 4*g4 .. +3 for head n16 (0 past the group)
+    u32x2 pbv = u32x2{0, 0};
+    if (n16 < G) pbv = *reinterpret_cast<const u32x2*>(&s_pb[n16 * tmax + st * 16 + 4 * g4]);
+    // A: V^T[dim nb*16 + n16][tokens 4*g4 .. +3] by transposing reads (lane
+    // (g4, n16) addresses token 4*g4 + n16/4, dims nb*16 + 4*(n16%4) .. +3)
+    const uint16_t* vl = s_v + (g4 * 4 + (n16 >> 2)) * kVRow + 4 * (n16 & 3);
 #pragma unroll
-        for (int h4 = 0; h4 < GP; h4 += 4) {
-          const u32x4 t4 = *reinterpret_cast<const u32x4*>(src + h4);
-          pp[h4] = t4.x; pp[h4 + 1] = t4.y; pp[h4 + 2] = t4.z; pp[h4 + 3] = t4.w;
-        }
-      } else {
-#pragma unroll
-        for (int h = 0; h < GP; ++h) pp[h] = src[h];
-      }
-      const uint32_t wa[4] = {vbuf[2 * q].x, vbuf[2 * q].y, vbuf[2 * q].z, vbuf[2 * q].w};
-      const uint32_t wb[4] = {vbuf[2 * q + 1].x, vbuf[2 * q + 1].y, vbuf[2 * q + 1].z,
-                              vbuf[2 * q + 1].w};
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const uint32_t lo = __builtin_amdgcn_perm(wb[c], wa[c], 0x05040100u);
-        const uint32_t hi = __builtin_amdgcn_perm(wb[c], wa[c], 0x07060302u);
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-          acc[h][2 * c] = TT::dot2(lo, pp[h], acc[h][2 * c]);
-          acc[h][2 * c + 1] = TT::dot2(hi, pp[h], acc[h][2 * c + 1]);
-        }
-      }
-    }
+    for (int nb = 0; nb < NOB; ++nb) oacc[nb] = Mfma16<TT>::mma(lds_read_tr(vl + nb * 16), pbv, oacc[nb]);
   } else {
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
@@ -952,6 +1034,23 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
 #pragma unroll
     for (int b = 0; b < NBUF; ++b) pv_step(vb[b], st0 + b);
   }
+  if constexpr (kMma) {
+    // O^T blocks (lane (g4, n16): dims nb*16 + 4*g4 .. +3 of head n16) ->
+    // acc[h][8] of dims j*8 .. +7 in every row of the wave, through LDS (the
+    // staged V tile is no longer read: G x D floats <= its 16 x kVRow x 2 bytes)
+    float* s_o = reinterpret_cast<float*>(s_v);
+    if (n16 < G) {
+#pragma unroll
+      for (int nb = 0; nb < NOB; ++nb) *reinterpret_cast<f32x4*>(&s_o[n16 * D + nb * 16 + 4 * g4]) = oacc[nb];
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const f32x4 lo = *reinterpret_cast<const f32x4*>(&s_o[h * D + j * 8]);
+      const f32x4 hi = *reinterpret_cast<const f32x4*>(&s_o[h * D + j * 8 + 4]);
+      acc[h][0] = lo.x; acc[h][1] = lo.y; acc[h][2] = lo.z; acc[h][3] = lo.w;
+      acc[h][4] = hi.x; acc[h][5] = hi.y; acc[h][6] = hi.z; acc[h][7] = hi.w;
+    }
+  } else {
   // sum over the TPL rows of the wave (lanes equal in j): lane ^ 8 by DPP
   // (D 64), then the gfx950 row swaps: v_permlane16_swap / v_permlane32_swap
   // with both operands x hand every lane {x, x of lane ^ 16} (^ 32) in some
@@ -971,6 +1070,7 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
                                                         false, false);
       acc[h][d] = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
     }
+  }
 
   if (nparts == 1) {
     if (lane < LPT) {
@@ -1064,12 +1164,19 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
 // workgroups past the list (all at the end of the grid) exit at once.
 // LDS is dynamic, sized for the launch's partition (fast_lds_bytes).
 template <class TT, int D, int G, int SPB, bool kF8>
-__global__ __launch_bounds__(64) void decode_fast_kernel(DecodeArgs a) {
+// FP8 pools with up to 4 heads per group: at most 128 VGPRs, four waves per
+// SIMD (the MFMA pass 3 would otherwise take the kernel to 148)
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kF8 && G <= 4 ? 4 : 1)))
+void decode_fast_kernel(DecodeArgs a) {
   constexpr int GP = pow2ceil(G);
   extern __shared__ __attribute__((aligned(16))) float s_dyn[];
   float* s_p = s_dyn;   // [partition + ring padding][GP] scores
-  uint32_t* s_pp =   // [(partition + ring padding) / 2][GP] packed probabilities (kDot2)
-      kF8 ? reinterpret_cast<uint32_t*>(s_dyn + (a.partition + 16 * ring_of(D)) * GP) : nullptr;
+  // FP8 pools: [GP][partition + ring padding] 2-byte probabilities after the
+  // scores; pass 3's [16][kVRow] V tile reuses the scores' region (no longer
+  // read once the probabilities are out), which is sized to hold it
+  const int tpad = a.partition + 16 * ring_of(D);
+  uint16_t* s_pb = kF8 ? reinterpret_cast<uint16_t*>(s_dyn + fast_score_floats(tpad, GP, kF8)) : nullptr;
+  uint16_t* s_v = kF8 ? reinterpret_cast<uint16_t*>(s_dyn) : nullptr;
   int unit, part, ps = a.partition;
   if (a.num_seqs <= kInlineSchedMax) {
     // Small batch: every workgroup derives its item from seq_lens alone, in
@@ -1174,7 +1281,7 @@ __global__ __launch_bounds__(64) void decode_fast_kernel(DecodeArgs a) {
     unit = it.x;
     part = it.y;
   }
-  decode_fast_item<TT, D, G, SPB, kF8>(a, unit, part, ps, s_p, s_pp);
+  decode_fast_item<TT, D, G, SPB, kF8>(a, unit, part, ps, s_p, s_pb, s_v);
 }
 
 // Builds the work list of decode_fast_kernel (one workgroup):
@@ -1336,12 +1443,14 @@ int64_t fast_grid(const DecodeArgs& a, int64_t units) {
 }
 
 // Dynamic LDS of decode_fast_kernel for a partition: scores (fp32) of every
-// token of the partition plus the ring padding, and their packed bf16/fp16
-// probabilities when pass 3 uses v_dot2 (FP8 pools).
+// token of the partition plus the ring padding (for FP8 pools at least the
+// 16-row V tile of pass 3's MFMAs, which reuses that region), then for FP8
+// pools the 2-byte probabilities (at least pass 1's 16-row K tile, which
+// reuses that region).
 int64_t fast_lds_bytes(int partition, int g, bool fp8, int d) {
-  const int64_t t = partition + 16 * ring_of(d);
-  const int64_t gp = pow2ceil(g);
-  return t * gp * 4 + (fp8 ? t / 2 * gp * 4 : 0);
+  const int t = partition + 16 * ring_of(d);
+  const int gp = pow2ceil(g);
+  return (int64_t)fast_score_floats(t, gp, fp8) * 4 + (fp8 ? fast_prob_bytes(t, gp) : 0);
 }
 
 template <class TT, int D, int G, int SPB, bool kF8 = false>

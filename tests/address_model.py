@@ -44,6 +44,22 @@ MERGE_GROUP = 16
 RING = 2
 
 
+V_ROW = 128 + 16   # elements per row of the FP8 pass-3 V tile in LDS (kVRow)
+
+
+K_ROW = 128 + 8    # elements per row of the FP8 pass-1 K tile in LDS (kKRow)
+
+
+def fast_prob_bytes(t: int, gp: int) -> int:
+    """fast_prob_bytes: the FP8 probability region, at least the K tile."""
+    return 16 * K_ROW * 2 if t * gp * 2 < 16 * K_ROW * 2 else t * gp * 2
+
+
+def fast_score_floats(t: int, gp: int, fp8: bool) -> int:
+    """fast_score_floats: the score region, at least the FP8 V tile."""
+    return 16 * V_ROW // 2 if fp8 and t * gp < 16 * V_ROW // 2 else t * gp
+
+
 def ring_of(D: int) -> int:
     """decode_attention.hip ring_of: steps in flight per pass."""
     return 2 * RING if D == 64 else RING
@@ -273,7 +289,7 @@ def decode_host(S, H, KV, bs, max_bps, fp8, D=128) -> DecodeLaunch:
     L.grid = n
     gp = pow2ceil(G)
     t = L.partition + 16 * ring_of(D)
-    L.lds_floats = t * gp + (t // 2 * gp if fp8 else 0)
+    L.lds_floats = fast_score_floats(t, gp, fp8) + (fast_prob_bytes(t, gp) // 4 if fp8 else 0)
     return L
 
 
@@ -415,15 +431,26 @@ def decode(W: Writes, L: DecodeLaunch, out: Buf, ws: Buf, seq_lens: np.ndarray,
         pass   # such items return at once (decode_attention.hip:646)
     single = run & (nparts == 1)
     out_rows(single, "decode output rows")
-    # LDS of the item's passes: scores s_p[tl * GP + h], packed s_pp[pi * GP + h]
+    # LDS of the item's passes: scores s_p[tl * GP + h]; FP8 pools: 2-byte
+    # probabilities s_pb[h * tpad + tl] and pass 3's V tile / O exchange
     ntok = np.minimum(ctx - part * ps, ps)   # ps: per item
     ring = ring_of(D)
     nsteps = _ceil(_ceil(np.maximum(ntok, 0), 16), ring) * ring
     if run.any():
         W.index(nsteps[run] * 16 * gp - 1, L.partition * gp + 16 * ring * gp, "decode LDS scores")
         if L.fp8:
-            W.index((L.partition + 16 * ring) * gp + nsteps[run] * 8 * gp - 1, L.lds_floats,
-                    "decode LDS packed probabilities")
+            tpad = L.partition + 16 * ring
+            pb0 = fast_score_floats(tpad, gp, True) * 4   # bytes
+            W.index(pb0 + 2 * ((L.G - 1) * tpad + nsteps[run] * 16 - 1) + 1, L.lds_floats * 4,
+                    "decode LDS probabilities (bytes)")
+            # pass 1's K tile reuses the probability region
+            W.index([pb0 + 2 * (15 * K_ROW + 127) + 1], L.lds_floats * 4,
+                    "decode LDS K tile in the probability region (bytes)")
+            W.index([2 * (15 * K_ROW + 127) + 1], fast_prob_bytes(tpad, gp),
+                    "decode K tile within the probability region (bytes)")
+            # the V tile and the O exchange reuse the score region
+            W.index([2 * (15 * V_ROW + 127) + 1, 4 * L.G * D - 1], pb0,
+                    "decode LDS V tile / O exchange in the score region (bytes)")
         nb = _ceil(ntok[run], L.bs)
         W.index(nb - 1, 128, "decode block ids per lane")
         # block-table reads of the partition
