@@ -56,6 +56,24 @@ def check(out, q, kc, vc, bt, sl, scale):
     return err
 
 
+@pytest.mark.parametrize("D,bs", [(64, 16), (128, 16), (128, 32), (256, 16), (128, 8)])
+def test_nan_rows_past_the_context(device, D, bs):
+    """Rows of a sequence's last block past its context hold NaN: the kernels
+    mask those tokens' scores by selection and zero their V rows, so the
+    output is finite and equals the oracle's over the context (fast path at
+    head dims 64 / 128 / 256, block sizes 16 and 32; the generic path at block
+    size 8)."""
+    lens = [1, 17, 300, 777, 5, 40]
+    q, kc, vc, bt, sl, scale, mb = make_inputs(len(lens), 12, 3, D, lens, bs, torch.bfloat16,
+                                               device, seed=D + bs)
+    for i, n in enumerate(lens):
+        if n % bs:
+            b = int(bt[i, (n - 1) // bs])
+            kc[b, :, n % bs:, :] = float("nan")
+            vc[b, :, n % bs:, :] = float("nan")
+    check(run(q, kc, vc, bt, sl, scale, mb, bs), q, kc, vc, bt, sl, scale)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_single_seq_single_head(device, dtype):
     args = make_inputs(1, 1, 1, 64, [8], 16, dtype, device)

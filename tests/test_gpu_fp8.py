@@ -96,6 +96,24 @@ def test_decode_group_sizes(device, dtype, G):
     _run_and_check(device, *args, 16, dtype)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("G", [3, 5])
+def test_decode_nan_rows_past_the_context(device, dtype, G):
+    """Rows of a sequence's last block past its context hold e4m3 NaN codes
+    (0x7F / 0xFF): the scores of those tokens are selected out and their V
+    rows zeroed before the products, so the output stays finite and equal to
+    the oracle's over the context alone (odd group sizes: padded head slots)."""
+    kvh, bs = 2, 16
+    q, kc, vc, bt, sl, ks, vs, mb = _fp8_case(device, [1, 17, 300, 777, 5, 40], G * kvh, kvh, bs,
+                                              dtype, seed=100 + G)
+    for i, n in enumerate(sl.tolist()):
+        if n % bs:
+            b = int(bt[i, (n - 1) // bs])
+            kc[b, :, n % bs:, :] = 0x7F
+            vc[b, :, n % bs:, :] = 0xFF
+    _run_and_check(device, q, kc, vc, bt, sl, ks, vs, mb, bs, dtype)
+
+
 @pytest.mark.parametrize("bs", [16, 32])
 def test_decode_block_sizes_and_long_context(device, bs):
     args = _fp8_case(device, [4097, 64, 2500], 32, 8, bs, torch.bfloat16, seed=bs)

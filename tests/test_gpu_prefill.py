@@ -220,6 +220,23 @@ def test_head_dims_64_and_256(device, hd, dtype, prefixes, chunks, G, kvh, bs):
     check(run(*args, scale), q, kc, vc, bt, cu, ctx, scale)
 
 
+@pytest.mark.parametrize("hd", [64, 128, 256])
+def test_nan_rows_past_the_context(device, hd):
+    """Rows of a sequence's last block past its context hold NaN: keys past
+    the visible range are clamped to the last visible key, so those rows are
+    never read and the output equals the oracle's (key splits included at
+    head dims 64 and 128)."""
+    prefixes, chunks, bs = [3000, 0, 700, 5], [200, 37, 130, 1], 16
+    q, kc, vc, bt, cu, ctx, mb, mq = make_case(device, prefixes, chunks, D=hd, bs=bs, seed=hd + 5)
+    for i, n in enumerate(ctx.tolist()):
+        if n % bs:
+            b = int(bt[i, (n - 1) // bs])
+            kc[b, :, n % bs:, :] = float("nan")
+            vc[b, :, n % bs:, :] = float("nan")
+    scale = 1 / math.sqrt(hd)
+    check(run(q, kc, vc, bt, cu, ctx, mb, mq, scale), q, kc, vc, bt, cu, ctx, scale)
+
+
 @pytest.mark.parametrize("hd", [64, 256])
 def test_head_dims_64_and_256_zero_rows_and_decode(device, hd):
     """Rows before position 0 are zeros; the last row of a chunk equals a
