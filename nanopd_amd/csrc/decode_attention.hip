@@ -21,8 +21,11 @@
 //           combined with shuffles at the end.
 // A sequence that fits in one partition writes its output directly; longer
 // ones write fp32 partials (acc, max, sum) and merge_partitions_kernel
-// combines them (log-sum-exp merge). 2-byte pools use no MFMA: at one query
-// row per sequence the op is HBM-bound. FP8 pools move half the bytes with
+// combines them (log-sum-exp merge). 2-byte pools with up to 4 heads per
+// group use no MFMA: at one query row per sequence the op is HBM-bound; with
+// 5-8 heads pass 3's fp32 products no longer keep up, and it runs on
+// v_mfma_f32_16x16x16 as below (the probabilities rounded to the pool type in
+// place). FP8 pools move half the bytes with
 // twice the conversions per byte, so their passes 1 and 3 stage each 16-token
 // step's converted K / V rows in LDS and run S = Q.K^T and O^T += V^T.P^T on
 // v_mfma_f32_16x16x16 (the G heads padded to 16): no reduce-scatter and no
@@ -673,10 +676,18 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int64_t slo
   }
 }
 
+// Head-group sizes from which 2-byte pools (head dim 128) run pass 3 on the
+// matrix cores: below it the fp32 VALU products keep up with HBM.
+constexpr int kMmaPvMinG = 5;
+__host__ __device__ constexpr bool mma_pv_2byte(int d, int g) { return d == 128 && g >= kMmaPvMinG; }
 // Floats of the fast path's score region for t tokens (incl. ring padding):
-// FP8 pools' pass 3 stages its 16 x kVRow V tile there.
-__host__ __device__ constexpr int fast_score_floats(int t, int gp, bool fp8) {
-  return fp8 && t * gp < 16 * kVRow / 2 ? 16 * kVRow / 2 : t * gp;
+// FP8 pools' pass 3 stages its 16 x kVRow V tile there; 2-byte pools with an
+// MFMA pass 3 keep their 2-byte probabilities in its first half and the V
+// tile after them.
+__host__ __device__ constexpr int fast_score_floats(int t, int gp, bool fp8, bool mma_pv = false) {
+  return fp8 ? (t * gp < 16 * kVRow / 2 ? 16 * kVRow / 2 : t * gp)
+             : mma_pv ? (t * gp < t * gp / 2 + 16 * kVRow / 2 ? t * gp / 2 + 16 * kVRow / 2 : t * gp)
+                      : t * gp;
 }
 // Bytes of FP8 pools' probability region ([GP][t] 2-byte values): pass 1
 // stages its 16 x kKRow K tile there first.
@@ -736,6 +747,11 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
   // in LDS as TT; their short partitions leave LDS room for both), else on
   // the VALU with fp32 probabilities
   constexpr bool kMma = kF8;
+  // 2-byte pools with large groups: pass 3 on the matrix cores too, with the
+  // probabilities rounded to TT in place (token-major pairs in the first half
+  // of the score region) and the V tile after them
+  constexpr bool kMmaPv2 = !kF8 && mma_pv_2byte(D, G);
+  constexpr bool kMmaPv = kMma || kMmaPv2;
   const int tmax = a.partition + 16 * NBUF;   // row of s_pb: tokens incl. ring padding
   constexpr int MAXT = kFastMaxPartition + 16 * NBUF;   // tokens incl. ring padding
 
@@ -947,6 +963,31 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
       s_pb[h * tmax + t] = (uint16_t)u;
     }
   }
+  } else if constexpr (kMmaPv2) {
+  // probabilities rounded to TT, token-major pairs written in place: the word
+  // t * GP/2 + k holds heads 2k, 2k + 1 of token t. A word lands on the
+  // scores of token (t * GP/2 + k) / GP <= t/2, which every lane has read
+  // before (this iteration's reads precede its writes; the compiler barrier
+  // keeps them so). l sums the rounded values.
+  for (int t0 = 0; t0 < ntl; t0 += 64) {
+    const int t = t0 + lane;
+    uint32_t u[GP];
+#pragma unroll
+    for (int h = 0; h < GP; ++h) u[h] = 0u;
+    if (t < ntl) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        u[h] = TT::from_float(__builtin_amdgcn_exp2f(s_p[t * GP + h] - m[h]));
+        l[h] += TT::lo(u[h]);
+      }
+    }
+    asm volatile("" ::: "memory");
+    if (t < ntl) {
+#pragma unroll
+      for (int k = 0; k < GP / 2; ++k) s_p[t * (GP / 2) + k] = __uint_as_float(u[2 * k] | (u[2 * k + 1] << 16));
+    }
+    asm volatile("" ::: "memory");
+  }
   } else {
   for (int t = lane; t < ntl; t += 64) {
 #pragma unroll
@@ -967,7 +1008,10 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
   for (int h = 0; h < G; ++h)
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[h][d] = 0.f;
-  constexpr int NOB = kMma ? D / 16 : 1;   // 16-dim blocks of O^T (MFMA path)
+  constexpr int NOB = kMmaPv ? D / 16 : 1;   // 16-dim blocks of O^T (MFMA path)
+  // V tile of an MFMA pass 3 (FP8: s_v; 2-byte pools: after the in-place
+  // probabilities, tmax * GP/2 floats into the score region)
+  uint16_t* s_vt = kMmaPv2 ? reinterpret_cast<uint16_t*>(s_p + tmax * (GP / 2)) : s_v;
   f32x4 oacc[NOB];
 #pragma unroll
   for (int nb = 0; nb < NOB; ++nb) oacc[nb] = f32x4{0, 0, 0, 0};
@@ -980,17 +1024,29 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
       for (int i = 0; i < NL; ++i)
         if (st * 16 + i * TPL + r >= ntok) vbuf[i] = u32x4{0, 0, 0, 0};
     }
-  if constexpr (kMma) {
+  if constexpr (kMmaPv) {
     // the step's 16 rows into LDS (row = token of the step, TT elements)
 #pragma unroll
     for (int i = 0; i < NL; ++i)
-      *reinterpret_cast<u32x4*>(&s_v[(i * TPL + r) * kVRow + j * 8]) = vbuf[i];
+      *reinterpret_cast<u32x4*>(&s_vt[(i * TPL + r) * kVRow + j * 8]) = vbuf[i];
     // B: probabilities of tokens st*16 + 4*g4 .. +3 for head n16 (0 past the group)
     u32x2 pbv = u32x2{0, 0};
-    if (n16 < G) pbv = *reinterpret_cast<const u32x2*>(&s_pb[n16 * tmax + st * 16 + 4 * g4]);
+    if constexpr (kMma) {
+      if (n16 < G) pbv = *reinterpret_cast<const u32x2*>(&s_pb[n16 * tmax + st * 16 + 4 * g4]);
+    } else {
+      if (n16 < G) {
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t pr = __float_as_uint(s_p[(st * 16 + 4 * g4 + e) * (GP / 2) + (n16 >> 1)]);
+          w[e] = (n16 & 1) ? (pr >> 16) : (pr & 0xffffu);
+        }
+        pbv = u32x2{w[0] | (w[1] << 16), w[2] | (w[3] << 16)};
+      }
+    }
     // A: V^T[dim nb*16 + n16][tokens 4*g4 .. +3] by transposing reads (lane
     // (g4, n16) addresses token 4*g4 + n16/4, dims nb*16 + 4*(n16%4) .. +3)
-    const uint16_t* vl = s_v + (g4 * 4 + (n16 >> 2)) * kVRow + 4 * (n16 & 3);
+    const uint16_t* vl = s_vt + (g4 * 4 + (n16 >> 2)) * kVRow + 4 * (n16 & 3);
 #pragma unroll
     for (int nb = 0; nb < NOB; ++nb) oacc[nb] = Mfma16<TT>::mma(lds_read_tr(vl + nb * 16), pbv, oacc[nb]);
   } else {
@@ -1034,11 +1090,11 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
 #pragma unroll
     for (int b = 0; b < NBUF; ++b) pv_step(vb[b], st0 + b);
   }
-  if constexpr (kMma) {
+  if constexpr (kMmaPv) {
     // O^T blocks (lane (g4, n16): dims nb*16 + 4*g4 .. +3 of head n16) ->
     // acc[h][8] of dims j*8 .. +7 in every row of the wave, through LDS (the
     // staged V tile is no longer read: G x D floats <= its 16 x kVRow x 2 bytes)
-    float* s_o = reinterpret_cast<float*>(s_v);
+    float* s_o = reinterpret_cast<float*>(s_vt);
     if (n16 < G) {
 #pragma unroll
       for (int nb = 0; nb < NOB; ++nb) *reinterpret_cast<f32x4*>(&s_o[n16 * D + nb * 16 + 4 * g4]) = oacc[nb];
@@ -1450,7 +1506,8 @@ int64_t fast_grid(const DecodeArgs& a, int64_t units) {
 int64_t fast_lds_bytes(int partition, int g, bool fp8, int d) {
   const int t = partition + 16 * ring_of(d);
   const int gp = pow2ceil(g);
-  return (int64_t)fast_score_floats(t, gp, fp8) * 4 + (fp8 ? fast_prob_bytes(t, gp) : 0);
+  return (int64_t)fast_score_floats(t, gp, fp8, mma_pv_2byte(d, g)) * 4 +
+         (fp8 ? fast_prob_bytes(t, gp) : 0);
 }
 
 template <class TT, int D, int G, int SPB, bool kF8 = false>

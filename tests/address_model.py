@@ -55,9 +55,17 @@ def fast_prob_bytes(t: int, gp: int) -> int:
     return 16 * K_ROW * 2 if t * gp * 2 < 16 * K_ROW * 2 else t * gp * 2
 
 
-def fast_score_floats(t: int, gp: int, fp8: bool) -> int:
-    """fast_score_floats: the score region, at least the FP8 V tile."""
-    return 16 * V_ROW // 2 if fp8 and t * gp < 16 * V_ROW // 2 else t * gp
+MMA_PV_MIN_G = 5   # kMmaPvMinG: 2-byte pools at head dim 128 from this group size
+
+
+def fast_score_floats(t: int, gp: int, fp8: bool, mma_pv: bool = False) -> int:
+    """fast_score_floats: the score region; at least the FP8 V tile, and for
+    a 2-byte MFMA pass 3 the in-place probabilities plus the V tile."""
+    if fp8:
+        return 16 * V_ROW // 2 if t * gp < 16 * V_ROW // 2 else t * gp
+    if mma_pv:
+        return max(t * gp, t * gp // 2 + 16 * V_ROW // 2)
+    return t * gp
 
 
 def ring_of(D: int) -> int:
@@ -289,7 +297,8 @@ def decode_host(S, H, KV, bs, max_bps, fp8, D=128) -> DecodeLaunch:
     L.grid = n
     gp = pow2ceil(G)
     t = L.partition + 16 * ring_of(D)
-    L.lds_floats = fast_score_floats(t, gp, fp8) + (fast_prob_bytes(t, gp) // 4 if fp8 else 0)
+    mma_pv = D == 128 and G >= MMA_PV_MIN_G
+    L.lds_floats = fast_score_floats(t, gp, fp8, mma_pv) + (fast_prob_bytes(t, gp) // 4 if fp8 else 0)
     return L
 
 
@@ -451,6 +460,14 @@ def decode(W: Writes, L: DecodeLaunch, out: Buf, ws: Buf, seq_lens: np.ndarray,
             # the V tile and the O exchange reuse the score region
             W.index([2 * (15 * V_ROW + 127) + 1, 4 * L.G * D - 1], pb0,
                     "decode LDS V tile / O exchange in the score region (bytes)")
+        elif D == 128 and L.G >= MMA_PV_MIN_G:
+            # MFMA pass 3 of 2-byte pools: probabilities in place as pairs
+            # (word t * GP/2 + k), then the V tile / O exchange after them
+            tpad = L.partition + 16 * ring
+            W.index(nsteps[run] * 16 * (gp // 2) - 1, tpad * (gp // 2), "decode in-place probabilities")
+            v0 = tpad * (gp // 2) * 4   # bytes
+            W.index([v0 + 2 * (15 * V_ROW + 127) + 1, v0 + 4 * L.G * D - 1], L.lds_floats * 4,
+                    "decode LDS V tile / O exchange after the probabilities (bytes)")
         nb = _ceil(ntok[run], L.bs)
         W.index(nb - 1, 128, "decode block ids per lane")
         # block-table reads of the partition
