@@ -1222,10 +1222,10 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
 template <class TT, int D, int G, int SPB, bool kF8>
 // FP8 pools with up to 4 heads per group: at most 128 VGPRs, four waves per
 // SIMD (the MFMA pass 3 would otherwise take the kernel to 148). Head dim 128
-// with 5-6 heads per group: at most 168, three waves per SIMD (about 1%
-// faster than 8 waves per CU at 180-192; 7-8 heads would spill there).
+// with 5-6 heads per group (FP8 pools: 5-7): at most 168, three waves per
+// SIMD (1-3% faster than 8 waves per CU at 180-212; more heads would spill).
 __global__ __launch_bounds__(64)
-__attribute__((amdgpu_waves_per_eu(kF8 && G <= 4 ? 4 : (D == 128 && G >= 5 && G <= 6 ? 3 : 1))))
+__attribute__((amdgpu_waves_per_eu(kF8 && G <= 4 ? 4 : (D == 128 && G >= 5 && G <= (kF8 ? 7 : 6) ? 3 : 1))))
 void decode_fast_kernel(DecodeArgs a) {
   constexpr int GP = pow2ceil(G);
   extern __shared__ __attribute__((aligned(16))) float s_dyn[];

@@ -97,7 +97,7 @@ def test_decode_group_sizes(device, dtype, G):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("G", [3, 5])
+@pytest.mark.parametrize("G", [3, 5, 7])
 def test_decode_nan_rows_past_the_context(device, dtype, G):
     """Rows of a sequence's last block past its context hold e4m3 NaN codes
     (0x7F / 0xFF): the scores of those tokens are selected out and their V
