@@ -652,6 +652,9 @@ def main() -> int:
                          "copy: a plain 256 MiB device copy, the calibration kernel for "
                          "the FETCH_SIZE / WRITE_SIZE counters")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--num-heads", type=int, default=32,
+                    help="decode / decode-fp8: query heads over config 2's 8 kv heads (32: "
+                         "config 2 itself; 40 / 64: groups of 5 / 8)")
     ap.add_argument("--requests", type=int, default=256, help="e2e: number of requests")
     ap.add_argument("--kv-blocks", type=int, default=12288, help="e2e: KV pool blocks of 16")
     ap.add_argument("--kv-fp8", action="store_true",
@@ -676,13 +679,13 @@ def main() -> int:
     if args.workload == "transfer":
         return bench_transfer(args, dev)
     if args.workload == "decode-fp8":
-        return bench_decode_fp8(args, workloads.config2(dev))
+        return bench_decode_fp8(args, workloads.config2(dev, num_heads=args.num_heads))
     if args.workload == "prefill":
         return emit_prefill(args, workloads.config3(dev))
     if args.workload == "store":
         return bench_store(args, workloads.config3(dev))
     if args.workload == "decode":
-        w = workloads.config2(dev)
+        w = workloads.config2(dev, num_heads=args.num_heads)
     else:
         w = workloads.config4(dev)
         from nanopd_amd import paged_kernels as pk

@@ -179,9 +179,13 @@ def config2_seq_lens(seed: int = 2, batch: int = 64) -> list:
     return [int(x) for x in rng.integers(128, 4096, size=batch, endpoint=True)]
 
 
-def config2(device="cpu", seed: int = 2, batch: int = 64) -> DecodeWorkload:
+def config2(device="cpu", seed: int = 2, batch: int = 64, num_heads: int = 32) -> DecodeWorkload:
+    """Configuration 2 (32 q / 8 kv heads). num_heads other than 32 gives the
+    same contexts, tables and kv heads with another group size (e.g. 64: the
+    64 q / 8 kv heads of larger Qwen models)."""
+    name = "cfg2_qwen3_8b_decode_b64" if num_heads == 32 else f"cfg2_contexts_h{num_heads}_kv8_b64"
     return make_decode_workload(
-        "cfg2_qwen3_8b_decode_b64", num_heads=32, num_kv_heads=8, head_dim=128, block_size=16,
+        name, num_heads=num_heads, num_kv_heads=8, head_dim=128, block_size=16,
         dtype=torch.bfloat16, seq_lens=config2_seq_lens(seed, batch), seed=seed, device=device)
 
 
