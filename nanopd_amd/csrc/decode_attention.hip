@@ -562,7 +562,10 @@ using npd::st_coherent2;
 //      gives M (partitions past 64 are read in a second loop). The first
 //      batch of partial rows is requested at the same time;
 //   B: per chunk of 64 partitions, the weights 2^(m_p - M) go to LDS (0 past
-//      the last partition) and each lane accumulates its (head, 8-dim chunk)
+//      the last partition; with at most 64 partitions they are written at the
+//      end of A, so the (m, l) registers die before the accumulation, which
+//      sets the kernel's register peak at 5-8 heads per group; with more, each
+//      chunk reads its (m, l) again) and each lane accumulates its (head, 8-dim chunk)
 //      with kMergeFlight partitions of loads in flight. The loads are
 //      unconditional (clamped to the chunk's last partition, weight 0), so
 //      each wait covers exactly one batch.
@@ -595,44 +598,63 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int64_t slo
     }
   };
   load_batch(0, n0, 0, h0, c0);
-  float M[G], L[G], m0[G], l0[G];   // m0, l0: partition `lane`
+  float M[G], L[G];
+  {
+    float m0[G], l0[G];   // partition `lane`
 #pragma unroll
-  for (int h = 0; h < G; ++h) { m0[h] = -INFINITY; l0[h] = 0.f; }
-  if (lane < nparts) {
+    for (int h = 0; h < G; ++h) { m0[h] = -INFINITY; l0[h] = 0.f; }
+    if (lane < nparts) {
 #pragma unroll
-    for (int h = 0; h < G; ++h) ld_coherent2(a.part_ml + (slot(lane) * G + h) * 2, m0[h], l0[h]);
-  }
+      for (int h = 0; h < G; ++h) ld_coherent2(a.part_ml + (slot(lane) * G + h) * 2, m0[h], l0[h]);
+    }
 #pragma unroll
-  for (int h = 0; h < G; ++h) { M[h] = m0[h]; L[h] = 0.f; }
-  for (int p = lane + 64; p < nparts; p += 64) {
+    for (int h = 0; h < G; ++h) { M[h] = m0[h]; L[h] = 0.f; }
+    for (int p = lane + 64; p < nparts; p += 64) {
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      float mp, lp;
-      ld_coherent2(a.part_ml + (slot(p) * G + h) * 2, mp, lp);
-      M[h] = fmaxf(M[h], mp);
+      for (int h = 0; h < G; ++h) {
+        float mp, lp;
+        ld_coherent2(a.part_ml + (slot(p) * G + h) * 2, mp, lp);
+        M[h] = fmaxf(M[h], mp);
+      }
+    }
+    // M and L are wave-uniform (held in scalar registers)
+#pragma unroll
+    for (int h = 0; h < G; ++h) M[h] = uniform_f(wave_max_f(M[h]));
+    // up to 64 partitions: the weights come from the registers, which die
+    // here rather than living through the accumulation below
+    if (nparts <= 64) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        float w = 0.f, lw = 0.f;
+        if (lane < nparts) {
+          w = __builtin_amdgcn_exp2f(m0[h] - M[h]);
+          lw = l0[h] * w;
+        }
+        s_w[lane * GP + h] = w;
+        L[h] = uniform_f(L[h] + wave_sum_f(lw));
+      }
     }
   }
-  // M and L are wave-uniform (held in scalar registers)
-#pragma unroll
-  for (int h = 0; h < G; ++h) M[h] = uniform_f(wave_max_f(M[h]));
   float o[OWN][8];
 #pragma unroll
   for (int k = 0; k < OWN; ++k)
 #pragma unroll
     for (int d = 0; d < 8; ++d) o[k][d] = 0.f;
   for (int p0 = 0; p0 < nparts; p0 += 64) {
-    const int p = p0 + lane;
+    if (nparts > 64) {   // weights of this chunk of 64 partitions
+      const int p = p0 + lane;
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      float w = 0.f, lw = 0.f;
-      if (p < nparts) {
-        float mp = m0[h], lp = l0[h];
-        if (p0 > 0) ld_coherent2(a.part_ml + (slot(p) * G + h) * 2, mp, lp);
-        w = __builtin_amdgcn_exp2f(mp - M[h]);
-        lw = lp * w;
+      for (int h = 0; h < G; ++h) {
+        float w = 0.f, lw = 0.f;
+        if (p < nparts) {
+          float mp, lp;
+          ld_coherent2(a.part_ml + (slot(p) * G + h) * 2, mp, lp);
+          w = __builtin_amdgcn_exp2f(mp - M[h]);
+          lw = lp * w;
+        }
+        s_w[lane * GP + h] = w;
+        L[h] = uniform_f(L[h] + wave_sum_f(lw));
       }
-      s_w[lane * GP + h] = w;
-      L[h] = uniform_f(L[h] + wave_sum_f(lw));
     }
     __syncthreads();
     const int n = nparts - p0 < 64 ? nparts - p0 : 64;
@@ -1222,10 +1244,11 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
 template <class TT, int D, int G, int SPB, bool kF8>
 // FP8 pools with up to 4 heads per group: at most 128 VGPRs, four waves per
 // SIMD (the MFMA pass 3 would otherwise take the kernel to 148). Head dim 128
-// with 5-6 heads per group (FP8 pools: 5-7): at most 168, three waves per
-// SIMD (1-3% faster than 8 waves per CU at 180-212; more heads would spill).
+// with 5-7 heads per group: at most 168, three waves per SIMD (1-3% faster
+// than 8 waves per CU at 180-212; at 8 heads the bound spills in the epilogue
+// and measured no faster).
 __global__ __launch_bounds__(64)
-__attribute__((amdgpu_waves_per_eu(kF8 && G <= 4 ? 4 : (D == 128 && G >= 5 && G <= (kF8 ? 7 : 6) ? 3 : 1))))
+__attribute__((amdgpu_waves_per_eu(kF8 && G <= 4 ? 4 : (D == 128 && G >= 5 && G <= 7 ? 3 : 1))))
 void decode_fast_kernel(DecodeArgs a) {
   constexpr int GP = pow2ceil(G);
   extern __shared__ __attribute__((aligned(16))) float s_dyn[];
