@@ -558,17 +558,20 @@ using npd::st_coherent2;
 
 // Merge of one (sequence, kv-head) by a single wave (fast path), the
 // same log-sum-exp merge as merge_unit but latency-bound work done in parallel:
-//   A: lane p loads (m, l) of partition p for every head; a wave reduction
-//      gives M (partitions past 64 are read in a second loop). The first
-//      batch of partial rows is requested at the same time;
-//   B: per chunk of 64 partitions, the weights 2^(m_p - M) go to LDS (0 past
-//      the last partition; with at most 64 partitions they are written at the
-//      end of A, so the (m, l) registers die before the accumulation, which
-//      sets the kernel's register peak at 5-8 heads per group; with more, each
-//      chunk reads its (m, l) again) and each lane accumulates its (head, 8-dim chunk)
-//      with kMergeFlight partitions of loads in flight. The loads are
-//      unconditional (clamped to the chunk's last partition, weight 0), so
-//      each wait covers exactly one batch.
+//   A: up to 64 partitions, lane p loads (m, l) of partition p for every head,
+//      a wave reduction gives M, and the weights 2^(m_p - M) go to LDS (0 past
+//      the last partition); the first batch of partial rows is requested at
+//      the same time, and the (m, l) registers die before B. More partitions
+//      (a second-level merge of over 64 groups): M from a loop over them, no
+//      batch in flight meanwhile;
+//   B: each lane accumulates its (head, 8-dim chunk) pairs one after the
+//      other (one accumulator live), with kMergeFlight partitions of loads in
+//      flight. The loads are unconditional (clamped to the chunk's last
+//      partition, weight 0), so each wait covers exactly one batch. With more
+//      than 64 partitions the weights of each chunk of 64 are read again per
+//      chunk and pair (L summed with the first pair).
+// This keeps the merge's registers below those of the passes' loops, which
+// it would otherwise set for 5-8 heads per group.
 // The partials merged are the nparts consecutive slots from slot0. dst >= 0
 // (wave-uniform): the result is itself a partial (accumulator and (m, l)
 // relative to the merged max, not normalised), written to slot dst; else the
@@ -584,7 +587,6 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int64_t slo
   auto slot = [&](int p) -> int64_t { return slot0 + p; };
   // the first batch of partial rows of the lane's first (head, chunk) pair is
   // requested together with the (m, l) values: it does not depend on them
-  const int n0 = nparts < 64 ? nparts : 64;
   const bool pair0 = lane < G * CH;
   const int h0 = pair0 ? lane / CH : 0, c0 = lane % CH;
   float x[kMergeFlight][8];
@@ -597,9 +599,14 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int64_t slo
       for (int k2 = 0; k2 < 4; ++k2) ld_coherent2(src + k2 * (2 * CH), x[q][2 * k2], x[q][2 * k2 + 1]);
     }
   };
-  load_batch(0, n0, 0, h0, c0);
-  float M[G], L[G];
-  {
+  float M[G], L[G];   // wave-uniform (held in scalar registers)
+#pragma unroll
+  for (int h = 0; h < G; ++h) L[h] = 0.f;
+  if (nparts <= 64) {
+    // the first batch of partial rows is requested with the (m, l) values;
+    // the weights come from the registers, which die here rather than living
+    // through the accumulation below
+    load_batch(0, nparts, 0, h0, c0);
     float m0[G], l0[G];   // partition `lane`
 #pragma unroll
     for (int h = 0; h < G; ++h) { m0[h] = -INFINITY; l0[h] = 0.f; }
@@ -608,8 +615,24 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int64_t slo
       for (int h = 0; h < G; ++h) ld_coherent2(a.part_ml + (slot(lane) * G + h) * 2, m0[h], l0[h]);
     }
 #pragma unroll
-    for (int h = 0; h < G; ++h) { M[h] = m0[h]; L[h] = 0.f; }
-    for (int p = lane + 64; p < nparts; p += 64) {
+    for (int h = 0; h < G; ++h) M[h] = uniform_f(wave_max_f(m0[h]));
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float w = 0.f, lw = 0.f;
+      if (lane < nparts) {
+        w = __builtin_amdgcn_exp2f(m0[h] - M[h]);
+        lw = l0[h] * w;
+      }
+      s_w[lane * GP + h] = w;
+      L[h] = uniform_f(L[h] + wave_sum_f(lw));
+    }
+  } else {
+    // more than 64 partitions (a second-level merge of over 64 groups): no
+    // batch in flight while the maxima are read, so that this rare branch
+    // does not set the register peak
+#pragma unroll
+    for (int h = 0; h < G; ++h) M[h] = -INFINITY;
+    for (int p = lane; p < nparts; p += 64) {
 #pragma unroll
       for (int h = 0; h < G; ++h) {
         float mp, lp;
@@ -617,81 +640,64 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int64_t slo
         M[h] = fmaxf(M[h], mp);
       }
     }
-    // M and L are wave-uniform (held in scalar registers)
 #pragma unroll
     for (int h = 0; h < G; ++h) M[h] = uniform_f(wave_max_f(M[h]));
-    // up to 64 partitions: the weights come from the registers, which die
-    // here rather than living through the accumulation below
-    if (nparts <= 64) {
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        float w = 0.f, lw = 0.f;
-        if (lane < nparts) {
-          w = __builtin_amdgcn_exp2f(m0[h] - M[h]);
-          lw = l0[h] * w;
-        }
-        s_w[lane * GP + h] = w;
-        L[h] = uniform_f(L[h] + wave_sum_f(lw));
-      }
-    }
   }
-  float o[OWN][8];
+  // one (head, chunk) pair of the lane at a time: its accumulator is the
+  // only one live (with more than 64 partitions the weights are recomputed
+  // per pair; L is summed with the first)
 #pragma unroll
-  for (int k = 0; k < OWN; ++k)
+  for (int k = 0; k < OWN; ++k) {
+    const int idx = lane + 64 * k;
+    const bool own = idx < G * CH;
+    const int h = own ? idx / CH : 0, c = idx % CH;
+    float o[8];
 #pragma unroll
-    for (int d = 0; d < 8; ++d) o[k][d] = 0.f;
-  for (int p0 = 0; p0 < nparts; p0 += 64) {
-    if (nparts > 64) {   // weights of this chunk of 64 partitions
-      const int p = p0 + lane;
+    for (int d = 0; d < 8; ++d) o[d] = 0.f;
+    for (int p0 = 0; p0 < nparts; p0 += 64) {
+      if (nparts > 64) {   // weights of this chunk of 64 partitions
+        __syncthreads();   // every lane has read the previous ones
+        const int p = p0 + lane;
 #pragma unroll
-      for (int h = 0; h < G; ++h) {
-        float w = 0.f, lw = 0.f;
-        if (p < nparts) {
-          float mp, lp;
-          ld_coherent2(a.part_ml + (slot(p) * G + h) * 2, mp, lp);
-          w = __builtin_amdgcn_exp2f(mp - M[h]);
-          lw = lp * w;
+        for (int hh = 0; hh < G; ++hh) {
+          float w = 0.f, lw = 0.f;
+          if (p < nparts) {
+            float mp, lp;
+            ld_coherent2(a.part_ml + (slot(p) * G + hh) * 2, mp, lp);
+            w = __builtin_amdgcn_exp2f(mp - M[hh]);
+            lw = lp * w;
+          }
+          s_w[lane * GP + hh] = w;
+          if (k == 0) L[hh] = uniform_f(L[hh] + wave_sum_f(lw));
         }
-        s_w[lane * GP + h] = w;
-        L[h] = uniform_f(L[h] + wave_sum_f(lw));
       }
-    }
-    __syncthreads();
-    const int n = nparts - p0 < 64 ? nparts - p0 : 64;
-#pragma unroll
-    for (int k = 0; k < OWN; ++k) {
-      const int idx = lane + 64 * k;
-      if (idx < G * CH) {
-        const int h = idx / CH, c = idx % CH;
+      __syncthreads();
+      const int n = nparts - p0 < 64 ? nparts - p0 : 64;
+      if (own) {
         for (int q0 = 0; q0 < n; q0 += kMergeFlight) {
-          if (p0 > 0 || k > 0 || q0 > 0) load_batch(p0, n, q0, h, c);
+          if (p0 > 0 || k > 0 || q0 > 0 || nparts > 64) load_batch(p0, n, q0, h, c);
 #pragma unroll
           for (int q = 0; q < kMergeFlight; ++q) {
             const float w = s_w[(q0 + q) * GP + h];   // 0 past the chunk's last partition
 #pragma unroll
-            for (int d = 0; d < 8; ++d) o[k][d] = fmaf(x[q][d], w, o[k][d]);
+            for (int d = 0; d < 8; ++d) o[d] = fmaf(x[q][d], w, o[d]);
           }
         }
       }
     }
-    __syncthreads();
-  }
-#pragma unroll
-  for (int k = 0; k < OWN; ++k) {
-    const int idx = lane + 64 * k;
-    if (idx < G * CH) {
-      const int h = idx / CH, c = idx % CH;
+    if (own) {
       if (dst >= 0) {
         // same layout as a published partition: [dim pair][chunk][2]
         float* row = a.part_acc + (dst * G + h) * D + c * 2;
 #pragma unroll
-        for (int k2 = 0; k2 < 4; ++k2) st_coherent2(row + k2 * (2 * CH), o[k][2 * k2], o[k][2 * k2 + 1]);
+        for (int k2 = 0; k2 < 4; ++k2) st_coherent2(row + k2 * (2 * CH), o[2 * k2], o[2 * k2 + 1]);
       } else {
         store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + c * 8,
-                       o[k], oscale / L[h]);
+                       o, oscale / L[h]);
       }
     }
   }
+  __syncthreads();   // s_w is read no more
   if (dst >= 0 && lane == 0) {
 #pragma unroll
     for (int h = 0; h < G; ++h) st_coherent2(a.part_ml + (dst * G + h) * 2, M[h], L[h]);
@@ -1244,11 +1250,10 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
 template <class TT, int D, int G, int SPB, bool kF8>
 // FP8 pools with up to 4 heads per group: at most 128 VGPRs, four waves per
 // SIMD (the MFMA pass 3 would otherwise take the kernel to 148). Head dim 128
-// with 5-7 heads per group: at most 168, three waves per SIMD (1-3% faster
-// than 8 waves per CU at 180-212; at 8 heads the bound spills in the epilogue
-// and measured no faster).
+// with 5-8 heads per group: at most 168, three waves per SIMD (1-4% faster
+// than 8 waves per CU at 180-212).
 __global__ __launch_bounds__(64)
-__attribute__((amdgpu_waves_per_eu(kF8 && G <= 4 ? 4 : (D == 128 && G >= 5 && G <= 7 ? 3 : 1))))
+__attribute__((amdgpu_waves_per_eu(kF8 && G <= 4 ? 4 : (D == 128 && G >= 5 && G <= 8 ? 3 : 1))))
 void decode_fast_kernel(DecodeArgs a) {
   constexpr int GP = pow2ceil(G);
   extern __shared__ __attribute__((aligned(16))) float s_dyn[];

@@ -190,10 +190,13 @@ def test_two_level_merge_group_boundaries(device, lens):
     check(run(*args, 16), q, kc, vc, bt, sl, scale)
 
 
-def test_two_level_merge_many_groups(device):
+@pytest.mark.parametrize("num_heads", [4, 16])
+def test_two_level_merge_many_groups(device, num_heads):
     """1025 partitions of 64 tokens in one unit: 65 group results, so the
-    second level reads them in two 64-lane chunks."""
-    args = make_inputs(1, 4, 2, 128, [65537], 16, torch.bfloat16, device, seed=7)
+    second level reads them in two 64-lane chunks. With 8 heads per kv head a
+    lane merges two (head, chunk) pairs, the second reading the chunk weights
+    again."""
+    args = make_inputs(1, num_heads, 2, 128, [65537], 16, torch.bfloat16, device, seed=7)
     q, kc, vc, bt, sl, scale, mb = args
     check(run(*args, 16), q, kc, vc, bt, sl, scale)
 
