@@ -585,8 +585,8 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int64_t slo
   constexpr int GP = pow2ceil(G), CH = D / 8;
   constexpr int OWN = (G * CH + 63) / 64;   // (head, chunk) pairs per lane
   auto slot = [&](int p) -> int64_t { return slot0 + p; };
-  // the first batch of partial rows of the lane's first (head, chunk) pair is
-  // requested together with the (m, l) values: it does not depend on them
+  // the lane's first (head, chunk) pair, whose first batch of partial rows
+  // does not depend on the (m, l) values
   const bool pair0 = lane < G * CH;
   const int h0 = pair0 ? lane / CH : 0, c0 = lane % CH;
   float x[kMergeFlight][8];
