@@ -62,6 +62,10 @@ int npd_version(void);
  *   [kvh, T, D] contiguous, i.e. src_stride_head = T*D, src_stride_token = D.
  * Tokens with pos < 0, pos / block_size >= max_blocks_per_seq or blk outside
  * [0, num_blocks) are skipped.
+ * head_dim: any positive multiple of 4 up to 4096, as the reference's
+ * (PA/csrc/kvstore/paged_kv_store_ops.cu:25-26 moves 8-byte pieces). Caches
+ * and sources 16-byte aligned with strides in multiples of 8 elements, or, when
+ * head_dim % 8 == 4, 8-byte aligned with strides in multiples of 4.
  */
 int npd_paged_kv_store(void* k_cache, void* v_cache,
                        const void* k_src, const void* v_src,
@@ -79,6 +83,7 @@ int npd_paged_kv_store(void* k_cache, void* v_cache,
  *   slot = slot_mapping[t]; if slot < 0 or slot >= num_blocks*block_size: skip
  *   k_cache[slot / block_size, h, slot % block_size, :] = k_src[t*src_stride_token + h*src_stride_head + :]
  * Accepts token-major sources ([T, kvh, D] straight from k_proj) without a copy.
+ * head_dim, alignment and strides as npd_paged_kv_store.
  */
 int npd_paged_kv_store_slots(void* k_cache, void* v_cache,
                              const void* k_src, const void* v_src,
@@ -96,7 +101,8 @@ int npd_paged_kv_store_slots(void* k_cache, void* v_cache,
  *   byte = e4m3_rne(clamp(x / scale[h], -448, 448))   (IEEE fp32 division;
  *   NaN stays NaN), so that element = e4m3(byte) * scale[h].
  * Sources are fp16 or bf16 (src_dtype), as in npd_paged_kv_store_slots.
- * Caches 8-byte aligned, sources 16-byte aligned.
+ * Caches 8-byte aligned, sources 16-byte aligned; head_dim a positive multiple
+ * of 8 up to 4096.
  */
 int npd_paged_kv_store_slots_fp8(void* k_cache, void* v_cache,
                                  const void* k_src, const void* v_src,
@@ -126,6 +132,9 @@ int64_t npd_paged_attention_workspace_size(int64_t num_seqs, int64_t num_heads,
  * query/out strides are in elements (head_dim contiguous). seq_lens[s] <= 0
  * gives zeros; seq_lens[s] is clamped to max_blocks_per_seq * block_size.
  * Every output element is written: out need not be zeroed.
+ * head_dim: a multiple of 8 from 32 to 256 (64, 128 and 256 have tuned
+ * kernels; the reference takes multiples of 32 up to 1024,
+ * PA/csrc/attention/paged_attention_kernel.cu:16-20).
  * workspace: at least npd_paged_attention_workspace_size(...) bytes, 256-byte
  * aligned (may be NULL when that size is 0), zero-filled before its first
  * use. Layout: a fixed 1 MiB region of merge counters (at most 262144
@@ -158,9 +167,13 @@ int npd_paged_attention(void* out, const void* query,
  * NPD_NOALLOC_SCRATCH_BYTES that each GPU the library runs on holds until the
  * process ends; shapes whose npd_paged_attention_workspace_size exceeds it
  * fail with NPD_E_WORKSPACE (e.g. 64 sequences of up to 4096 tokens need
- * 17.3 MiB, 8 of up to 32768 need 18.3 MiB). The first call on a device looks
- * up the array's address and enqueues the clear of its counter region on
- * `stream`. All calls on one GPU share the array: calls that overlap on one
+ * 17.3 MiB, 8 of up to 32768 need 18.3 MiB). Arguments are checked first, as
+ * by npd_paged_attention (same error codes; nothing is launched on failure).
+ * The device is the stream's (hipStreamGetDevice; the null stream's is the
+ * calling thread's current device): the call makes it current while it looks
+ * up that device's array and launches, then restores the caller's device. The
+ * first call on a device looks up the array's address and enqueues the clear
+ * of its counter region on `stream`. All calls on one GPU share the array: calls that overlap on one
  * GPU (concurrent streams or threads) race and must be serialised by the
  * caller; stream-ordered calls are safe, since every call leaves the counters
  * at zero.
@@ -195,10 +208,11 @@ int64_t npd_paged_prefill_workspace_size(int64_t num_seqs, int64_t total_q,
  * Rows with p < 0 (context shorter than the chunk) get zeros. scale must be
  * positive and finite.
  * max_q_len: host-known upper bound on the chunk lengths (grid size).
- * head_dim 64, 128 or 256.
+ * head_dim: a multiple of 32 from 32 to 256 (64 and 128 have the tuned
+ * kernel; the reference's SDPA takes any, nanoPD/engine/model_runner.py:166-168).
  * max_context_len: host-known upper bound on context_lens; at head dims 64
  * and 128 key ranges longer than 1024 keys are split over up to 8 workgroups
- * when it allows (<= 0: no split; head dim 256 never splits). It sizes the
+ * when it allows (<= 0: no split; other head dims never split). It sizes the
  * workspace: npd_paged_prefill_workspace_size(...) bytes,
  * 256-byte aligned, zero-filled before first use, with the same fixed 1 MiB
  * counter region as npd_paged_attention's (every call leaves its counters at
@@ -227,8 +241,8 @@ int npd_paged_prefill_attention(void* out, const void* query,
  * prefill, nanoPD/engine/model_runner.py:152-168, reads fp16 K/V). K and V
  * elements are e4m3(byte) * k_scale[kv head] (v_scale for V), converted
  * exactly to the query's type (fp16/bf16, dtype) before the MFMAs; arithmetic
- * and workspace as in npd_paged_prefill_attention. head_dim 64, 128 or
- * 256; caches 8-byte aligned.
+ * and workspace as in npd_paged_prefill_attention. head_dim as there;
+ * caches 8-byte aligned.
  */
 int npd_paged_prefill_attention_fp8(void* out, const void* query,
                                     const void* key_cache, const void* value_cache,
@@ -307,9 +321,10 @@ int npd_kv_scatter_blocks(void* k_cache, void* v_cache, int64_t num_layers,
                           const void* wire_k, const void* wire_v, void* stream);
 
 /*
- * Fused attention prologue of a Qwen3-style layer (replaces the per-layer
- * q_norm / k_norm, rotary embedding, K/V transpose copies and paged_kv_store
- * calls of nanoPD/engine/model_runner.py:97-115, :142-146, :189-192).
+ * Fused attention prologue of a Qwen3-, Qwen2- or Llama-style layer (replaces
+ * the per-layer q_norm / k_norm, rotary embedding, K/V transpose copies and
+ * paged_kv_store calls of nanoPD/engine/model_runner.py:97-115, :142-146,
+ * :189-192).
  * qkv: [num_tokens, (num_heads + 2 num_kv_heads) * head_dim] token rows
  * (q heads, then k heads, then v heads) with token stride qkv_stride_token
  * elements -- the fused QKV projection output as it is.
@@ -321,10 +336,12 @@ int npd_kv_scatter_blocks(void* k_cache, void* v_cache, int64_t num_layers,
  * [num_blocks, num_kv_heads, block_size, head_dim]); tokens whose slot is
  * negative or outside the pool are not stored (q_out is still written).
  * rmsnorm(x, w) = half(half(x * rsqrt(mean(x^2) + eps)) * w) as HF
- * Qwen3RMSNorm; rope is rotate-half with angle positions[t] * inv_freq[i]
+ * Qwen3RMSNorm; with both norm weights NULL (layers without q / k norms,
+ * which the reference skips, model_runner.py:101-104) rmsnorm(x, .) = x.
+ * rope is rotate-half with angle positions[t] * inv_freq[i]
  * (inv_freq: fp32 [head_dim / 2]), computed in fp32 and rounded once.
  * q_out token stride is q_stride_token elements (heads contiguous).
- * head_dim 128 only; dtype fp16 or bf16 for every 2-byte tensor.
+ * head_dim 64, 128 or 256; dtype fp16 or bf16 for every 2-byte tensor.
  */
 int npd_qk_norm_rope_store(void* q_out, void* k_cache, void* v_cache,
                            const void* qkv, const int32_t* slot_mapping,

@@ -157,6 +157,7 @@ struct DecodeArgs {
   int min_partition; // fast path, <= 64 sequences: the kernel may halve PS down to this
   int max_parts;
   int max_groups;    // fast path: merge groups per unit (0: one-level merge)
+  int head_dim;      // D (the generic path reads it at run time)
   float scale_log2;  // softmax scale * log2(e)
   int64_t q_stride_seq, q_stride_head, out_stride_seq, out_stride_head;
 };
@@ -176,11 +177,12 @@ __device__ __forceinline__ float ld_part(const float* p) {
     return *p;
 }
 
-template <class TT, int D, int G, bool kCoherent = false>
+template <class TT, int G, bool kCoherent = false>
 __device__ __forceinline__ void merge_unit(const DecodeArgs& a, int unit, int s, int kh, int nparts,
                                            int tid, int nthreads) {
   const int64_t base = (int64_t)unit * a.max_parts;
-  constexpr int CH = D / 8;  // 8-dim chunks per head
+  const int D = a.head_dim;
+  const int CH = D / 8;  // 8-dim chunks per head
   for (int idx = tid; idx < G * CH; idx += nthreads) {
     const int h = idx / CH, c = idx % CH;
     float M = -INFINITY;
@@ -201,9 +203,13 @@ __device__ __forceinline__ void merge_unit(const DecodeArgs& a, int unit, int s,
   }
 }
 
-template <class TT, int D, int G>
+// LPT: lanes per token row, a power of two >= the row's CPR = D / 8 16-byte
+// chunks (D at run time, a multiple of 8 from 32 to 256); lanes j >= CPR of a
+// row hold a zero query and load its last chunk (an address inside the row),
+// so they add nothing to the dot products and store nothing.
+template <class TT, int LPT, int G>
 __global__ __launch_bounds__(64) void decode_partition_kernel(DecodeArgs a) {
-  constexpr int LPT = D / 8;             // lanes per token row
+  static_assert(LPT == 4 || LPT == 8 || LPT == 16 || LPT == 32, "lanes per token row");
   constexpr int TPL = 64 / LPT;          // tokens per load
   constexpr int NL = kStep / TPL;        // loads per step
   constexpr int GP = pow2ceil(G);        // heads padded to a power of two
@@ -220,6 +226,9 @@ __global__ __launch_bounds__(64) void decode_partition_kernel(DecodeArgs a) {
   const int lane = threadIdx.x;
   const int r = lane / LPT;   // token row within a load
   const int j = lane % LPT;   // 16-byte chunk of the head row
+  const int cpr = a.head_dim / 8;          // chunks per head row
+  const bool live = j < cpr;               // a chunk of the row (else padding)
+  const int jc = live ? j : cpr - 1;       // the chunk this lane loads
   const int unit = blockIdx.x;
   const int s = unit / a.num_kv_heads;
   const int kh = unit - s * a.num_kv_heads;
@@ -229,7 +238,7 @@ __global__ __launch_bounds__(64) void decode_partition_kernel(DecodeArgs a) {
   const int cap = a.max_bps * a.block_size;
   ctx = ctx < cap ? ctx : cap;
   if (ctx <= 0) {
-    if (part == 0 && lane < LPT) {
+    if (part == 0 && lane < LPT && live) {
       const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
       for (int h = 0; h < G; ++h)
         store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + j * 8, z, 0.f);
@@ -253,11 +262,15 @@ __global__ __launch_bounds__(64) void decode_partition_kernel(DecodeArgs a) {
     s_blk[e] = b;
   }
 
-  // Query chunk j of each head in the group, as packed pairs.
+  // Query chunk j of each head in the group, as packed pairs (zero on
+  // padding lanes).
   u32x4 qv[G];
-  const uint16_t* qbase = a.q + s * a.q_stride_seq + (kh * G) * a.q_stride_head + j * 8;
+  const uint16_t* qbase = a.q + s * a.q_stride_seq + (kh * G) * a.q_stride_head + jc * 8;
 #pragma unroll
-  for (int h = 0; h < G; ++h) qv[h] = *reinterpret_cast<const u32x4*>(qbase + h * a.q_stride_head);
+  for (int h = 0; h < G; ++h) {
+    qv[h] = *reinterpret_cast<const u32x4*>(qbase + h * a.q_stride_head);
+    if (!live) qv[h] = u32x4{0, 0, 0, 0};
+  }
   __syncthreads();
 
   // rows of the unit's pool kv head inside a block
@@ -268,7 +281,7 @@ __global__ __launch_bounds__(64) void decode_partition_kernel(DecodeArgs a) {
     const int lb = t / bs;
     const int off = t - lb * bs;
     const int blk = s_blk[lb - b0];
-    return (((int64_t)blk * a.pool_kv_heads * bs) + head_off + off) * LPT + j;
+    return (((int64_t)blk * a.pool_kv_heads * bs) + head_off + off) * cpr + jc;
   };
 
   // ---------------- pass 1: scores ----------------
@@ -410,7 +423,8 @@ __global__ __launch_bounds__(64) void decode_partition_kernel(DecodeArgs a) {
 #pragma unroll
       for (int d = 0; d < 8; ++d) acc[h][d] += shfl_xor(acc[h][d], mask);
 
-  if (lane >= LPT) return;
+  if (lane >= LPT || !live) return;
+  const int D = a.head_dim;
   if (nparts == 1) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -426,9 +440,11 @@ __global__ __launch_bounds__(64) void decode_partition_kernel(DecodeArgs a) {
       dst[0] = f32x4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
       dst[1] = f32x4{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
     }
-    if (j < G) {
-      a.part_ml[(base * G + j) * 2] = s_ml[j];
-      a.part_ml[(base * G + j) * 2 + 1] = s_ml[GP + j];
+    // (m, l) of every head: the row's live lanes take heads j, j + cpr, ...
+    // (cpr may be below G at small head dims)
+    for (int h = j; h < G; h += cpr) {
+      a.part_ml[(base * G + h) * 2] = s_ml[h];
+      a.part_ml[(base * G + h) * 2 + 1] = s_ml[GP + h];
     }
   }
 }
@@ -1449,7 +1465,7 @@ __global__ __launch_bounds__(kSchedThreads) void decode_schedule_kernel(DecodeAr
 }
 
 // Merge kernel for the generic path: one workgroup per (sequence, kv-head).
-template <class TT, int D, int G>
+template <class TT, int G>
 __global__ __launch_bounds__(256) void merge_partitions_kernel(DecodeArgs a) {
   const int unit = blockIdx.x;
   const int s = unit / a.num_kv_heads;
@@ -1460,7 +1476,7 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(DecodeArgs a) {
   if (ctx <= 0) return;
   const int nparts = (ctx + a.partition - 1) / a.partition;
   if (nparts <= 1) return;
-  merge_unit<TT, D, G>(a, unit, s, kh, nparts, threadIdx.x, blockDim.x);
+  merge_unit<TT, G>(a, unit, s, kh, nparts, threadIdx.x, blockDim.x);
 }
 
 bool use_fast_path(int64_t head_dim, int64_t block_size, int64_t num_seqs) {
@@ -1590,6 +1606,25 @@ int dispatch_fp8(int g, const DecodeArgs& a, int64_t units, hipStream_t st) {
   return npd::check_launch("npd_paged_attention_fp8");
 }
 
+// Generic path: any head dim (a multiple of 8 from 32 to 256), block size and
+// batch; a wave's lanes per token row are the next power of two above D / 8.
+template <class TT, int G>
+int launch_generic(const DecodeArgs& a, int64_t units, hipStream_t st) {
+  const dim3 grid((unsigned)units, (unsigned)a.max_parts);
+  const int cpr = a.head_dim / 8;
+  if (cpr <= 4)
+    hipLaunchKernelGGL((decode_partition_kernel<TT, 4, G>), grid, dim3(64), 0, st, a);
+  else if (cpr <= 8)
+    hipLaunchKernelGGL((decode_partition_kernel<TT, 8, G>), grid, dim3(64), 0, st, a);
+  else if (cpr <= 16)
+    hipLaunchKernelGGL((decode_partition_kernel<TT, 16, G>), grid, dim3(64), 0, st, a);
+  else
+    hipLaunchKernelGGL((decode_partition_kernel<TT, 32, G>), grid, dim3(64), 0, st, a);
+  if (a.max_parts > 1)
+    hipLaunchKernelGGL((merge_partitions_kernel<TT, G>), dim3((unsigned)units), dim3(256), 0, st, a);
+  return npd::check_launch("npd_paged_attention");
+}
+
 template <class TT, int D, int G>
 int launch_decode(const DecodeArgs& a, int64_t units, hipStream_t st) {
   if (use_fast_path(D, a.block_size, units / a.num_kv_heads)) {
@@ -1597,11 +1632,7 @@ int launch_decode(const DecodeArgs& a, int64_t units, hipStream_t st) {
     if (rc != NPD_OK) return rc;
     return npd::check_launch("npd_paged_attention");
   }
-  hipLaunchKernelGGL((decode_partition_kernel<TT, D, G>),
-                     dim3((unsigned)units, (unsigned)a.max_parts), dim3(64), 0, st, a);
-  if (a.max_parts > 1)
-    hipLaunchKernelGGL((merge_partitions_kernel<TT, D, G>), dim3((unsigned)units), dim3(256), 0, st, a);
-  return npd::check_launch("npd_paged_attention");
+  return launch_generic<TT, G>(a, units, st);
 }
 
 template <class TT, int D>
@@ -1619,11 +1650,26 @@ int dispatch_g(int g, const DecodeArgs& a, int64_t units, hipStream_t st) {
 }
 
 template <class TT>
+int dispatch_generic_g(int g, const DecodeArgs& a, int64_t units, hipStream_t st) {
+  switch (g) {
+    case 1: return launch_generic<TT, 1>(a, units, st);
+    case 2: return launch_generic<TT, 2>(a, units, st);
+    case 3: return launch_generic<TT, 3>(a, units, st);
+    case 4: return launch_generic<TT, 4>(a, units, st);
+    case 5: return launch_generic<TT, 5>(a, units, st);
+    case 6: return launch_generic<TT, 6>(a, units, st);
+    case 7: return launch_generic<TT, 7>(a, units, st);
+    default: return launch_generic<TT, 8>(a, units, st);
+  }
+}
+
+template <class TT>
 int dispatch_d(int64_t d, int g, const DecodeArgs& a, int64_t units, hipStream_t st) {
   switch (d) {
     case 64: return dispatch_g<TT, 64>(g, a, units, st);
     case 128: return dispatch_g<TT, 128>(g, a, units, st);
-    default: return dispatch_g<TT, 256>(g, a, units, st);
+    case 256: return dispatch_g<TT, 256>(g, a, units, st);
+    default: return dispatch_generic_g<TT>(g, a, units, st);
   }
 }
 
@@ -1686,16 +1732,15 @@ extern "C" int64_t npd_paged_attention_workspace_size(int64_t num_seqs, int64_t 
 
 namespace {
 
-// Shared by the 2-byte and the fp8 entry points: k_scale / v_scale are null
-// for 2-byte pools.
-int attention_impl(void* out, const void* query, const void* key_cache, const void* value_cache,
-                   const int32_t* block_tables, const int32_t* seq_lens, int64_t num_seqs,
-                   int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t num_blocks,
-                   int64_t block_size, int64_t max_blocks_per_seq, float scale,
-                   int64_t q_stride_seq, int64_t q_stride_head, int64_t out_stride_seq,
-                   int64_t out_stride_head, const float* k_scale, const float* v_scale,
-                   void* workspace, int64_t workspace_bytes, int32_t dtype, void* stream,
-                   bool fp8, const char* name) {
+// Argument checks of every decode entry point (everything but the workspace),
+// before any launch: NPD_OK or the error code, with the message set.
+int attention_check(const void* out, const void* query, const void* key_cache,
+                    const void* value_cache, const int32_t* block_tables, const int32_t* seq_lens,
+                    int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                    int64_t num_blocks, int64_t block_size, int64_t max_blocks_per_seq,
+                    int64_t q_stride_seq, int64_t q_stride_head, int64_t out_stride_seq,
+                    int64_t out_stride_head, const float* k_scale, const float* v_scale,
+                    int32_t dtype, bool fp8, const char* name) {
   using namespace npd;
   if (dtype != NPD_DTYPE_F16 && dtype != NPD_DTYPE_BF16)
     return fail(NPD_E_DTYPE, "%s: unsupported dtype code %d (fp16/bf16 only)", name, dtype);
@@ -1713,9 +1758,9 @@ int attention_impl(void* out, const void* query, const void* key_cache, const vo
   const int split = kv_split_of(num_heads, num_kv_heads);
   const int64_t pool_kv_heads = num_kv_heads;
   num_kv_heads *= split;
-  const int64_t g = num_heads / num_kv_heads;
-  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
-    return fail(NPD_E_INVALID, "%s: head_dim %lld not in {64, 128, 256}", name, (long long)head_dim);
+  if (head_dim < 32 || head_dim > 256 || head_dim % 8 != 0)
+    return fail(NPD_E_INVALID, "%s: head_dim %lld is not a multiple of 8 in [32, 256]", name,
+                (long long)head_dim);
   if (num_blocks * block_size * pool_kv_heads > INT32_MAX ||
       max_blocks_per_seq * block_size > INT32_MAX)
     return fail(NPD_E_INVALID, "%s: pool exceeds int32 row indexing", name);
@@ -1739,21 +1784,53 @@ int attention_impl(void* out, const void* query, const void* key_cache, const vo
       (reinterpret_cast<uintptr_t>(value_cache) & cache_align))
     return fail(NPD_E_ALIGN, "%s: out/query pointers must be 16-byte aligned, caches %d-byte", name,
                 fp8 ? 8 : 16);
-
   const int64_t max_ctx = block_size * max_blocks_per_seq;
   const int partition =
       choose_partition(num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_ctx, fp8);
+  const bool fast = use_fast_path(head_dim, block_size, num_seqs);
+  const int limit = fast ? kFastMaxPartition : kMaxPartition;
+  if (partition > limit)
+    return fail(NPD_E_INVALID, "%s: block_size %lld is above %d", name, (long long)block_size,
+                limit);
+  const int min_partition = fast ? fast_min_partition(partition, block_size, fp8) : partition;
+  if ((max_ctx + min_partition - 1) / min_partition > 65535)
+    return fail(NPD_E_INVALID, "%s: context too long", name);
+  if (num_seqs * num_kv_heads > kMaxCounters)
+    return fail(NPD_E_INVALID, "%s: %lld (sequence, kv-head) units exceed the %lld merge counters",
+                name, (long long)(num_seqs * num_kv_heads), (long long)kMaxCounters);
+  return NPD_OK;
+}
+
+// Shared by the 2-byte and the fp8 entry points: k_scale / v_scale are null
+// for 2-byte pools.
+int attention_impl(void* out, const void* query, const void* key_cache, const void* value_cache,
+                   const int32_t* block_tables, const int32_t* seq_lens, int64_t num_seqs,
+                   int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t num_blocks,
+                   int64_t block_size, int64_t max_blocks_per_seq, float scale,
+                   int64_t q_stride_seq, int64_t q_stride_head, int64_t out_stride_seq,
+                   int64_t out_stride_head, const float* k_scale, const float* v_scale,
+                   void* workspace, int64_t workspace_bytes, int32_t dtype, void* stream,
+                   bool fp8, const char* name) {
+  using namespace npd;
   {
-    const int limit = use_fast_path(head_dim, block_size, num_seqs) ? kFastMaxPartition : kMaxPartition;
-    if (partition > limit)
-      return fail(NPD_E_INVALID, "%s: block_size %lld is above %d", name, (long long)block_size,
-                  limit);
+    const int rc = attention_check(out, query, key_cache, value_cache, block_tables, seq_lens,
+                                   num_seqs, num_heads, num_kv_heads, head_dim, num_blocks,
+                                   block_size, max_blocks_per_seq, q_stride_seq, q_stride_head,
+                                   out_stride_seq, out_stride_head, k_scale, v_scale, dtype, fp8,
+                                   name);
+    if (rc != NPD_OK || num_seqs == 0) return rc;
   }
+  const int split = kv_split_of(num_heads, num_kv_heads);
+  const int64_t pool_kv_heads = num_kv_heads;
+  num_kv_heads *= split;
+  const int64_t g = num_heads / num_kv_heads;
+  const int64_t max_ctx = block_size * max_blocks_per_seq;
+  const int partition =
+      choose_partition(num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_ctx, fp8);
   const bool fast = use_fast_path(head_dim, block_size, num_seqs);
   const int min_partition = fast ? fast_min_partition(partition, block_size, fp8) : partition;
   // partial slots per unit: for the shortest partition the kernel may take
   const int64_t max_parts = (max_ctx + min_partition - 1) / min_partition;
-  if (max_parts > 65535) return fail(NPD_E_INVALID, "%s: context too long", name);
   const int64_t need = npd_paged_attention_workspace_size(num_seqs, num_heads, pool_kv_heads,
                                                           head_dim, block_size, max_blocks_per_seq);
   if (need > 0) {
@@ -1772,9 +1849,6 @@ int attention_impl(void* out, const void* query, const void* key_cache, const vo
   a.block_tables = block_tables;
   a.seq_lens = seq_lens;
   const int64_t units = num_seqs * num_kv_heads;
-  if (units > kMaxCounters)
-    return fail(NPD_E_INVALID, "%s: %lld (sequence, kv-head) units exceed the %lld merge counters",
-                name, (long long)units, (long long)kMaxCounters);
   // [counters | item count | work list | partial acc | partial (m, l)]
   char* wsb = static_cast<char*>(workspace);
   const bool fast_ws = use_fast_path(head_dim, block_size, num_seqs);
@@ -1796,6 +1870,7 @@ int attention_impl(void* out, const void* query, const void* key_cache, const vo
   a.partition = partition;
   a.min_partition = min_partition;
   a.max_parts = (int)max_parts;
+  a.head_dim = (int)head_dim;
   a.scale_log2 = scale * kLog2e;
   a.q_stride_seq = q_stride_seq;
   a.q_stride_head = q_stride_head;
@@ -1871,14 +1946,40 @@ __global__ __launch_bounds__(256) void clear_counters_kernel(u32x4* p, int64_t n
   if (i < n) p[i] = u32x4{0, 0, 0, 0};
 }
 
-// The device address of the current device's `scratch` (nullptr and an error
-// message on failure). The first call on a device looks the address up and
-// enqueues the clear of its counter region on `st`, ahead of the caller's
-// kernels.
-void* scratch_of_current_device(hipStream_t st, const char* name) {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices) {
-    npd::fail(NPD_E_LAUNCH, "%s: no usable current device (%d)", name, dev);
+// The device a stream's work runs on: the stream's own device for a created
+// stream; the null stream and the per-thread / legacy handles belong to the
+// calling thread's current device. -1 on failure.
+int stream_device(hipStream_t st) {
+  if (st == nullptr || st == hipStreamPerThread || st == hipStreamLegacy) {
+    int dev = -1;
+    return hipGetDevice(&dev) == hipSuccess ? dev : -1;
+  }
+  hipDevice_t dev = -1;
+  return hipStreamGetDevice(st, &dev) == hipSuccess ? (int)dev : -1;
+}
+
+// Makes `dev` the calling thread's current device for its lifetime and
+// restores the previous one after (a new host thread starts on device 0,
+// whatever device the stream it is handed belongs to).
+struct DeviceGuard {
+  int prev = -1;
+  bool ok = false;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) return;
+    ok = prev == dev || hipSetDevice(dev) == hipSuccess;
+  }
+  ~DeviceGuard() {
+    if (ok && prev >= 0) (void)hipSetDevice(prev);
+  }
+};
+
+// The device address of device `dev`'s `scratch` (nullptr and an error
+// message on failure); `dev` must be the current device. The first call on a
+// device looks the address up and enqueues the clear of its counter region on
+// `st`, ahead of the caller's kernels.
+void* scratch_of_device(int dev, hipStream_t st, const char* name) {
+  if (dev < 0 || dev >= kScratchDevices) {
+    npd::fail(NPD_E_LAUNCH, "%s: no usable device for the stream (%d)", name, dev);
     return nullptr;
   }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
@@ -1909,6 +2010,14 @@ extern "C" int npd_paged_attention_noalloc(void* out, const void* query, const v
                                            int64_t q_stride_head, int64_t out_stride_seq,
                                            int64_t out_stride_head, int32_t dtype, void* stream) {
   const char* name = "npd_paged_attention_noalloc";
+  // the same argument checks as npd_paged_attention, before the scratch is
+  // touched: invalid calls get the same codes and launch nothing
+  const int rc = attention_check(out, query, key_cache, value_cache, block_tables, seq_lens,
+                                 num_seqs, num_heads, num_kv_heads, head_dim, num_blocks,
+                                 block_size, max_blocks_per_seq, q_stride_seq, q_stride_head,
+                                 out_stride_seq, out_stride_head, nullptr, nullptr, dtype, false,
+                                 name);
+  if (rc != NPD_OK || num_seqs == 0) return rc;
   const int64_t need = npd_paged_attention_workspace_size(num_seqs, num_heads, num_kv_heads,
                                                           head_dim, block_size, max_blocks_per_seq);
   if (need > kScratchBytes)
@@ -1916,9 +2025,16 @@ extern "C" int npd_paged_attention_noalloc(void* out, const void* query, const v
                      "%s: these shapes need %lld bytes of workspace, above the %lld-byte static "
                      "scratch; call npd_paged_attention with a workspace", name, (long long)need,
                      (long long)kScratchBytes);
+  // the scratch of the stream's device, looked up (and the launches made)
+  // with that device current
+  const hipStream_t st = npd::as_stream(stream);
+  const int dev = stream_device(st);
+  if (dev < 0) return npd::fail(NPD_E_LAUNCH, "%s: cannot tell the stream's device", name);
+  DeviceGuard guard(dev);
+  if (!guard.ok) return npd::fail(NPD_E_LAUNCH, "%s: cannot make device %d current", name, dev);
   void* ws = nullptr;
-  if (num_seqs > 0 && need > 0) {
-    ws = scratch_of_current_device(npd::as_stream(stream), name);
+  if (need > 0) {
+    ws = scratch_of_device(dev, st, name);
     if (!ws) return NPD_E_LAUNCH;
   }
   return attention_impl(out, query, key_cache, value_cache, block_tables, seq_lens, num_seqs,

@@ -39,18 +39,20 @@ __device__ __forceinline__ u32x2 to_e4m3(u32x4 w, float scale) {
   return u32x2{out[0], out[1]};
 }
 
-// LPR = 8-element chunks per head row (head_dim / 8).
+// LPR = 8-element chunks per head row (head_dim / 8); 0: a runtime count
+// `lpr` (head dims other than 64, 128 and 256).
 template <class TT, int LPR>
 __global__ __launch_bounds__(kThreads) void kv_store_fp8_kernel(
     u32x2* __restrict__ k_cache, u32x2* __restrict__ v_cache, const u32x4* __restrict__ k_src,
     const u32x4* __restrict__ v_src, const int32_t* __restrict__ slots,
     const float* __restrict__ k_scale, const float* __restrict__ v_scale, int64_t total,
     int num_kv_heads, int block_size, int num_blocks, int64_t stride_head_v,
-    int64_t stride_token_v) {
+    int64_t stride_token_v, int lpr) {
   const int64_t gid = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (gid >= total) return;
-  const int c = (int)(gid & (LPR - 1));
-  const int64_t row = gid / LPR;
+  const int lanes = LPR > 0 ? LPR : lpr;
+  const int64_t row = LPR > 0 ? gid / LPR : gid / lanes;
+  const int c = (int)(gid - row * lanes);
   const int t = (int)(row / num_kv_heads);
   const int h = (int)(row - (int64_t)t * num_kv_heads);
   const int slot = slots[t];
@@ -58,7 +60,7 @@ __global__ __launch_bounds__(kThreads) void kv_store_fp8_kernel(
   const int blk = slot / block_size;
   const int off = slot - blk * block_size;
   const int64_t src = (int64_t)h * stride_head_v + (int64_t)t * stride_token_v + c;
-  const int64_t dst = (((int64_t)blk * num_kv_heads + h) * block_size + off) * LPR + c;
+  const int64_t dst = (((int64_t)blk * num_kv_heads + h) * block_size + off) * lanes + c;
   k_cache[dst] = to_e4m3<TT>(k_src[src], k_scale[h]);
   v_cache[dst] = to_e4m3<TT>(v_src[src], v_scale[h]);
 }
@@ -82,8 +84,9 @@ extern "C" int npd_paged_kv_store_slots_fp8(void* k_cache, void* v_cache, const 
     return fail(NPD_E_INVALID, "%s: bad sizes (tokens %lld, kv heads %lld, block %lld, blocks %lld)",
                 name, (long long)num_tokens, (long long)num_kv_heads, (long long)block_size,
                 (long long)num_blocks);
-  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
-    return fail(NPD_E_INVALID, "%s: head_dim %lld not in {64, 128, 256}", name, (long long)head_dim);
+  if (head_dim <= 0 || head_dim % 8 != 0 || head_dim > 4096)
+    return fail(NPD_E_INVALID, "%s: head_dim %lld is not a positive multiple of 8 (at most 4096)",
+                name, (long long)head_dim);
   if (num_blocks * block_size > INT32_MAX || num_tokens > INT32_MAX)
     return fail(NPD_E_INVALID, "%s: pool or token count exceeds int32 indexing", name);
   if (num_tokens == 0) return NPD_OK;
@@ -108,12 +111,13 @@ extern "C" int npd_paged_kv_store_slots_fp8(void* k_cache, void* v_cache, const 
 #define NPD_FP8_LAUNCH(T, L)                                                                   \
   hipLaunchKernelGGL((kv_store_fp8_kernel<T, L>), dim3((unsigned)grid), dim3(kThreads), 0, st, \
                      kc, vc, ks, vs, slot_mapping, k_scale, v_scale, total, (int)num_kv_heads, \
-                     (int)block_size, (int)num_blocks, sh, stt)
+                     (int)block_size, (int)num_blocks, sh, stt, lpr)
   const bool bf = src_dtype == NPD_DTYPE_BF16;
   switch (lpr) {
     case 8: if (bf) NPD_FP8_LAUNCH(BF16, 8); else NPD_FP8_LAUNCH(F16, 8); break;
     case 16: if (bf) NPD_FP8_LAUNCH(BF16, 16); else NPD_FP8_LAUNCH(F16, 16); break;
-    default: if (bf) NPD_FP8_LAUNCH(BF16, 32); else NPD_FP8_LAUNCH(F16, 32); break;
+    case 32: if (bf) NPD_FP8_LAUNCH(BF16, 32); else NPD_FP8_LAUNCH(F16, 32); break;
+    default: if (bf) NPD_FP8_LAUNCH(BF16, 0); else NPD_FP8_LAUNCH(F16, 0); break;
   }
 #undef NPD_FP8_LAUNCH
   return check_launch(name);

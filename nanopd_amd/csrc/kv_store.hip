@@ -8,31 +8,40 @@
 // head row of D 2-byte elements takes D/8 lanes, so one wave64 writes 4 (D=128)
 // rows of K and 4 of V as fully coalesced 1 KiB bursts. The grid is flat over
 // (token, head, 16-byte chunk); every launch shape divides evenly. At
-// configuration 3's size (2096 tokens, 17.2 MB moved) a launch takes 3.4 us
-// back to back, against 2.8 us for a one-token store: the fixed cost of a
-// launch, not HBM, bounds it. Measured and dropped at that size: 2 or 4
-// chunks per thread (3.8 / 4.7 us), 64- or 512-thread workgroups (same or
-// slower), non-temporal loads and stores (2.99 us on one box, 3.97 on another).
+// configuration 3's size (2096 tokens, 17.2 MB moved) a launch takes 3.84 us
+// back to back (4.32 us in a rocprofv3 trace), against 2.8 us for a one-token
+// store: the fixed cost of a launch, not HBM, bounds it. Measured and dropped
+// at that size: 2 or 4 chunks per thread (3.8 / 4.7 us against 3.4 us on that
+// box), 64- or 512-thread workgroups (same or slower), non-temporal loads and
+// stores (2.99 us on one box, 3.97 on another).
+// Head dims 64, 128 and 256 have compile-time lane counts; any other multiple
+// of 8 runs the same kernel with a runtime count, and a head dim of 4 mod 8
+// moves 8-byte vectors (the reference's float2 granularity, any head_dim % 4
+// == 0, paged_kv_store_ops.cu:25-26).
 #include "common.h"
 
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
 
-// LPR = 16-byte lanes per head row (head_dim / 8).
-template <int LPR, bool kSlots>
+// LPR = vector lanes per head row: head_dim / 8 for 16-byte vectors (V =
+// u32x4), head_dim / 4 for 8-byte ones (u32x2). LPR 0: a runtime lane count
+// `lpr` (head dims other than 64, 128 and 256).
+template <int LPR, bool kSlots, class V = u32x4>
 __global__ __launch_bounds__(kThreads) void kv_store_kernel(
-    u32x4* __restrict__ k_cache, u32x4* __restrict__ v_cache,
-    const u32x4* __restrict__ k_src, const u32x4* __restrict__ v_src,
+    V* __restrict__ k_cache, V* __restrict__ v_cache,
+    const V* __restrict__ k_src, const V* __restrict__ v_src,
     const int32_t* __restrict__ block_tables, const int32_t* __restrict__ index,
     int64_t total, int num_kv_heads, int block_size, int num_blocks, int max_bps,
-    int64_t stride_head_v, int64_t stride_token_v) {
+    int64_t stride_head_v, int64_t stride_token_v, int lpr) {
   const int64_t gid = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (gid >= total) return;
-  const int c = (int)(gid & (LPR - 1));
-  const int64_t row = gid / LPR;
+  const int lanes = LPR > 0 ? LPR : lpr;
+  const int64_t row = LPR > 0 ? gid / LPR : gid / lanes;
+  const int c = (int)(gid - row * lanes);
   const int t = (int)(row / num_kv_heads);
   const int h = (int)(row - (int64_t)t * num_kv_heads);
 
@@ -52,9 +61,9 @@ __global__ __launch_bounds__(kThreads) void kv_store_kernel(
     off = pos - lb * block_size;
   }
   const int64_t src = (int64_t)h * stride_head_v + (int64_t)t * stride_token_v + c;
-  const int64_t dst = (((int64_t)blk * num_kv_heads + h) * block_size + off) * LPR + c;
-  const u32x4 kv = k_src[src];
-  const u32x4 vv = v_src[src];
+  const int64_t dst = (((int64_t)blk * num_kv_heads + h) * block_size + off) * lanes + c;
+  const V kv = k_src[src];
+  const V vv = v_src[src];
   k_cache[dst] = kv;
   v_cache[dst] = vv;
 }
@@ -72,8 +81,9 @@ int launch_store(bool slots, void* k_cache, void* v_cache, const void* k_src,
     return fail(NPD_E_INVALID, "%s: bad sizes (tokens %lld, kv heads %lld, block %lld, blocks %lld)",
                 name, (long long)num_tokens, (long long)num_kv_heads, (long long)block_size,
                 (long long)num_blocks);
-  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
-    return fail(NPD_E_INVALID, "%s: head_dim %lld not in {64, 128, 256}", name, (long long)head_dim);
+  if (head_dim <= 0 || head_dim % 4 != 0 || head_dim > 4096)
+    return fail(NPD_E_INVALID, "%s: head_dim %lld is not a positive multiple of 4 (at most 4096)",
+                name, (long long)head_dim);
   if (!slots && max_bps <= 0)
     return fail(NPD_E_INVALID, "%s: max_blocks_per_seq must be positive", name);
   if (num_blocks * block_size > INT32_MAX || num_tokens > INT32_MAX)
@@ -81,36 +91,49 @@ int launch_store(bool slots, void* k_cache, void* v_cache, const void* k_src,
   if (num_tokens == 0) return NPD_OK;
   if (!k_cache || !v_cache || !k_src || !v_src || !index || (!slots && !block_tables))
     return fail(NPD_E_INVALID, "%s: null pointer", name);
-  if (!aligned16(k_cache) || !aligned16(v_cache) || !aligned16(k_src) || !aligned16(v_src))
-    return fail(NPD_E_ALIGN, "%s: cache and source pointers must be 16-byte aligned", name);
-  if ((stride_head % 8) != 0 || (stride_token % 8) != 0 || stride_head < 0 || stride_token < 0)
-    return fail(NPD_E_ALIGN, "%s: source strides (%lld, %lld) must be non-negative multiples of 8 elements",
-                name, (long long)stride_head, (long long)stride_token);
+  // 16-byte vectors when head rows are whole 16-byte units, else 8-byte ones
+  // (head_dim % 8 == 4, rows of 8-byte units as the reference moves them)
+  const bool v16 = head_dim % 8 == 0;
+  const int vb = v16 ? 16 : 8;   // vector bytes
+  const uintptr_t am = (uintptr_t)vb - 1;
+  if (((uintptr_t)k_cache & am) || ((uintptr_t)v_cache & am) || ((uintptr_t)k_src & am) ||
+      ((uintptr_t)v_src & am))
+    return fail(NPD_E_ALIGN, "%s: cache and source pointers must be %d-byte aligned", name, vb);
+  const int64_t ve = vb / 2;     // elements per vector
+  if ((stride_head % ve) != 0 || (stride_token % ve) != 0 || stride_head < 0 || stride_token < 0)
+    return fail(NPD_E_ALIGN, "%s: source strides (%lld, %lld) must be non-negative multiples of %lld elements",
+                name, (long long)stride_head, (long long)stride_token, (long long)ve);
 
-  const int lpr = (int)(head_dim / 8);
+  const int lpr = (int)(head_dim / ve);
   const int64_t total = num_tokens * num_kv_heads * lpr;
   const int64_t grid = (total + kThreads - 1) / kThreads;
   hipStream_t st = as_stream(stream);
-  auto* kc = static_cast<u32x4*>(k_cache);
-  auto* vc = static_cast<u32x4*>(v_cache);
-  auto* ks = static_cast<const u32x4*>(k_src);
-  auto* vs = static_cast<const u32x4*>(v_src);
-  const int64_t sh = stride_head / 8, stt = stride_token / 8;
-#define NPD_STORE_LAUNCH(L)                                                                    \
-  do {                                                                                         \
-    if (slots)                                                                                 \
-      hipLaunchKernelGGL((kv_store_kernel<L, true>), dim3((unsigned)grid), dim3(kThreads), 0, \
-                         st, kc, vc, ks, vs, block_tables, index, total, (int)num_kv_heads,    \
-                         (int)block_size, (int)num_blocks, (int)max_bps, sh, stt);             \
-    else                                                                                       \
-      hipLaunchKernelGGL((kv_store_kernel<L, false>), dim3((unsigned)grid), dim3(kThreads), 0, \
-                         st, kc, vc, ks, vs, block_tables, index, total, (int)num_kv_heads,    \
-                         (int)block_size, (int)num_blocks, (int)max_bps, sh, stt);             \
+  const int64_t sh = stride_head / ve, stt = stride_token / ve;
+  const int nkv = (int)num_kv_heads, bsz = (int)block_size, nbk = (int)num_blocks, mbs = (int)max_bps;
+#define NPD_STORE_LAUNCH(L, V)                                                                   \
+  do {                                                                                           \
+    auto* kc = static_cast<V*>(k_cache);                                                         \
+    auto* vc = static_cast<V*>(v_cache);                                                         \
+    auto* ks = static_cast<const V*>(k_src);                                                     \
+    auto* vs = static_cast<const V*>(v_src);                                                     \
+    if (slots)                                                                                   \
+      hipLaunchKernelGGL((kv_store_kernel<L, true, V>), dim3((unsigned)grid), dim3(kThreads), 0, \
+                         st, kc, vc, ks, vs, block_tables, index, total, nkv, bsz, nbk, mbs, sh, \
+                         stt, lpr);                                                              \
+    else                                                                                         \
+      hipLaunchKernelGGL((kv_store_kernel<L, false, V>), dim3((unsigned)grid), dim3(kThreads), 0, \
+                         st, kc, vc, ks, vs, block_tables, index, total, nkv, bsz, nbk, mbs, sh, \
+                         stt, lpr);                                                              \
   } while (0)
-  switch (lpr) {
-    case 8: NPD_STORE_LAUNCH(8); break;
-    case 16: NPD_STORE_LAUNCH(16); break;
-    default: NPD_STORE_LAUNCH(32); break;
+  if (!v16) {
+    NPD_STORE_LAUNCH(0, u32x2);
+  } else {
+    switch (lpr) {
+      case 8: NPD_STORE_LAUNCH(8, u32x4); break;
+      case 16: NPD_STORE_LAUNCH(16, u32x4); break;
+      case 32: NPD_STORE_LAUNCH(32, u32x4); break;
+      default: NPD_STORE_LAUNCH(0, u32x4); break;
+    }
   }
 #undef NPD_STORE_LAUNCH
   return check_launch(name);

@@ -10,8 +10,8 @@
 // them before attending, model_runner.py:146). For an empty prefix both agree.
 //
 // MI355X design (gfx950, v_mfma_f32_16x16x32_{bf16,f16}, wave64):
-//   head dim D = 64 or 128 (prefill_kernel<.., D, ..>; 256 has its own
-//   kernel below);
+//   head dim D = 64 or 128 (prefill_kernel<.., D, ..>; the other multiples
+//   of 32 up to 256 run prefill_generic_kernel below);
 //   workgroup = 8 waves = one (sequence, kv-head, head group, 64-row query
 //   tile, key split); wave w owns one query head and 32 query rows. Two waves
 //   per SIMD, 256 VGPRs each (MFMA operands stay in VGPRs). HW = gcd(G, 4)
@@ -694,8 +694,9 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   }
 }
 
-// Head dim 256 (the tiles and register ring of prefill_kernel would need
-// about 174 KB of LDS and 336 VGPRs at this D). One workgroup of 4 waves per
+// Every head dim but 64 and 128 (multiples of 32 from 32 to 256): at 256 the
+// tiles and register ring of prefill_kernel would need about 174 KB of LDS
+// and 336 VGPRs. One workgroup of 4 waves per
 // (sequence, query head, 64-row query tile); wave w owns query rows
 // 16w .. 16w + 15 of the tile. Per step of 64 keys the workgroup copies the kv
 // head's K and V rows into LDS (keys past the visible range clamped to the
@@ -717,11 +718,11 @@ __global__ __launch_bounds__(256, 2) void prefill_generic_kernel(PrefillArgs a) 
   constexpr int kGT = 256;                      // threads
   constexpr int RW = D + 16;                    // LDS row (elements); 16-byte multiple
   constexpr int CPR = D / 8;                    // 8-element chunks per K/V row
-  constexpr int KPP = kGT / CPR;                // keys per load pass
-  constexpr int NPASS = kKT / KPP;
+  constexpr int NPASS = kKT * CPR / kGT;        // chunks of the 64-key tile per thread
   constexpr int NC = D / 32;                    // head-dim chunks of QK
   constexpr int NB = D / 16;                    // 16-dim blocks of O
-  static_assert(kKT % KPP == 0 && RW % 8 == 0, "tile shape");
+  static_assert(D % 32 == 0 && D >= 32 && D <= 256, "head dims of this kernel");
+  static_assert(NPASS * kGT == kKT * CPR && RW % 8 == 0, "tile shape");
   __shared__ __attribute__((aligned(16))) uint16_t s_k[kKT * RW];
   __shared__ __attribute__((aligned(16))) uint16_t s_v[kKT * RW];
 
@@ -794,13 +795,18 @@ __global__ __launch_bounds__(256, 2) void prefill_generic_kernel(PrefillArgs a) 
   // (in flight during the previous step's MFMAs), converted and copied into
   // LDS at the step's start. Keys past the visible range are clamped to the
   // last visible key (a real, finite row; the causal mask removes them).
+  // Chunk tid + 256e of the tile (e < NPASS) is chunk col_of(e) of key
+  // key_of(e): every thread moves whole 16-byte chunks, also when D / 8 is
+  // not a power of two.
   typedef typename std::conditional<kF8, u32x2, u32x4>::type raw_t;   // 8 elements
   raw_t kr[NPASS], vr[NPASS];
-  const int col = tid - (tid / CPR) * CPR;
+  auto key_of = [&](int e) { return (tid + kGT * e) / CPR; };
+  auto col_of = [&](int e) { return (tid + kGT * e) % CPR; };
   auto fetch = [&](int step) {
 #pragma unroll
     for (int e = 0; e < NPASS; ++e) {
-      int tok = step * kKT + tid / CPR + KPP * e;
+      const int col = col_of(e);
+      int tok = step * kKT + key_of(e);
       tok = tok < nkeys ? tok : nkeys - 1;
       const int lb = a.bs_shift >= 0 ? tok >> a.bs_shift : tok / bs;
       int blk = a.block_tables[(int64_t)s * a.max_bps + lb];
@@ -828,7 +834,7 @@ __global__ __launch_bounds__(256, 2) void prefill_generic_kernel(PrefillArgs a) 
     __syncthreads();   // every wave is done with the previous tile
 #pragma unroll
     for (int e = 0; e < NPASS; ++e) {
-      const int kk = tid / CPR + KPP * e;
+      const int kk = key_of(e), col = col_of(e);
       *reinterpret_cast<u32x4*>(&s_k[kk * RW + col * 8]) = pairs(kr[e]);
       *reinterpret_cast<u32x4*>(&s_v[kk * RW + col * 8]) = pairs(vr[e]);
     }
@@ -903,9 +909,18 @@ __global__ __launch_bounds__(256, 2) void prefill_generic_kernel(PrefillArgs a) 
 }
 
 template <class TT, bool kF8>
-int launch_generic(const PrefillArgs& a, int64_t grid, hipStream_t st, const char* name) {
-  hipLaunchKernelGGL((prefill_generic_kernel<TT, 256, kF8>), dim3((unsigned)grid), dim3(256), 0,
-                     st, a);
+int launch_generic(int64_t head_dim, const PrefillArgs& a, int64_t grid, hipStream_t st,
+                   const char* name) {
+  const dim3 g((unsigned)grid), b(256);
+  switch (head_dim) {
+    case 32: hipLaunchKernelGGL((prefill_generic_kernel<TT, 32, kF8>), g, b, 0, st, a); break;
+    case 96: hipLaunchKernelGGL((prefill_generic_kernel<TT, 96, kF8>), g, b, 0, st, a); break;
+    case 160: hipLaunchKernelGGL((prefill_generic_kernel<TT, 160, kF8>), g, b, 0, st, a); break;
+    case 192: hipLaunchKernelGGL((prefill_generic_kernel<TT, 192, kF8>), g, b, 0, st, a); break;
+    case 224: hipLaunchKernelGGL((prefill_generic_kernel<TT, 224, kF8>), g, b, 0, st, a); break;
+    case 256: hipLaunchKernelGGL((prefill_generic_kernel<TT, 256, kF8>), g, b, 0, st, a); break;
+    default: return npd::fail(NPD_E_INVALID, "%s: head_dim %lld", name, (long long)head_dim);
+  }
   return npd::check_launch(name);
 }
 
@@ -969,7 +984,7 @@ extern "C" int64_t npd_paged_prefill_workspace_size(int64_t num_seqs, int64_t to
                                                     int64_t num_heads, int64_t head_dim,
                                                     int64_t max_q_len, int64_t max_context_len) {
   (void)total_q;
-  // head dim 256 (prefill_generic_kernel) needs no workspace
+  // head dims other than 64 and 128 (prefill_generic_kernel) need no workspace
   if (head_dim != 64 && head_dim != 128) return 0;
   return prefill_layout(num_seqs, num_heads, head_dim, max_q_len, max_context_len).total;
 }
@@ -994,9 +1009,12 @@ int prefill_impl(void* out, const void* query, const void* key_cache, const void
   if (num_seqs < 0 || total_q < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_blocks <= 0 ||
       block_size <= 0 || max_blocks_per_seq <= 0 || max_q_len < 0)
     return fail(NPD_E_INVALID, "%s: bad sizes", name);
-  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
-    return fail(NPD_E_INVALID, "%s: head_dim %lld not in {64, 128, 256}", name,
+  if (head_dim < 32 || head_dim > 256 || head_dim % 32 != 0)
+    return fail(NPD_E_INVALID, "%s: head_dim %lld is not a multiple of 32 in [32, 256]", name,
                 (long long)head_dim);
+  // head dims 64 and 128: prefill_kernel (key splits, shared K/V tiles);
+  // every other one: prefill_generic_kernel
+  const bool generic = head_dim != 64 && head_dim != 128;
   if (num_heads % num_kv_heads != 0)
     return fail(NPD_E_INVALID, "%s: num_heads %lld is not a multiple of num_kv_heads %lld", name,
                 (long long)num_heads, (long long)num_kv_heads);
@@ -1004,7 +1022,7 @@ int prefill_impl(void* out, const void* query, const void* key_cache, const void
   const int hw = (g % 4 == 0) ? 4 : (g % 2 == 0 ? 2 : 1);   // gcd(g, 4)
   if (num_blocks * block_size * num_kv_heads > INT32_MAX || max_blocks_per_seq * block_size > INT32_MAX)
     return fail(NPD_E_INVALID, "%s: pool exceeds int32 row indexing", name);
-  if (head_dim != 256 && max_blocks_per_seq > kMaxBlocksLds)
+  if (!generic && max_blocks_per_seq > kMaxBlocksLds)
     return fail(NPD_E_INVALID, "%s: block tables wider than %d blocks are not supported", name,
                 kMaxBlocksLds);
   if (q_stride_token % 8 || q_stride_head % 8 || out_stride_token % 4 || out_stride_head % 4 ||
@@ -1023,7 +1041,7 @@ int prefill_impl(void* out, const void* query, const void* key_cache, const void
       (reinterpret_cast<uintptr_t>(out) & 7u) != 0)
     return fail(NPD_E_ALIGN, "%s: query pointer must be 16-byte aligned, caches %d-byte, out 8-byte",
                 name, fp8 ? 8 : 16);
-  if (head_dim == 256) {
+  if (generic) {
     const int64_t tiles = (max_q_len + 63) / 64;
     const int64_t grid = (num_seqs * num_kv_heads + 7) / 8 * 8 * tiles * g;
     if (grid > INT32_MAX) return fail(NPD_E_INVALID, "%s: too many tiles", name);
@@ -1052,10 +1070,10 @@ int prefill_impl(void* out, const void* query, const void* key_cache, const void
     a.out_stride_head = out_stride_head;
     hipStream_t st = as_stream(stream);
     if (dtype == NPD_DTYPE_BF16)
-      return fp8 ? launch_generic<BF16, true>(a, grid, st, name)
-                 : launch_generic<BF16, false>(a, grid, st, name);
-    return fp8 ? launch_generic<F16, true>(a, grid, st, name)
-               : launch_generic<F16, false>(a, grid, st, name);
+      return fp8 ? launch_generic<BF16, true>(head_dim, a, grid, st, name)
+                 : launch_generic<BF16, false>(head_dim, a, grid, st, name);
+    return fp8 ? launch_generic<F16, true>(head_dim, a, grid, st, name)
+               : launch_generic<F16, false>(head_dim, a, grid, st, name);
   }
   const Layout L = prefill_layout(num_seqs, num_heads, head_dim, max_q_len, max_context_len);
   if (L.total > 0) {

@@ -53,10 +53,23 @@ def test_c_validation_paths_need_no_gpu():
     rc = _rc("npd_paged_kv_store", fake, fake, fake, fake, fake, fake, 4, 2, 128, 16, 16, 4, 512,
              128, 7, None)
     assert rc == -2 and b"dtype" in lib.npd_last_error()
-    # bad head dim
-    rc = _rc("npd_paged_kv_store", fake, fake, fake, fake, fake, fake, 4, 2, 96, 16, 16, 4, 384,
-             96, 1, None)
+    # bad head dims: not a multiple of 4 for the store, of 8 (or outside [32,
+    # 256]) for decode; a head dim of 4 mod 8 needs 8-byte alignment only
+    rc = _rc("npd_paged_kv_store", fake, fake, fake, fake, fake, fake, 4, 2, 98, 16, 16, 4, 392,
+             98, 1, None)
     assert rc == -1 and b"head_dim" in lib.npd_last_error()
+    # (an odd stride stops each call before any launch: the pointer check
+    # passed when the message names the strides)
+    rc = _rc("npd_paged_kv_store", fake + 8, fake, fake, fake, fake, fake, 4, 2, 100, 16, 16, 4,
+             402, 100, 1, None)
+    assert rc == -3 and b"strides" in lib.npd_last_error()
+    rc = _rc("npd_paged_kv_store", fake + 4, fake, fake, fake, fake, fake, 4, 2, 100, 16, 16, 4,
+             402, 100, 1, None)
+    assert rc == -3 and b"8-byte aligned" in lib.npd_last_error()
+    for d in (24, 100, 264):
+        rc = _rc("npd_paged_attention", fake, fake, fake, fake, fake, fake, 2, 32, 8, d, 64, 16, 4,
+                 ctypes.c_float(0.1), 32 * d, d, 32 * d, d, None, 0, 1, None)
+        assert rc == -1 and b"head_dim" in lib.npd_last_error(), d
     # misaligned pointer
     rc = _rc("npd_paged_kv_store", fake + 2, fake, fake, fake, fake, fake, 4, 2, 128, 16, 16, 4,
              512, 128, 1, None)
@@ -101,6 +114,38 @@ def test_c_validation_paths_need_no_gpu():
     assert rope(128, 40 * 128, 1) == -1 and b"stride" in lib.npd_last_error()
     assert rope(128, 48 * 128, 5) == -2
     assert rope(128, 48 * 128, 1, t=0) == 0
+
+
+@pytest.mark.skipif(torch.cuda.is_available(),
+                    reason="fake pointers: validation-only test, never run where a launch could happen")
+def test_noalloc_validates_like_the_workspace_entry_point():
+    # npd_paged_attention_noalloc checks its arguments before it looks at its
+    # static scratch (or the device): every invalid call returns the code
+    # npd_paged_attention returns, with the same message, and launches nothing
+    lib = _lib.load()
+    fake = 0x1000
+    f = ctypes.c_float(0.1)
+    cases = [
+        # (seqs, heads, kv heads, head dim, blocks, block, max bps, strides, dtype, out ptr)
+        (2, 32, 8, 128, 64, 16, 4, (4096, 128, 4096, 128), 7, fake),        # dtype
+        (2, 12, 5, 128, 64, 16, 4, (1536, 128, 1536, 128), 1, fake),        # heads % kv heads
+        (2, 32, 8, 100, 64, 16, 4, (3200, 100, 3200, 100), 1, fake),        # head dim
+        (2, 32, 8, 128, 64, 16, 4, (4100, 128, 4096, 128), 1, fake),        # q stride
+        (2, 32, 8, 128, 64, 16, 4, (4096, 128, 4096, 128), 1, fake + 8),    # out alignment
+        (2, 32, 8, 128, 64, 16, 4, (4096, 128, 4096, 128), 1, 0),           # null out
+        (-1, 32, 8, 128, 64, 16, 4, (4096, 128, 4096, 128), 1, fake),       # sizes
+    ]
+    for s, h, kvh, d, nb, bs, mb, (qs, qh, os_, oh), code, out in cases:
+        rc_ws = _rc("npd_paged_attention", out, fake, fake, fake, fake, fake, s, h, kvh, d, nb, bs,
+                    mb, f, qs, qh, os_, oh, None, 0, code, None)
+        msg_ws = lib.npd_last_error().split(b":", 1)[1]
+        rc_na = _rc("npd_paged_attention_noalloc", out, fake, fake, fake, fake, fake, s, h, kvh, d,
+                    nb, bs, mb, f, qs, qh, os_, oh, code, None)
+        msg_na = lib.npd_last_error().split(b":", 1)[1]
+        assert rc_ws < 0 and rc_na == rc_ws and msg_na == msg_ws, (s, h, kvh, d, rc_ws, rc_na)
+    # no work is a no-op for both
+    assert _rc("npd_paged_attention_noalloc", 0, 0, 0, 0, 0, 0, 0, 32, 8, 128, 4096, 16, 256, f,
+               4096, 128, 4096, 128, 1, None) == 0
 
 
 def test_workspace_size():

@@ -58,6 +58,48 @@ def _with_workspace(q, kc, vc, bt, sl, mb):
     return out
 
 
+def _graph_replays(device, eager_first, seed):
+    """Captures one npd_paged_attention_noalloc call into a HIP graph (after
+    an eager call when eager_first), then replays it three times over new
+    query contents and new context lengths written into the captured input
+    buffers, with eager work and synchronisations between the replays. Each
+    replay must equal npd_paged_attention on a caller workspace bit for bit."""
+    num_seqs, heads, kvh, ctx_max = 16, 32, 8, 4096
+    q, kc, vc, bt, sl, mb = _inputs(num_seqs, heads, kvh, ctx_max, torch.bfloat16, device, seed)
+    out = torch.full_like(q, float("nan"))
+    if eager_first:
+        assert _noalloc(out, q, kc, vc, bt, sl, mb) == 0, _lib.load().npd_last_error()
+        torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    rcs = []
+    with torch.cuda.graph(graph):
+        rcs.append(_noalloc(out, q, kc, vc, bt, sl, mb))
+    assert rcs == [0], _lib.load().npd_last_error()
+    gen = torch.Generator(device="cpu").manual_seed(seed + 100)
+    for rep in range(3):
+        print(f"noalloc graph replay {rep} (eager first: {eager_first})", flush=True)
+        q.copy_((torch.randn(q.shape, generator=gen) * 0.5).to(q.dtype))
+        lens = torch.randint(1, ctx_max + 1, (num_seqs,), generator=gen)
+        lens[rep] = ctx_max   # some sequence spans the whole table (the longest split)
+        sl.copy_(lens.to(torch.int32))
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        want = _with_workspace(q, kc, vc, bt, sl, mb)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(out), bits(want)), f"replay {rep} differs"
+
+
+def test_noalloc_under_graph_capture_first_call(device):
+    # the first noalloc call of the process (the scratch look-up and the clear
+    # of its counter region happen inside the capture)
+    _graph_replays(device, eager_first=False, seed=11)
+
+
+def test_noalloc_under_graph_capture_after_eager_call(device):
+    _graph_replays(device, eager_first=True, seed=12)
+
+
 @pytest.mark.parametrize("first,second", [
     # (num_seqs, heads, kv_heads, ctx_max, dtype, seed)
     ((96, 32, 8, 4096, torch.bfloat16, 1), (8, 32, 8, 2000, torch.float16, 2)),
