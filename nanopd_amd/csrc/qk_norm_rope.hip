@@ -1,7 +1,10 @@
 // Fused attention prologue for Qwen3-style layers: per-head RMSNorm of q and k
 // (q_norm / k_norm), rotate-half RoPE at each token's position, and the paged
 // KV store of the rotated k and of v by slot -- one launch per layer, reading
-// the fused QKV projection output as it is.
+// the fused QKV projection output as it is. Without norm weights (null
+// pointers) the same launch serves Qwen2 / Llama layers, whose attention has
+// no q / k norm (the reference applies them only when the module has them,
+// nanoPD/engine/model_runner.py:101-104): RoPE of q and k as projected.
 //
 // Reference: per layer, paged_forward runs HF Qwen3Attention's q_norm / k_norm
 // and apply_rotary_pos_emb (nanoPD/engine/model_runner.py:97-115), transposes
@@ -115,18 +118,27 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_store_kernel(RopeArgs a
   }
   const bool is_q = hh < a.heads;
   const uint16_t* w = is_q ? a.q_w : a.k_w;
-  float ss = 0.f;
+  // no norm weight (Qwen2 / Llama layers): RoPE of the projection output as
+  // it is. The choice is uniform over a row's lanes, so the row reduction
+  // below runs on every lane it exchanges with.
+  const bool norm = w != nullptr;
+  float r = 1.f;
+  if (norm) {
+    float ss = 0.f;
 #pragma unroll
-  for (int p = 0; p < P; ++p) ss += x0[p] * x0[p] + x1[p] * x1[p];
-  const float r = rsqrtf(group_sum<LW>(ss) * (1.f / D) + a.eps);
+    for (int p = 0; p < P; ++p) ss += x0[p] * x0[p] + x1[p] * x1[p];
+    r = rsqrtf(group_sum<LW>(ss) * (1.f / D) + a.eps);
+  }
   const float pos = (float)a.positions[t];
   uint16_t y0[P], y1[P];
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int i = l + p * LW;
-    const float n0 = TT::lo(TT::from_float(TT::lo(TT::from_float(x0[p] * r)) * ld<TT>(w + i)));
-    const float n1 =
-        TT::lo(TT::from_float(TT::lo(TT::from_float(x1[p] * r)) * ld<TT>(w + i + HALF)));
+    float n0 = x0[p], n1 = x1[p];
+    if (norm) {
+      n0 = TT::lo(TT::from_float(TT::lo(TT::from_float(x0[p] * r)) * ld<TT>(w + i)));
+      n1 = TT::lo(TT::from_float(TT::lo(TT::from_float(x1[p] * r)) * ld<TT>(w + i + HALF)));
+    }
     float s, c;
     sincosf(pos * a.inv_freq[i], &s, &c);
     y0[p] = (uint16_t)TT::from_float(n0 * c - n1 * s);
@@ -205,8 +217,11 @@ int rope_impl(void* q_out, void* k_cache, void* v_cache, const void* qkv,
     return fail(NPD_E_INVALID, "%s: eps must be non-negative", name);
   if (num_tokens == 0) return NPD_OK;
   if (!q_out || !k_cache || !v_cache || !qkv || !slot_mapping || !positions || !inv_freq ||
-      !q_norm_weight || !k_norm_weight || (fp8 && (!k_scale || !v_scale)))
+      (fp8 && (!k_scale || !v_scale)))
     return fail(NPD_E_INVALID, "%s: null pointer", name);
+  if ((q_norm_weight == nullptr) != (k_norm_weight == nullptr))
+    return fail(NPD_E_INVALID, "%s: pass both norm weights (Qwen3) or neither (Qwen2 / Llama)",
+                name);
   const int64_t rows = num_tokens * (num_heads + 2 * num_kv_heads);
   const int64_t rows_per_block = (kThreads / 64) * (head_dim == 64 ? 2 : 1);
   const int64_t grid = (rows + rows_per_block - 1) / rows_per_block;

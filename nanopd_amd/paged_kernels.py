@@ -442,8 +442,8 @@ def paged_prefill_attention_fp8(out: torch.Tensor, query: torch.Tensor, key_cach
     """:func:`paged_prefill_attention` over an FP8 pool written by
     :func:`paged_kv_store_slots_fp8` (no reference counterpart): K =
     e4m3(byte) * k_scale[kv head], V likewise, converted exactly to the
-    query's type before the MFMAs. query/out fp16 or bf16; head_dim 64, 128
-    or 256."""
+    query's type before the MFMAs. query/out fp16 or bf16; head_dim a
+    multiple of 32 from 32 to 256."""
     _prefill(out, query, key_cache, value_cache, block_tables, cu_seqlens_q, context_lens, scale,
              block_size, max_num_blocks_per_seq, max_q_len, max_context_len, workspace,
              (k_scale, v_scale))
@@ -553,13 +553,16 @@ def load_kv(k_cache: torch.Tensor, v_cache: torch.Tensor, block_table, wire_k: t
 
 def qk_norm_rope_store(q_out: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                        qkv: torch.Tensor, slot_mapping: torch.Tensor, positions: torch.Tensor,
-                       inv_freq: torch.Tensor, q_norm_weight: torch.Tensor,
-                       k_norm_weight: torch.Tensor, eps: float,
+                       inv_freq: torch.Tensor, q_norm_weight: torch.Tensor | None,
+                       k_norm_weight: torch.Tensor | None, eps: float,
                        k_scale: torch.Tensor | None = None,
                        v_scale: torch.Tensor | None = None) -> None:
     """Qwen3 attention prologue in one launch (replaces q_norm / k_norm,
     rotary embedding, the K/V copies and paged_kv_store of
-    nanoPD/engine/model_runner.py:97-115, :142-146, :189-192).
+    nanoPD/engine/model_runner.py:97-115, :142-146, :189-192). With both norm
+    weights None it is the Qwen2 / Llama prologue: RoPE of q and k as
+    projected (the reference applies the norms only where the attention
+    module has them, model_runner.py:101-104).
 
     qkv: [T, (H + 2 KV) * D] rows of the fused projection (q, k, v heads;
     token stride free, elements contiguous); q_out: [T, H, D], heads
@@ -578,8 +581,10 @@ def qk_norm_rope_store(q_out: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
         _cache_checks(k_cache, v_cache)
     dev = qkv.device
     _check(qkv.is_cuda, "qkv must be on CUDA")
-    _same_device(dev, q_out, k_cache, v_cache, slot_mapping, positions, inv_freq, q_norm_weight,
-                 k_norm_weight)
+    _check((q_norm_weight is None) == (k_norm_weight is None),
+           "pass both norm weights (Qwen3) or neither (Qwen2 / Llama)")
+    norms = [w for w in (q_norm_weight, k_norm_weight) if w is not None]
+    _same_device(dev, q_out, k_cache, v_cache, slot_mapping, positions, inv_freq, *norms)
     _int32(slot_mapping, "slot_mapping")
     _int32(positions, "positions")
     num_blocks, kvh, bs, d = k_cache.shape
@@ -589,12 +594,13 @@ def qk_norm_rope_store(q_out: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
            "qkv must be [num_tokens, (num_heads + 2 * num_kv_heads) * head_dim]")
     _check(qkv.stride(1) == 1, "qkv rows must be contiguous")
     _check(q_out.stride(2) == 1 and q_out.stride(1) == d, "q_out heads must be contiguous")
-    for x in (q_out, qkv, q_norm_weight, k_norm_weight):
+    for x in (q_out, qkv, *norms):
         _check(x.dtype == (qkv.dtype if fp8 else k_cache.dtype),
                "qkv / q_out / norm weights must have one dtype (the cache dtype of a 2-byte pool)")
-    _check(q_norm_weight.numel() == d and k_norm_weight.numel() == d
-           and q_norm_weight.is_contiguous() and k_norm_weight.is_contiguous(),
+    _check(all(w.numel() == d and w.is_contiguous() for w in norms),
            "norm weights must be contiguous [head_dim]")
+    qw = q_norm_weight.data_ptr() if norms else None
+    kw = k_norm_weight.data_ptr() if norms else None
     _check(inv_freq.dtype == torch.float32 and inv_freq.numel() == d // 2
            and inv_freq.is_contiguous(), "inv_freq must be contiguous float32 [head_dim / 2]")
     for x, nm in ((slot_mapping, "slot_mapping"), (positions, "positions")):
@@ -607,13 +613,13 @@ def qk_norm_rope_store(q_out: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
         _same_device(dev, k_scale, v_scale)
         _lib.call("npd_qk_norm_rope_store_fp8", q_out.data_ptr(), k_cache.data_ptr(),
                   v_cache.data_ptr(), qkv.data_ptr(), slot_mapping.data_ptr(),
-                  positions.data_ptr(), inv_freq.data_ptr(), q_norm_weight.data_ptr(),
-                  k_norm_weight.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr(), t, h, kvh, d,
+                  positions.data_ptr(), inv_freq.data_ptr(), qw, kw, k_scale.data_ptr(),
+                  v_scale.data_ptr(), t, h, kvh, d,
                   num_blocks, bs, qkv.stride(0), q_out.stride(0), float(eps), code, _stream(dev))
         return
     _lib.call("npd_qk_norm_rope_store", q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
               qkv.data_ptr(), slot_mapping.data_ptr(), positions.data_ptr(), inv_freq.data_ptr(),
-              q_norm_weight.data_ptr(), k_norm_weight.data_ptr(), t, h, kvh, d, num_blocks, bs,
+              qw, kw, t, h, kvh, d, num_blocks, bs,
               qkv.stride(0), q_out.stride(0), float(eps), code, _stream(dev))
 
 

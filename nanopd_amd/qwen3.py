@@ -22,6 +22,12 @@ with a PyTorch restatement of the attention and compare.
 Shapes follow Qwen3-8B (config.json of the Qwen3 release): 36 layers, hidden
 4096, 32 query / 8 kv heads of 128, MLP 12288, vocab 151936, RoPE theta 1e6,
 RMSNorm eps 1e-6, untied LM head.
+The reference's runner also serves Qwen2 (and Llama) models
+(model_runner.py:53-58) and applies q_norm / k_norm only where the attention
+has them (:101-104). Qwen3Config's qk_norm=False, qkv_bias=True and
+tie_word_embeddings=True give that layer (Qwen2: q/k/v biases, no q/k norms,
+tied LM head on the 1.5B model); the fused prologue then runs without norm
+weights.
 """
 from __future__ import annotations
 
@@ -47,18 +53,26 @@ class Qwen3Config:
     rope_theta: float = 1.0e6
     rms_eps: float = 1.0e-6
     init_std: float = 0.02
+    qk_norm: bool = True              # per-head q/k RMSNorm (Qwen3); False: Qwen2 / Llama
+    qkv_bias: bool = False            # q/k/v projection biases (Qwen2)
+    tie_word_embeddings: bool = False  # LM head = embedding (Qwen2-1.5B)
 
     @property
     def num_params(self) -> int:
-        qkv = self.hidden * (self.num_heads + 2 * self.num_kv_heads) * self.head_dim
+        width = (self.num_heads + 2 * self.num_kv_heads) * self.head_dim
+        qkv = self.hidden * width + (width if self.qkv_bias else 0)
         o = self.num_heads * self.head_dim * self.hidden
         mlp = 3 * self.hidden * self.intermediate
-        norms = 2 * self.hidden + 2 * self.head_dim
-        return (self.num_layers * (qkv + o + mlp + norms) + 2 * self.vocab * self.hidden
-                + self.hidden)
+        norms = 2 * self.hidden + (2 * self.head_dim if self.qk_norm else 0)
+        heads = (1 if self.tie_word_embeddings else 2) * self.vocab * self.hidden
+        return self.num_layers * (qkv + o + mlp + norms) + heads + self.hidden
 
 
 QWEN3_8B = Qwen3Config()
+# Qwen2-1.5B (config.json of the Qwen2 release; configuration 1's head shape)
+QWEN2_1_5B = Qwen3Config(num_layers=28, hidden=1536, num_heads=12, num_kv_heads=2, head_dim=128,
+                         intermediate=8960, vocab=151936, rope_theta=1.0e6, rms_eps=1.0e-6,
+                         qk_norm=False, qkv_bias=True, tie_word_embeddings=True)
 
 
 @dataclass
@@ -122,15 +136,16 @@ class PagedQwen3:
             self.layers.append({
                 "in_norm": ones(E),
                 "qkv": rnd((H + 2 * KV) * D, E),
-                "q_norm": ones(D),
-                "k_norm": ones(D),
+                "qkv_bias": rnd((H + 2 * KV) * D) if cfg.qkv_bias else None,
+                "q_norm": ones(D) if cfg.qk_norm else None,
+                "k_norm": ones(D) if cfg.qk_norm else None,
                 "o": rnd(E, H * D),
                 "post_norm": ones(E),
                 "gate_up": rnd(2 * cfg.intermediate, E),
                 "down": rnd(E, cfg.intermediate),
             })
         self.final_norm = ones(E)
-        self.lm_head = rnd(cfg.vocab, E)
+        self.lm_head = self.embed if cfg.tie_word_embeddings else rnd(cfg.vocab, E)
         self.inv_freq = 1.0 / (cfg.rope_theta ** (torch.arange(0, D, 2, dtype=torch.float32,
                                                                device=self.device) / D))
         shape = (cfg.num_layers, num_blocks, KV, block_size, D)
@@ -155,8 +170,11 @@ class PagedQwen3:
         x1, x2 = xf[..., :half], xf[..., half:]
         return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1).to(x.dtype)
 
-    def _rms_norm_heads(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-        """HF Qwen3RMSNorm over head_dim: fp32 statistics, round, times w."""
+    def _rms_norm_heads(self, x: torch.Tensor, w: Optional[torch.Tensor]) -> torch.Tensor:
+        """HF Qwen3RMSNorm over head_dim: fp32 statistics, round, times w
+        (x itself for layers without q/k norms)."""
+        if w is None:
+            return x
         xf = x.float()
         r = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.cfg.rms_eps)
         return w * (xf * r).to(x.dtype)
@@ -223,7 +241,7 @@ class PagedQwen3:
         attn = torch.empty(T, H, D, dtype=self.dtype, device=self.device)
         for li, w in enumerate(self.layers):
             h = F.rms_norm(x, (E,), w["in_norm"], cfg.rms_eps)
-            qkv = h @ w["qkv"].t()
+            qkv = F.linear(h, w["qkv"], w["qkv_bias"])
             self._prologue(li, w, qkv, q, b, rope)
             kc, vc = self.k_cache[li], self.v_cache[li]
             self.attention(li, q, kc, vc, b, attn)
@@ -238,11 +256,13 @@ class PagedQwen3:
 
     @torch.no_grad()
     def load_hf_state_dict(self, sd: dict) -> None:
-        """Takes the weights of a Hugging Face Qwen3ForCausalLM state dict (the
-        model the reference's ModelRunner wraps, nanoPD/engine/model_runner.py:
-        8-13): q/k/v projections fused into one [(H + 2 KV) * D, E] matrix,
-        gate/up into one [2 I, E], the rest as they are. An untied LM head
-        (lm_head.weight) is used when present, else the embedding."""
+        """Takes the weights of a Hugging Face Qwen3ForCausalLM (or, with the
+        Qwen2 options, Qwen2ForCausalLM) state dict (the models the reference's
+        ModelRunner wraps, nanoPD/engine/model_runner.py:8-13, :53-58): q/k/v
+        projections fused into one [(H + 2 KV) * D, E] matrix (and their
+        biases into one vector), gate/up into one [2 I, E], the rest as they
+        are. An untied model needs lm_head.weight; a tied one shares the
+        embedding."""
         def get(name):
             t = sd[name]
             return t.to(device=self.device, dtype=self.dtype)
@@ -254,16 +274,22 @@ class PagedQwen3:
             w["qkv"].copy_(torch.cat([get(p + "self_attn.q_proj.weight"),
                                       get(p + "self_attn.k_proj.weight"),
                                       get(p + "self_attn.v_proj.weight")], dim=0))
-            w["q_norm"].copy_(get(p + "self_attn.q_norm.weight"))
-            w["k_norm"].copy_(get(p + "self_attn.k_norm.weight"))
+            if self.cfg.qkv_bias:
+                w["qkv_bias"].copy_(torch.cat([get(p + "self_attn.q_proj.bias"),
+                                               get(p + "self_attn.k_proj.bias"),
+                                               get(p + "self_attn.v_proj.bias")], dim=0))
+            if self.cfg.qk_norm:
+                w["q_norm"].copy_(get(p + "self_attn.q_norm.weight"))
+                w["k_norm"].copy_(get(p + "self_attn.k_norm.weight"))
             w["o"].copy_(get(p + "self_attn.o_proj.weight"))
             w["post_norm"].copy_(get(p + "post_attention_layernorm.weight"))
             w["gate_up"].copy_(torch.cat([get(p + "mlp.gate_proj.weight"),
                                           get(p + "mlp.up_proj.weight")], dim=0))
             w["down"].copy_(get(p + "mlp.down_proj.weight"))
         self.final_norm.copy_(get("model.norm.weight"))
-        self.lm_head.copy_(get("lm_head.weight" if "lm_head.weight" in sd
-                               else "model.embed_tokens.weight"))
+        if not self.cfg.tie_word_embeddings:   # an untied head without its own weight: the embedding
+            self.lm_head.copy_(get("lm_head.weight" if "lm_head.weight" in sd
+                                   else "model.embed_tokens.weight"))
 
     def copy_blocks(self, pairs) -> None:
         """Copy-on-write copies (old, new) in every layer's cache."""

@@ -10,7 +10,10 @@ apply_rotary_pos_emb and paged_kv_store (nanoPD/engine/model_runner.py:97-115,
 - HF's rotation, which rounds cos / sin and each product to the storage dtype:
   within a few ulps.
 V rows are copied, so the V cache must match bit for bit; slots that are
-negative leave the pool untouched."""
+negative leave the pool untouched. Without norm weights (the Qwen2 / Llama
+prologue: the reference applies q_norm / k_norm only where the attention has
+them, nanoPD/engine/model_runner.py:101-104) the same composites without the
+norm step."""
 import pytest
 import torch
 
@@ -59,9 +62,11 @@ def _case(device, dtype, T, H, KV, num_blocks, bs, pad=0, seed=0, max_pos=40000,
     return qkv, qw, kw, slots, pos, inv_freq
 
 
-def _run(device, dtype, T, H, KV, num_blocks=64, bs=16, pad=0, seed=0, D=D):
+def _run(device, dtype, T, H, KV, num_blocks=64, bs=16, pad=0, seed=0, D=D, norms=True):
     qkv, qw, kw, slots, pos, inv_freq = _case(device, dtype, T, H, KV, num_blocks, bs, pad, seed,
                                               D=D)
+    if not norms:
+        qw = kw = None
     sentinel = torch.tensor(7.0, dtype=dtype)
     kc = torch.full((num_blocks, KV, bs, D), float(sentinel), dtype=dtype, device=device)
     vc = kc.clone()
@@ -74,7 +79,10 @@ def _run(device, dtype, T, H, KV, num_blocks=64, bs=16, pad=0, seed=0, D=D):
     qs = qkv[:, : H * D].reshape(T, H, D)
     ks = qkv[:, H * D:(H + KV) * D].reshape(T, KV, D)
     vs = qkv[:, (H + KV) * D:].reshape(T, KV, D)
-    qn, kn = hf_rms_norm(qs, qw, 1e-6), hf_rms_norm(ks, kw, 1e-6)
+    if norms:
+        qn, kn = hf_rms_norm(qs, qw, 1e-6), hf_rms_norm(ks, kw, 1e-6)
+    else:
+        qn, kn = qs, ks
     ref = {"fp32": (rope_fp32(qn, cos, sin), rope_fp32(kn, cos, sin)),
            "hf": (rope_hf(qn, cos, sin), rope_hf(kn, cos, sin))}
     keep = slots >= 0
@@ -133,6 +141,31 @@ def test_head_dims_64_and_256(device, dtype, hd, T, H, KV, pad):
     print(f"qk_norm_rope_store D={hd} dtype={dtype} T={T} H={H} KV={KV} pad={pad}", flush=True)
     res, kc, vc, vref = _run(device, dtype, T, H, KV, pad=pad, seed=T + H + hd, D=hd)
     _check(res, kc, vc, vref, dtype, hd)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("hd", [64, 128, 256])
+@pytest.mark.parametrize("T,H,KV,pad", [(1, 12, 2, 0), (45, 12, 2, 0), (300, 12, 2, 64),
+                                        (129, 32, 8, 0)])
+def test_norm_free_matches_composites(device, dtype, hd, T, H, KV, pad):
+    """No q/k norm weights: RoPE of the projection output (12 / 2 heads is
+    configuration 1's Qwen2-1.5B shape)."""
+    print(f"rope_store (no norms) D={hd} dtype={dtype} T={T} H={H} KV={KV} pad={pad}", flush=True)
+    res, kc, vc, vref = _run(device, dtype, T, H, KV, pad=pad, seed=T + H + hd + 1, D=hd,
+                             norms=False)
+    _check(res, kc, vc, vref, dtype, hd)
+
+
+def test_one_norm_weight_is_refused(device):
+    dtype = torch.bfloat16
+    kc = torch.zeros(4, 2, 16, D, dtype=dtype, device=device)
+    q = torch.empty(3, 12, D, dtype=dtype, device=device)
+    qkv = torch.zeros(3, 16 * D, dtype=dtype, device=device)
+    i32 = torch.zeros(3, dtype=torch.int32, device=device)
+    w = torch.ones(D, dtype=dtype, device=device)
+    f = torch.ones(D // 2, device=device)
+    with pytest.raises(RuntimeError, match="both norm weights"):
+        pk.qk_norm_rope_store(q, kc, kc.clone(), qkv, i32, i32, f, w, None, 1e-6)
 
 
 def test_untouched_slots_and_empty(device):
