@@ -373,9 +373,12 @@ __global__ __launch_bounds__(64) void decode_partition_kernel(DecodeArgs a) {
   __syncthreads();
 
   // ---------------- pass 3: probabilities x V ----------------
-  float acc[G][8];
+  // (units of more than 8 heads keep O only in the MFMA accumulators and
+  // hand it over through LDS at the end: acc is for groups of up to 8)
+  constexpr int GA = G <= 8 ? G : 1;
+  float acc[GA][8];
 #pragma unroll
-  for (int h = 0; h < G; ++h)
+  for (int h = 0; h < GA; ++h)
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[h][d] = 0.f;
   for (int st = 0; st < nsteps; ++st) {
@@ -404,7 +407,7 @@ __global__ __launch_bounds__(64) void decode_partition_kernel(DecodeArgs a) {
       for (int c = 0; c < 4; ++c) {
         const float f0 = TT::lo(w[c]), f1 = TT::hi(w[c]);
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
+        for (int h = 0; h < GA; ++h) {
           acc[h][2 * c] = fmaf(p[h], f0, acc[h][2 * c]);
           acc[h][2 * c + 1] = fmaf(p[h], f1, acc[h][2 * c + 1]);
         }
@@ -723,17 +726,28 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int64_t slo
 // Head-group sizes from which 2-byte pools (head dim 128) run pass 3 on the
 // matrix cores: below it the fp32 VALU products keep up with HBM.
 constexpr int kMmaPvMinG = 5;
-__host__ __device__ constexpr bool mma_pv_2byte(int d, int g) { return d == 128 && g >= kMmaPvMinG; }
+__host__ __device__ constexpr bool mma_pv_2byte(int d, int g) {
+  return d == 128 && g >= kMmaPvMinG && g <= 8;
+}
+// Groups of more than 8 heads in one unit (16 per unit, head dim 128): both
+// passes on the matrix cores, as FP8 pools run them, since the v_mfma_f32_16x16x16
+// tiles that pad a group to 16 heads serve 16 heads as cheaply as 8, and the
+// kv head's K/V rows are read once instead of once per 8-head sub-group.
+constexpr int kWideGroup = 16;
+__host__ __device__ constexpr bool mma_passes(bool fp8, int g) { return fp8 || g > 8; }
 // Floats of the fast path's score region for t tokens (incl. ring padding):
-// FP8 pools' pass 3 stages its 16 x kVRow V tile there; 2-byte pools with an
-// MFMA pass 3 keep their 2-byte probabilities in its first half and the V
-// tile after them.
-__host__ __device__ constexpr int fast_score_floats(int t, int gp, bool fp8, bool mma_pv = false) {
-  return fp8 ? (t * gp < 16 * kVRow / 2 ? 16 * kVRow / 2 : t * gp)
+// the MFMA passes' pass 3 stages its 16 x kVRow V tile there, and the O^T
+// hand-off after pass 3 needs G x D floats of it; 2-byte pools with an MFMA
+// pass 3 keep their 2-byte probabilities in its first half and the V tile
+// after them.
+__host__ __device__ constexpr int fast_score_floats(int t, int gp, bool mma, bool mma_pv = false,
+                                                    int g = 8, int d = 128) {
+  return mma ? (t * gp < (16 * kVRow / 2 > g * d ? 16 * kVRow / 2 : g * d)
+                    ? (16 * kVRow / 2 > g * d ? 16 * kVRow / 2 : g * d) : t * gp)
              : mma_pv ? (t * gp < t * gp / 2 + 16 * kVRow / 2 ? t * gp / 2 + 16 * kVRow / 2 : t * gp)
                       : t * gp;
 }
-// Bytes of FP8 pools' probability region ([GP][t] 2-byte values): pass 1
+// Bytes of the MFMA passes' probability region ([GP][t] 2-byte values): pass 1
 // stages its 16 x kKRow K tile there first.
 __host__ __device__ constexpr int fast_prob_bytes(int t, int gp) {
   return t * gp * 2 < 16 * kKRow * 2 ? 16 * kKRow * 2 : t * gp * 2;
@@ -787,14 +801,16 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
   constexpr int NTS = NH > LGP ? NH - LGP : 0;   // token bits split by stages
   constexpr int BS = 16 * SPB;
   constexpr int NBUF = ring_of(D);      // steps in flight per pass
-  // pass 3 on the matrix cores for FP8 pools (2-byte probabilities, V staged
-  // in LDS as TT; their short partitions leave LDS room for both), else on
-  // the VALU with fp32 probabilities
-  constexpr bool kMma = kF8;
-  // 2-byte pools with large groups: pass 3 on the matrix cores too, with the
+  // passes 1 and 3 on the matrix cores for FP8 pools and for units of more
+  // than 8 heads (2-byte probabilities, K and V staged in LDS as TT; their
+  // short partitions leave LDS room for both), else on the VALU with fp32
+  // probabilities
+  constexpr bool kMma = mma_passes(kF8, G);
+  static_assert(G <= kWideGroup && (G <= 8 || D == 128), "group sizes of the fast path");
+  // 2-byte pools with 5-8 heads: pass 3 on the matrix cores too, with the
   // probabilities rounded to TT in place (token-major pairs in the first half
   // of the score region) and the V tile after them
-  constexpr bool kMmaPv2 = !kF8 && mma_pv_2byte(D, G);
+  constexpr bool kMmaPv2 = !kMma && mma_pv_2byte(D, G);
   constexpr bool kMmaPv = kMma || kMmaPv2;
   const int tmax = a.partition + 16 * NBUF;   // row of s_pb: tokens incl. ring padding
   constexpr int MAXT = kFastMaxPartition + 16 * NBUF;   // tokens incl. ring padding
@@ -837,8 +853,8 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
 
   // q slot h holds head h ^ headmask of the group (zeros for padding heads;
   // VALU pass 1 only)
-  u32x4 qv[GP];
-  if constexpr (!kF8) {
+  u32x4 qv[kMma ? 1 : GP];
+  if constexpr (!kMma) {
     const uint16_t* qb = a.q + s * a.q_stride_seq + (kh * G) * a.q_stride_head + j * 8;
 #pragma unroll
     for (int h = 0; h < GP; ++h) {
@@ -1047,9 +1063,12 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
   __syncthreads();
 
   // ---------------- pass 3: probabilities x V ----------------
-  float acc[G][8];
+  // (units of more than 8 heads keep O only in the MFMA accumulators and
+  // hand it over through LDS at the end: acc is for groups of up to 8)
+  constexpr int GA = G <= 8 ? G : 1;
+  float acc[GA][8];
 #pragma unroll
-  for (int h = 0; h < G; ++h)
+  for (int h = 0; h < GA; ++h)
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[h][d] = 0.f;
   constexpr int NOB = kMmaPv ? D / 16 : 1;   // 16-dim blocks of O^T (MFMA path)
@@ -1113,7 +1132,7 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
       for (int c = 0; c < 4; ++c) {
         const float f0 = TT::lo(w[c]), f1 = TT::hi(w[c]);
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
+        for (int h = 0; h < GA; ++h) {
           acc[h][2 * c] = fmaf(p[h], f0, acc[h][2 * c]);
           acc[h][2 * c + 1] = fmaf(p[h], f1, acc[h][2 * c + 1]);
         }
@@ -1134,17 +1153,51 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
 #pragma unroll
     for (int b = 0; b < NBUF; ++b) pv_step(vb[b], st0 + b);
   }
+  // the unit's O through LDS (MFMA pass 3): O^T blocks (lane (g4, n16): dims
+  // nb*16 + 4*g4 .. +3 of head n16) -> s_o[h][D], read back below per (head,
+  // 8-dim chunk). The staged V tile is no longer read; the region holds G x D
+  // floats (fast_score_floats)
+  float* s_o = reinterpret_cast<float*>(s_vt);
   if constexpr (kMmaPv) {
-    // O^T blocks (lane (g4, n16): dims nb*16 + 4*g4 .. +3 of head n16) ->
-    // acc[h][8] of dims j*8 .. +7 in every row of the wave, through LDS (the
-    // staged V tile is no longer read: G x D floats <= its 16 x kVRow x 2 bytes)
-    float* s_o = reinterpret_cast<float*>(s_vt);
     if (n16 < G) {
 #pragma unroll
       for (int nb = 0; nb < NOB; ++nb) *reinterpret_cast<f32x4*>(&s_o[n16 * D + nb * 16 + 4 * g4]) = oacc[nb];
     }
+  }
+  if constexpr (G > 8) {
+    // 16-head units: row r of the wave (TPL rows of LPT lanes) writes heads
+    // r, r + TPL, ... straight from s_o, to the output or as a partial
+    const int64_t base_p = nparts == 1 ? -1 : (int64_t)unit * a.max_parts + part;
+    const bool grouped1 = a.max_groups > 0 && nparts > kMergeGroup;
+    const int gq = part / kMergeGroup;
+    const int64_t base = base_p < 0 ? -1
+        : (grouped1 && min(kMergeGroup, nparts - gq * kMergeGroup) == 1
+               ? (int64_t)a.num_seqs * a.num_kv_heads * a.max_parts + (int64_t)unit * a.max_groups + gq
+               : base_p);
 #pragma unroll
     for (int h = 0; h < G; ++h) {
+      if ((h % TPL) != r) continue;
+      const f32x4 lo = *reinterpret_cast<const f32x4*>(&s_o[h * D + j * 8]);
+      const f32x4 hi = *reinterpret_cast<const f32x4*>(&s_o[h * D + j * 8 + 4]);
+      const float o[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+      if (base < 0) {
+        store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + j * 8, o,
+                       out_scale / l[h]);
+      } else {
+        float* dst = a.part_acc + (base * G + h) * D + j * 2;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) st_coherent2(dst + k * (2 * LPT), o[2 * k], o[2 * k + 1]);
+      }
+    }
+    if (base < 0) return;
+    if (lane == 0) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) st_coherent2(a.part_ml + (base * G + h) * 2, m[h], l[h]);
+    }
+  } else {
+  if constexpr (kMmaPv) {
+#pragma unroll
+    for (int h = 0; h < GA; ++h) {
       const f32x4 lo = *reinterpret_cast<const f32x4*>(&s_o[h * D + j * 8]);
       const f32x4 hi = *reinterpret_cast<const f32x4*>(&s_o[h * D + j * 8 + 4]);
       acc[h][0] = lo.x; acc[h][1] = lo.y; acc[h][2] = lo.z; acc[h][3] = lo.w;
@@ -1156,7 +1209,7 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
   // with both operands x hand every lane {x, x of lane ^ 16} (^ 32) in some
   // order
 #pragma unroll
-  for (int h = 0; h < G; ++h)
+  for (int h = 0; h < GA; ++h)
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
       float y = acc[h][d];
@@ -1175,11 +1228,12 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
   if (nparts == 1) {
     if (lane < LPT) {
 #pragma unroll
-      for (int h = 0; h < G; ++h)
+      for (int h = 0; h < GA; ++h)
         store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + j * 8,
                        acc[h], out_scale / l[h]);
     }
     return;
+  }
   }
   // Several partitions: publish this one's partial, then the last wave of the
   // (sequence, kv-head) to arrive merges them all and resets the counter.
@@ -1206,10 +1260,10 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
   const int gsize = min(kMergeGroup, nparts - g * kMergeGroup);
   const int64_t gbase =
       (int64_t)a.num_seqs * a.num_kv_heads * a.max_parts + (int64_t)unit * a.max_groups;
-  {
+  if constexpr (G <= 8) {
     const int64_t base = grouped && gsize == 1 ? gbase + g : ubase + part;
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
+    for (int h = 0; h < GA; ++h) {
       if ((h % TPL) != r) continue;
       float* dst = a.part_acc + (base * G + h) * D + j * 2;
 #pragma unroll
@@ -1267,9 +1321,10 @@ template <class TT, int D, int G, int SPB, bool kF8>
 // FP8 pools with up to 4 heads per group: at most 128 VGPRs, four waves per
 // SIMD (the MFMA pass 3 would otherwise take the kernel to 148). Head dim 128
 // with 5-8 heads per group: at most 168, three waves per SIMD (1-4% faster
-// than 8 waves per CU at 180-212).
+// than 8 waves per CU at 180-212). 16-head units: at most 256 (their LDS
+// allows 5 waves per CU).
 __global__ __launch_bounds__(64)
-__attribute__((amdgpu_waves_per_eu(kF8 && G <= 4 ? 4 : (D == 128 && G >= 5 && G <= 8 ? 3 : 1))))
+__attribute__((amdgpu_waves_per_eu(kF8 && G <= 4 ? 4 : (D == 128 && G >= 5 && G <= 8 ? 3 : (G > 8 ? 2 : 1)))))
 void decode_fast_kernel(DecodeArgs a) {
   constexpr int GP = pow2ceil(G);
   extern __shared__ __attribute__((aligned(16))) float s_dyn[];
@@ -1278,8 +1333,10 @@ void decode_fast_kernel(DecodeArgs a) {
   // scores; pass 3's [16][kVRow] V tile reuses the scores' region (no longer
   // read once the probabilities are out), which is sized to hold it
   const int tpad = a.partition + 16 * ring_of(D);
-  uint16_t* s_pb = kF8 ? reinterpret_cast<uint16_t*>(s_dyn + fast_score_floats(tpad, GP, kF8)) : nullptr;
-  uint16_t* s_v = kF8 ? reinterpret_cast<uint16_t*>(s_dyn) : nullptr;
+  constexpr bool kMma = mma_passes(kF8, G);
+  uint16_t* s_pb =
+      kMma ? reinterpret_cast<uint16_t*>(s_dyn + fast_score_floats(tpad, GP, true, false, G, D)) : nullptr;
+  uint16_t* s_v = kMma ? reinterpret_cast<uint16_t*>(s_dyn) : nullptr;
   int unit, part, ps = a.partition;
   if (a.num_seqs <= kInlineSchedMax) {
     // Small batch: every workgroup derives its item from seq_lens alone, in
@@ -1553,8 +1610,9 @@ int64_t fast_grid(const DecodeArgs& a, int64_t units) {
 int64_t fast_lds_bytes(int partition, int g, bool fp8, int d) {
   const int t = partition + 16 * ring_of(d);
   const int gp = pow2ceil(g);
-  return (int64_t)fast_score_floats(t, gp, fp8, mma_pv_2byte(d, g)) * 4 +
-         (fp8 ? fast_prob_bytes(t, gp) : 0);
+  const bool mma = mma_passes(fp8, g);
+  return (int64_t)fast_score_floats(t, gp, mma, mma_pv_2byte(d, g), g, d) * 4 +
+         (mma ? fast_prob_bytes(t, gp) : 0);
 }
 
 template <class TT, int D, int G, int SPB, bool kF8 = false>
@@ -1568,7 +1626,7 @@ int launch_fast_bs(const DecodeArgs& a, int num_seqs, int64_t max_items, hipStre
 
 template <class TT, int D, int G>
 int launch_fast(const DecodeArgs& a, int num_seqs, int64_t max_items, hipStream_t st) {
-  if constexpr (D != 128) {   // block sizes 16 and 32 (use_fast_path)
+  if constexpr (D != 128 || G > 8) {   // block sizes 16 and 32 (use_fast_path, wide_group)
     if (a.block_size == 16) return launch_fast_bs<TT, D, G, 1>(a, num_seqs, max_items, st);
     return launch_fast_bs<TT, D, G, 2>(a, num_seqs, max_items, st);
   } else {
@@ -1601,6 +1659,7 @@ int dispatch_fp8(int g, const DecodeArgs& a, int64_t units, hipStream_t st) {
     case 5: launch_fast_fp8<TT, 5>(a, ns, mi, st); break;
     case 6: launch_fast_fp8<TT, 6>(a, ns, mi, st); break;
     case 7: launch_fast_fp8<TT, 7>(a, ns, mi, st); break;
+    case kWideGroup: launch_fast_fp8<TT, kWideGroup>(a, ns, mi, st); break;
     default: launch_fast_fp8<TT, 8>(a, ns, mi, st); break;
   }
   return npd::check_launch("npd_paged_attention_fp8");
@@ -1632,11 +1691,17 @@ int launch_decode(const DecodeArgs& a, int64_t units, hipStream_t st) {
     if (rc != NPD_OK) return rc;
     return npd::check_launch("npd_paged_attention");
   }
-  return launch_generic<TT, G>(a, units, st);
+  if constexpr (G > 8)   // kv_split_of forms 16-head units on the fast path only
+    return npd::fail(NPD_E_INVALID, "npd_paged_attention: no kernel for %d-head units here", G);
+  else
+    return launch_generic<TT, G>(a, units, st);
 }
 
 template <class TT, int D>
 int dispatch_g(int g, const DecodeArgs& a, int64_t units, hipStream_t st) {
+  if constexpr (D == 128) {
+    if (g == kWideGroup) return launch_decode<TT, 128, kWideGroup>(a, units, st);
+  }
   switch (g) {
     case 1: return launch_decode<TT, D, 1>(a, units, st);
     case 2: return launch_decode<TT, D, 2>(a, units, st);
@@ -1673,12 +1738,18 @@ int dispatch_d(int64_t d, int g, const DecodeArgs& a, int64_t units, hipStream_t
   }
 }
 
-// Work units per pool kv head. The kernels keep a group's queries and
-// accumulators in registers for at most 8 query heads: a larger group is
-// served as kv_split equal groups of at most 8 heads (the smallest such
-// split), each reading the kv head's K/V once.
-int kv_split_of(int64_t num_heads, int64_t num_kv_heads) {
+// Work units per pool kv head. Groups that are a multiple of 16 heads at head
+// dim 128 with blocks of 16 or 32 (the fast path) run as units of 16 heads,
+// whose passes run on the matrix cores and read each K/V row once. Otherwise
+// the kernels keep a group's queries and accumulators in registers for at
+// most 8 query heads: a larger group is served as kv_split equal groups of
+// at most 8 heads (the smallest such split), each reading the kv head's K/V.
+int kv_split_of(int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
+                int64_t num_seqs) {
   const int64_t g = num_kv_heads > 0 ? num_heads / num_kv_heads : 1;
+  if (g > 8 && g % kWideGroup == 0 && head_dim == 128 && (block_size == 16 || block_size == 32) &&
+      use_fast_path(head_dim, block_size, num_seqs))
+    return (int)(g / kWideGroup);
   int64_t k = 1;
   while (k < g && (g / k > 8 || g % k != 0)) ++k;
   return (int)k;
@@ -1701,7 +1772,7 @@ extern "C" int64_t npd_paged_attention_workspace_size(int64_t num_seqs, int64_t 
   if (num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
       max_blocks_per_seq <= 0)
     return 0;
-  num_kv_heads *= kv_split_of(num_heads, num_kv_heads);   // kv heads of the work units
+  num_kv_heads *= kv_split_of(num_heads, num_kv_heads, head_dim, block_size, num_seqs);   // units' kv heads
   const int64_t max_ctx = block_size * max_blocks_per_seq;
   if (!use_fast_path(head_dim, block_size, num_seqs)) {
     const int ps =
@@ -1755,7 +1826,7 @@ int attention_check(const void* out, const void* query, const void* key_cache,
     return fail(NPD_E_INVALID, "%s: num_heads %lld is not a multiple of num_kv_heads %lld", name,
                 (long long)num_heads, (long long)num_kv_heads);
   // the work units' kv heads and group size (groups above 8 heads are split)
-  const int split = kv_split_of(num_heads, num_kv_heads);
+  const int split = kv_split_of(num_heads, num_kv_heads, head_dim, block_size, num_seqs);
   const int64_t pool_kv_heads = num_kv_heads;
   num_kv_heads *= split;
   if (head_dim < 32 || head_dim > 256 || head_dim % 8 != 0)
@@ -1820,7 +1891,7 @@ int attention_impl(void* out, const void* query, const void* key_cache, const vo
                                    name);
     if (rc != NPD_OK || num_seqs == 0) return rc;
   }
-  const int split = kv_split_of(num_heads, num_kv_heads);
+  const int split = kv_split_of(num_heads, num_kv_heads, head_dim, block_size, num_seqs);
   const int64_t pool_kv_heads = num_kv_heads;
   num_kv_heads *= split;
   const int64_t g = num_heads / num_kv_heads;

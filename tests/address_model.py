@@ -58,11 +58,21 @@ def fast_prob_bytes(t: int, gp: int) -> int:
 MMA_PV_MIN_G = 5   # kMmaPvMinG: 2-byte pools at head dim 128 from this group size
 
 
-def fast_score_floats(t: int, gp: int, fp8: bool, mma_pv: bool = False) -> int:
-    """fast_score_floats: the score region; at least the FP8 V tile, and for
-    a 2-byte MFMA pass 3 the in-place probabilities plus the V tile."""
-    if fp8:
-        return 16 * V_ROW // 2 if t * gp < 16 * V_ROW // 2 else t * gp
+WIDE_GROUP = 16    # kWideGroup: heads of a unit whose passes both run on the matrix cores
+
+
+def mma_passes(fp8: bool, g: int) -> bool:
+    """mma_passes: passes 1 and 3 on the matrix cores (FP8 pools, 16-head units)."""
+    return fp8 or g > 8
+
+
+def fast_score_floats(t: int, gp: int, mma: bool, mma_pv: bool = False, g: int = 8,
+                      d: int = 128) -> int:
+    """fast_score_floats: the score region; for the MFMA passes at least the
+    V tile and the G x D floats of the O hand-off, and for a 2-byte MFMA pass 3
+    the in-place probabilities plus the V tile."""
+    if mma:
+        return max(t * gp, 16 * V_ROW // 2, g * d)
     if mma_pv:
         return max(t * gp, t * gp // 2 + 16 * V_ROW // 2)
     return t * gp
@@ -229,10 +239,14 @@ def fast_min_partition(ps: int, bs: int, fp8: bool) -> int:
     return min(lo, ps)
 
 
-def kv_split_of(H: int, KV: int) -> int:
-    """decode_attention.hip kv_split_of: groups of more than 8 query heads are
-    served as the smallest number of equal groups of at most 8."""
+def kv_split_of(H: int, KV: int, D: int = 128, bs: int = 16, S: int = 1) -> int:
+    """decode_attention.hip kv_split_of: groups that are a multiple of 16 heads
+    (head dim 128, blocks of 16 or 32, the fast path) run as 16-head units;
+    other groups of more than 8 query heads as the smallest number of equal
+    groups of at most 8."""
     g = H // KV
+    if g > 8 and g % WIDE_GROUP == 0 and D == 128 and bs in (16, 32) and use_fast_path(D, bs, S):
+        return g // WIDE_GROUP
     k = 1
     while k < g and (g // k > 8 or g % k):
         k += 1
@@ -276,7 +290,7 @@ class DecodeLaunch:
 def decode_host(S, H, KV, bs, max_bps, fp8, D=128) -> DecodeLaunch:
     """The host choices of attention_impl (decode_attention.hip:1441-1511)."""
     assert use_fast_path(D, bs, S), "model covers the fast path"
-    split = kv_split_of(H, KV)
+    split = kv_split_of(H, KV, D, bs, S)
     KV *= split
     L = DecodeLaunch(S, H, KV, bs, max_bps, fp8, split)
     max_ctx = bs * max_bps
@@ -297,8 +311,10 @@ def decode_host(S, H, KV, bs, max_bps, fp8, D=128) -> DecodeLaunch:
     L.grid = n
     gp = pow2ceil(G)
     t = L.partition + 16 * ring_of(D)
-    mma_pv = D == 128 and G >= MMA_PV_MIN_G
-    L.lds_floats = fast_score_floats(t, gp, fp8, mma_pv) + (fast_prob_bytes(t, gp) // 4 if fp8 else 0)
+    mma = mma_passes(fp8, G)
+    mma_pv = D == 128 and MMA_PV_MIN_G <= G <= 8
+    L.lds_floats = (fast_score_floats(t, gp, mma, mma_pv, G, D)
+                    + (fast_prob_bytes(t, gp) // 4 if mma else 0))
     return L
 
 
@@ -447,9 +463,9 @@ def decode(W: Writes, L: DecodeLaunch, out: Buf, ws: Buf, seq_lens: np.ndarray,
     nsteps = _ceil(_ceil(np.maximum(ntok, 0), 16), ring) * ring
     if run.any():
         W.index(nsteps[run] * 16 * gp - 1, L.partition * gp + 16 * ring * gp, "decode LDS scores")
-        if L.fp8:
+        if mma_passes(L.fp8, L.G):
             tpad = L.partition + 16 * ring
-            pb0 = fast_score_floats(tpad, gp, True) * 4   # bytes
+            pb0 = fast_score_floats(tpad, gp, True, False, L.G, D) * 4   # bytes
             W.index(pb0 + 2 * ((L.G - 1) * tpad + nsteps[run] * 16 - 1) + 1, L.lds_floats * 4,
                     "decode LDS probabilities (bytes)")
             # pass 1's K tile reuses the probability region
@@ -460,7 +476,7 @@ def decode(W: Writes, L: DecodeLaunch, out: Buf, ws: Buf, seq_lens: np.ndarray,
             # the V tile and the O exchange reuse the score region
             W.index([2 * (15 * V_ROW + 127) + 1, 4 * L.G * D - 1], pb0,
                     "decode LDS V tile / O exchange in the score region (bytes)")
-        elif D == 128 and L.G >= MMA_PV_MIN_G:
+        elif D == 128 and MMA_PV_MIN_G <= L.G <= 8:
             # MFMA pass 3 of 2-byte pools: probabilities in place as pairs
             # (word t * GP/2 + k), then the V tile / O exchange after them
             tpad = L.partition + 16 * ring

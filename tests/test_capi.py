@@ -82,10 +82,16 @@ def test_c_validation_paths_need_no_gpu():
     rc = _rc("npd_paged_attention", fake, fake, fake, fake, fake, fake, 2, 12, 5, 128, 64, 16, 4,
              ctypes.c_float(0.1), 1536, 128, 1536, 128, None, 0, 1, None)
     assert rc == -1 and b"multiple" in lib.npd_last_error()
-    # a group of 16 q-heads per kv head is accepted (served as two groups of
-    # 8): validation gets as far as the missing workspace, sized for 4 units
-    need = lib.npd_paged_attention_workspace_size(2, 32, 2, 128, 16, 4)
-    assert need == lib.npd_paged_attention_workspace_size(2, 32, 4, 128, 16, 4)
+    # a group of 16 q-heads per kv head is accepted: at head dim 64 it is
+    # served as two groups of 8 (a workspace sized for 4 units), at head dim
+    # 128 with blocks of 16 as one 16-head unit per kv head (2 units, 256-token
+    # partitions: 16 x 256 scores); validation gets as far as the missing
+    # workspace
+    need = lib.npd_paged_attention_workspace_size(2, 32, 2, 64, 16, 4)
+    assert need == lib.npd_paged_attention_workspace_size(2, 32, 4, 64, 16, 4)
+    wide = lib.npd_paged_attention_workspace_size(2, 32, 2, 128, 16, 4)
+    # (4 units: too few items for longer partitions -> 64 tokens, 1 slot each)
+    assert wide == (2**20 + 16 + 2 * 2 * 1 * 8 + 255) // 256 * 256 + 2 * 32 * 1 * 130 * 4
     rc = _rc("npd_paged_attention", fake, fake, fake, fake, fake, fake, 2, 32, 2, 128, 64, 16, 4,
              ctypes.c_float(0.1), 4096, 128, 4096, 128, None, 0, 1, None)
     assert rc == -4 and b"workspace" in lib.npd_last_error()

@@ -124,13 +124,46 @@ def test_group_sizes_and_head_dims(device, dtype, D, G):
 def test_group_sizes_above_8(device, dtype, G, kvh):
     """More than 8 query heads per kv head (e.g. 64 q / 4 kv heads): the kv
     head of q-head h is still h // G (PA/csrc/attention/
-    paged_attention_kernel.cu:62); the op serves the group as equal
-    sub-groups of at most 8 heads. Contexts up to 32k tokens (two-level
-    merges), an empty sequence and a one-token one."""
+    paged_attention_kernel.cu:62); the op serves the group as 16-head units
+    (G = 16) or as equal sub-groups of at most 8 heads (G = 9, 11, 12).
+    Contexts up to 32k tokens (two-level merges), an empty sequence and a
+    one-token one."""
     lens = [1, 17, 300, 4097, 32768, 0]
     args = make_inputs(len(lens), G * kvh, kvh, 128, lens, 16, dtype, device, seed=G * 10 + kvh)
     q, kc, vc, bt, sl, scale, mb = args
     check(run(*args, 16), q, kc, vc, bt, sl, scale)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("G,kvh,bs", [(16, 2, 16), (16, 1, 32), (32, 2, 16), (48, 1, 32)])
+def test_sixteen_head_units(device, dtype, G, kvh, bs):
+    """Groups that are a multiple of 16 heads at head dim 128 with blocks of
+    16 or 32 run as 16-head units (both passes on the matrix cores, each K/V
+    row read once per unit): G = 16, 32 (two units per kv head) and 48.
+    Contexts up to 32k (two-level merges), an empty and a one-token
+    sequence, NaN rows past the last token of a partial block."""
+    lens = [1, 17, 300, 4097, 32768, 0, 1000]
+    print(f"16-head units G={G} kvh={kvh} bs={bs} {dtype}", flush=True)
+    q, kc, vc, bt, sl, scale, mb = make_inputs(len(lens), G * kvh, kvh, 128, lens, bs, dtype,
+                                               device, seed=G * 7 + kvh + bs)
+    for i, n in enumerate(lens):
+        if n % bs:
+            b = int(bt[i, (n - 1) // bs])
+            kc[b, :, n % bs:, :] = float("nan")
+            vc[b, :, n % bs:, :] = float("nan")
+    check(run(q, kc, vc, bt, sl, scale, mb, bs), q, kc, vc, bt, sl, scale)
+
+
+def test_sixteen_head_units_short_contexts(device):
+    """16-head units over few short sequences (the kernel halves the
+    partition while the contexts give too few items) and config 2's contexts
+    with 128 query heads over its 8 kv heads."""
+    g = torch.Generator().manual_seed(128)
+    for lens in ([33, 250, 9, 1000], torch.randint(128, 4097, (64,), generator=g).tolist()):
+        args = make_inputs(len(lens), 16 * 8, 8, 128, lens, 16, torch.bfloat16, device,
+                           seed=len(lens))
+        q, kc, vc, bt, sl, scale, mb = args
+        check(run(*args, 16), q, kc, vc, bt, sl, scale)
 
 
 @pytest.mark.parametrize("D,bs", [(64, 8), (256, 8), (128, 8)])

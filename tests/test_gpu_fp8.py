@@ -120,10 +120,12 @@ def test_decode_block_sizes_and_long_context(device, bs):
     _run_and_check(device, *args, bs, torch.bfloat16)
 
 
-def test_decode_group_of_16_long_context(device):
-    """16 query heads per kv head over an FP8 pool, up to 32k tokens."""
-    args = _fp8_case(device, [32768, 1, 4097, 0], 64, 4, 16, torch.bfloat16, seed=16)
-    _run_and_check(device, *args, 16, torch.bfloat16)
+@pytest.mark.parametrize("H,kvh,bs", [(64, 4, 16), (32, 1, 32), (96, 3, 16)])
+def test_decode_group_of_16_long_context(device, H, kvh, bs):
+    """16 and 32 query heads per kv head over an FP8 pool (16-head units),
+    up to 32k tokens."""
+    args = _fp8_case(device, [32768, 1, 4097, 0], H, kvh, bs, torch.bfloat16, seed=H + bs)
+    _run_and_check(device, *args, bs, torch.bfloat16)
 
 
 def test_decode_long_context_merge_groups(device):
