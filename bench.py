@@ -315,16 +315,37 @@ def bench_prefill(args, w) -> dict:
     }
 
 
+def sources_sha(paths) -> str:
+    """First 16 hex digits of the SHA-256 of the given repository files, in
+    order: the version of the kernel sources a stored counter reading was
+    taken on."""
+    import hashlib
+    h = hashlib.sha256()
+    for p in paths:
+        with open(os.path.join(ROOT, p), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def _profiled_traffic(key: str):
     """HBM bytes per launch of a kernel, from the committed rocprofv3 counter
     summary (FETCH_SIZE and WRITE_SIZE runs, scaled by a plain copy's counter
-    reading); None where no profile was taken."""
+    reading). Each entry names the kernel sources it was measured on and their
+    hash; when the sources have changed since, the reading is stale and None
+    is returned (as where no profile was taken)."""
     try:
         with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
             rec = json.load(f).get(key)
     except (OSError, ValueError):
         return None
-    return None if rec is None else rec.get("bytes")
+    if rec is None or "sources" not in rec:
+        return None
+    try:
+        if sources_sha(rec["sources"]) != rec.get("sources_sha"):
+            return None
+    except OSError:
+        return None
+    return rec.get("bytes")
 
 
 def bench_e2e(args, dev) -> int:

@@ -88,7 +88,14 @@ constexpr int kStep = 16;            // tokens per step
 constexpr int kRing = NPD_DECODE_RING;   // fast path: K/V steps in flight per wave
 // head dim 64: rows of 128 bytes, half the bytes per step; twice the steps in
 // flight keep the same bytes in flight (and the same ring registers)
-constexpr int ring_of(int d) { return d == 64 ? 2 * kRing : kRing; }
+// 16-head units (more than 8 heads): their LDS leaves room for 5 waves per
+// CU, so each wave keeps twice the steps in flight
+#ifndef NPD_WIDE_RING
+#define NPD_WIDE_RING 2
+#endif
+constexpr int ring_of(int d, int g = 1) {
+  return d == 64 ? 2 * kRing : (g > 8 ? NPD_WIDE_RING * kRing : kRing);
+}
 #ifndef NPD_FAST_MAX_PARTITION
 #define NPD_FAST_MAX_PARTITION 2048
 #endif
@@ -800,7 +807,7 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
   constexpr int HELD = NV >> NH;
   constexpr int NTS = NH > LGP ? NH - LGP : 0;   // token bits split by stages
   constexpr int BS = 16 * SPB;
-  constexpr int NBUF = ring_of(D);      // steps in flight per pass
+  constexpr int NBUF = ring_of(D, G);   // steps in flight per pass
   // passes 1 and 3 on the matrix cores for FP8 pools and for units of more
   // than 8 heads (2-byte probabilities, K and V staged in LDS as TT; their
   // short partitions leave LDS room for both), else on the VALU with fp32
@@ -1332,7 +1339,7 @@ void decode_fast_kernel(DecodeArgs a) {
   // FP8 pools: [GP][partition + ring padding] 2-byte probabilities after the
   // scores; pass 3's [16][kVRow] V tile reuses the scores' region (no longer
   // read once the probabilities are out), which is sized to hold it
-  const int tpad = a.partition + 16 * ring_of(D);
+  const int tpad = a.partition + 16 * ring_of(D, G);
   constexpr bool kMma = mma_passes(kF8, G);
   uint16_t* s_pb =
       kMma ? reinterpret_cast<uint16_t*>(s_dyn + fast_score_floats(tpad, GP, true, false, G, D)) : nullptr;
@@ -1608,7 +1615,7 @@ int64_t fast_grid(const DecodeArgs& a, int64_t units) {
 // pools the 2-byte probabilities (at least pass 1's 16-row K tile, which
 // reuses that region).
 int64_t fast_lds_bytes(int partition, int g, bool fp8, int d) {
-  const int t = partition + 16 * ring_of(d);
+  const int t = partition + 16 * ring_of(d, g);
   const int gp = pow2ceil(g);
   const bool mma = mma_passes(fp8, g);
   return (int64_t)fast_score_floats(t, gp, mma, mma_pv_2byte(d, g), g, d) * 4 +

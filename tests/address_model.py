@@ -78,9 +78,12 @@ def fast_score_floats(t: int, gp: int, mma: bool, mma_pv: bool = False, g: int =
     return t * gp
 
 
-def ring_of(D: int) -> int:
+WIDE_RING = 2      # NPD_WIDE_RING: ring multiple of 16-head units
+
+
+def ring_of(D: int, G: int = 1) -> int:
     """decode_attention.hip ring_of: steps in flight per pass."""
-    return 2 * RING if D == 64 else RING
+    return 2 * RING if D == 64 else (WIDE_RING * RING if G > 8 else RING)
 
 # prefill_attention.hip constants
 KT = 64
@@ -310,7 +313,7 @@ def decode_host(S, H, KV, bs, max_bps, fp8, D=128) -> DecodeLaunch:
         n = _ceil(n, 8 * split) * 8 * split
     L.grid = n
     gp = pow2ceil(G)
-    t = L.partition + 16 * ring_of(D)
+    t = L.partition + 16 * ring_of(D, G)
     mma = mma_passes(fp8, G)
     mma_pv = D == 128 and MMA_PV_MIN_G <= G <= 8
     L.lds_floats = (fast_score_floats(t, gp, mma, mma_pv, G, D)
@@ -459,7 +462,7 @@ def decode(W: Writes, L: DecodeLaunch, out: Buf, ws: Buf, seq_lens: np.ndarray,
     # LDS of the item's passes: scores s_p[tl * GP + h]; FP8 pools: 2-byte
     # probabilities s_pb[h * tpad + tl] and pass 3's V tile / O exchange
     ntok = np.minimum(ctx - part * ps, ps)   # ps: per item
-    ring = ring_of(D)
+    ring = ring_of(D, L.G)
     nsteps = _ceil(_ceil(np.maximum(ntok, 0), 16), ring) * ring
     if run.any():
         W.index(nsteps[run] * 16 * gp - 1, L.partition * gp + 16 * ring * gp, "decode LDS scores")
