@@ -486,6 +486,7 @@ using npd::kDppMirror;
 using npd::kDppRor8;
 using npd::kDppXor1;
 using npd::kDppXor2;
+using npd::lane_f;
 using npd::uniform_f;
 using npd::wave_max_f;
 using npd::wave_max_i;
@@ -603,6 +604,9 @@ using npd::st_coherent2;
 // relative to the merged max, not normalised), written to slot dst; else the
 // normalised rows of (sequence s, kv-head kh) go to the output.
 constexpr int kMergeFlight = 4;
+// MFMA passes: a head's probability reference moves only when a step's max
+// exceeds it by more than this (log2 units), so probabilities stay <= 2^8
+constexpr float kTauDecode = 8.f;
 constexpr int kMergeGroup = 16;   // partitions per first-level merge (long contexts)
 template <class TT, int D, int G>
 __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int64_t slot0, int nparts,
@@ -743,21 +747,29 @@ __host__ __device__ constexpr bool mma_pv_2byte(int d, int g) {
 constexpr int kWideGroup = 16;
 __host__ __device__ constexpr bool mma_passes(bool fp8, int g) { return fp8 || g > 8; }
 // Floats of the fast path's score region for t tokens (incl. ring padding):
-// the MFMA passes' pass 3 stages its 16 x kVRow V tile there, and the O^T
-// hand-off after pass 3 needs G x D floats of it; 2-byte pools with an MFMA
-// pass 3 keep their 2-byte probabilities in its first half and the V tile
-// after them.
-__host__ __device__ constexpr int fast_score_floats(int t, int gp, bool mma, bool mma_pv = false,
-                                                    int g = 8, int d = 128) {
-  return mma ? (t * gp < (16 * kVRow / 2 > g * d ? 16 * kVRow / 2 : g * d)
-                    ? (16 * kVRow / 2 > g * d ? 16 * kVRow / 2 : g * d) : t * gp)
+// FP8 pools' pass 3 stages its 16 x kVRow V tile there, and the O hand-off
+// after it needs G x D floats of it; 2-byte pools with an MFMA pass 3 keep
+// their 2-byte probabilities in its first half and the V tile after them.
+__host__ __device__ constexpr int fast_score_floats(int t, int gp, bool fp8, bool mma_pv = false) {
+  return fp8 ? (t * gp < 16 * kVRow / 2 ? 16 * kVRow / 2 : t * gp)
              : mma_pv ? (t * gp < t * gp / 2 + 16 * kVRow / 2 ? t * gp / 2 + 16 * kVRow / 2 : t * gp)
                       : t * gp;
 }
-// Bytes of the MFMA passes' probability region ([GP][t] 2-byte values): pass 1
+// Bytes of FP8 pools' probability region ([GP][t] 2-byte values): pass 1
 // stages its 16 x kKRow K tile there first.
 __host__ __device__ constexpr int fast_prob_bytes(int t, int gp) {
   return t * gp * 2 < 16 * kKRow * 2 ? 16 * kKRow * 2 : t * gp * 2;
+}
+// 16-head units form their probabilities in pass 1 (see decode_fast_item).
+__host__ __device__ constexpr bool online_probs(int g) { return g > 8; }
+// LDS of 16-head units: the [GP][t] 2-byte probabilities (pass 1 to pass 3),
+// then a tile region that holds pass 1's 16 x kKRow K tile, pass 3's
+// 16 x kVRow V tile, the G x D floats of the O hand-off after pass 3 and the
+// merge's [64][GP] weights, one after another.
+__host__ __device__ constexpr int online_prob_bytes(int t, int gp) { return (t * gp * 2 + 15) / 16 * 16; }
+__host__ __device__ constexpr int cmax(int a, int b) { return a > b ? a : b; }
+__host__ __device__ constexpr int online_tile_bytes(int g, int gp, int d) {
+  return cmax(cmax(16 * kKRow * 2, 16 * kVRow * 2), cmax(g * d * 4, 64 * gp * 4));
 }
 
 // Element source of the fast path. 2-byte pools: a lane's 8 elements are one
@@ -813,6 +825,8 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
   // short partitions leave LDS room for both), else on the VALU with fp32
   // probabilities
   constexpr bool kMma = mma_passes(kF8, G);
+  // 16-head units: probabilities formed in pass 1 (online_probs)
+  constexpr bool kOnline = online_probs(G);
   static_assert(G <= kWideGroup && (G <= 8 || D == 128), "group sizes of the fast path");
   // 2-byte pools with 5-8 heads: pass 3 on the matrix cores too, with the
   // probabilities rounded to TT in place (token-major pairs in the first half
@@ -909,21 +923,37 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
 
   // ---------------- pass 1: scores ----------------
   float runmax = -INFINITY;   // max of the scores this lane stored (its head: headmask)
-  // FP8 pools: S = Q . K^T on the matrix cores. A = Q[head n16][dims c*16 +
-  // 4*g4 .. +3] (zeros past the group), B = K^T from the step's K rows staged
-  // in LDS (row = token of the step), D[head 4*g4 + i][token n16]: each lane
-  // ends with the scores of 4 heads of one token, no reduce-scatter.
+  // MFMA passes (FP8 pools, 16-head units): S = Q . K^T on the matrix cores.
+  // A = Q[head n16][dims c*16 + 4*g4 .. +3] (zeros past the group), B = K^T
+  // from the step's K rows staged in LDS (row = token of the step),
+  // D[head 4*g4 + i][token n16]: each lane ends with the scores of 4 heads of
+  // one token, no reduce-scatter. FP8 pools with up to 8 heads store the
+  // scores (fp32) for pass 2. 16-head units (kOnline) form the probabilities
+  // in the same step, against a per-head reference that only moves up when a
+  // step's max exceeds it by more than 2^kTauDecode (probabilities <=
+  // 2^kTauDecode, rounded to TT), so they need no fp32 score buffer and no
+  // softmax pass over LDS: that LDS is what held them to 5 waves per CU.
+  // When the reference moves after the first step, the probabilities already
+  // stored for that head are rescaled in LDS (a rare event: the first step's
+  // max is usually within 2^kTauDecode of the partition's). For FP8 pools with
+  // up to 8 heads, which are not held by their LDS, the step's row reductions
+  // cost more than the pass they remove (52.6 against 50.9 us at config 2).
   const int g4 = lane >> 4, n16 = lane & 15;
   constexpr int NQC = kMma ? D / 16 : 1;
   u32x2 qa[NQC];
-  float runmax4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};   // heads 4*g4 + i
+  float mref[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};   // heads 4*g4 + i (row-uniform)
+  float lp[4] = {0.f, 0.f, 0.f, 0.f};   // this lane's sums of its rounded probabilities
   if constexpr (kMma) {
     const uint16_t* qrow = a.q + s * a.q_stride_seq + (kh * G + n16) * a.q_stride_head + 4 * g4;
 #pragma unroll
     for (int c = 0; c < NQC; ++c)
       qa[c] = n16 < G ? *reinterpret_cast<const u32x2*>(qrow + c * 16) : u32x2{0, 0};
   }
-  uint16_t* s_k = s_pb;   // pass 1's K tile (the probabilities come later)
+  // pass 1's K tile: with online probabilities the tile region, which pass
+  // 3's V tile reuses (the probabilities live in s_pb from pass 1 to pass 3);
+  // else the probability region, which pass 2 fills afterwards
+  uint16_t* s_k = kOnline ? s_v : s_pb;
+  float runmax4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};   // stored scores: heads 4*g4 + i
   auto score_step_mma = [&](const raw_t* kraw, int st) {
 #pragma unroll
     for (int i = 0; i < NL; ++i)
@@ -934,14 +964,63 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
       sacc = Mfma16<TT>::mma(qa[c], *reinterpret_cast<const u32x2*>(&s_k[n16 * kKRow + c * 16 + 4 * g4]),
                              sacc);
     const int tl = st * 16 + n16;
+    if constexpr (!kOnline) {
+      // scores to LDS; pass 2 forms the probabilities against the exact maxima
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int h = 4 * g4 + i;
+        if (h < G) {
+          // rows past the context may hold anything: select, not scale
+          const float sv = (tl < ntok) ? sacc[i] * score_scale : -INFINITY;
+          s_p[tl * GP + h] = sv;
+          runmax4[i] = fmaxf(runmax4[i], sv);
+        }
+      }
+      return;
+    }
+    float sv[4], f[4];
+    bool moved = false;   // a reference of this lane's heads moved after earlier probabilities
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // rows past the context may hold anything: select, not scale
+      sv[i] = (tl < ntok) ? sacc[i] * score_scale : -INFINITY;
+      // the step's max over the row's 16 tokens (DPP within the 16-lane row)
+      float x = sv[i];
+      x = fmaxf(x, dpp<kDppXor1>(x));
+      x = fmaxf(x, dpp<kDppXor2>(x));
+      x = fmaxf(x, dpp<kDppHalfMirror>(x));
+      x = fmaxf(x, dpp<kDppMirror>(x));
+      const bool up = x > mref[i] + kTauDecode;
+      f[i] = 1.f;
+      if (up) {
+        f[i] = mref[i] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mref[i] - x);
+        moved = moved || (mref[i] != -INFINITY);
+        lp[i] *= f[i];
+        mref[i] = x;
+      }
+    }
+    if (__ballot(moved) != 0) {
+      // rare: rescale the probabilities already stored for the heads whose
+      // reference moved (tokens of the earlier steps)
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float fh = lane_f(f[h % 4], 16 * (h / 4));
+        if (fh != 1.f) {
+          for (int t = lane; t < st * 16; t += 64) {
+            uint16_t* pp = &s_pb[h * tmax + t];
+            *pp = (uint16_t)TT::from_float(TT::lo(*pp) * fh);
+          }
+        }
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int h = 4 * g4 + i;
+      const float ref = mref[i] == -INFINITY ? 0.f : mref[i];
+      const uint32_t u = TT::from_float(__builtin_amdgcn_exp2f(sv[i] - ref));
       if (h < G) {
-        // rows past the context may hold anything: select, not scale
-        const float sv = (tl < ntok) ? sacc[i] * score_scale : -INFINITY;
-        s_p[tl * GP + h] = sv;
-        runmax4[i] = fmaxf(runmax4[i], sv);
+        s_pb[h * tmax + tl] = (uint16_t)u;
+        lp[i] += TT::lo(u);
       }
     }
   };
@@ -1008,18 +1087,31 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
 
   // ---------------- pass 2: softmax statistics over the partition ----------------
   // the maxima come from pass 1's running maxima (DPP wave reductions, one
-  // per head over the lanes that stored that head's scores)
+  // per head over the lanes that stored that head's scores); the MFMA passes
+  // have their references and probability sums from pass 1 already
   float m[GP], l[GP];
 #pragma unroll
   for (int h = 0; h < GP; ++h) {
-    if constexpr (kMma)
+    if constexpr (kOnline) {
+      float lr = lp[h % 4];   // the row's sum of head h's probabilities
+      lr += dpp<kDppXor1>(lr);
+      lr += dpp<kDppXor2>(lr);
+      lr += dpp<kDppHalfMirror>(lr);
+      lr += dpp<kDppMirror>(lr);
+      m[h] = h < G ? lane_f(mref[h % 4], 16 * (h / 4)) : -INFINITY;
+      l[h] = h < G ? lane_f(lr, 16 * (h / 4)) : 0.f;
+    } else if constexpr (kMma) {
       m[h] = h < G ? wave_max_f(g4 == h / 4 ? runmax4[h % 4] : -INFINITY) : -INFINITY;
-    else
+      l[h] = 0.f;
+    } else {
       m[h] = h < G ? wave_max_f(headmask == h ? runmax : -INFINITY) : -INFINITY;
-    l[h] = 0.f;
+      l[h] = 0.f;
+    }
   }
   const int ntl = nsteps * 16;
-  if constexpr (kMma) {
+  if constexpr (kOnline) {
+    // nothing left to do: pass 1 wrote the probabilities
+  } else if constexpr (kMma) {
   // 2-byte probabilities, head-major (s_pb[h * tmax + t]): the B operand of
   // pass 3's MFMAs. l sums the rounded values, so the normalisation matches.
   for (int t = lane; t < ntl; t += 64) {
@@ -1065,8 +1157,10 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
     }
   }
   }
+  if constexpr (!kOnline) {
 #pragma unroll
-  for (int h = 0; h < G; ++h) l[h] = wave_sum_f(l[h]);
+    for (int h = 0; h < G; ++h) l[h] = wave_sum_f(l[h]);
+  }
   __syncthreads();
 
   // ---------------- pass 3: probabilities x V ----------------
@@ -1163,7 +1257,7 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
   // the unit's O through LDS (MFMA pass 3): O^T blocks (lane (g4, n16): dims
   // nb*16 + 4*g4 .. +3 of head n16) -> s_o[h][D], read back below per (head,
   // 8-dim chunk). The staged V tile is no longer read; the region holds G x D
-  // floats (fast_score_floats)
+  // floats (online_tile_bytes for 16-head units, fast_score_floats otherwise)
   float* s_o = reinterpret_cast<float*>(s_vt);
   if constexpr (kMmaPv) {
     if (n16 < G) {
@@ -1341,9 +1435,21 @@ void decode_fast_kernel(DecodeArgs a) {
   // read once the probabilities are out), which is sized to hold it
   const int tpad = a.partition + 16 * ring_of(D, G);
   constexpr bool kMma = mma_passes(kF8, G);
-  uint16_t* s_pb =
-      kMma ? reinterpret_cast<uint16_t*>(s_dyn + fast_score_floats(tpad, GP, true, false, G, D)) : nullptr;
-  uint16_t* s_v = kMma ? reinterpret_cast<uint16_t*>(s_dyn) : nullptr;
+  uint16_t* s_pb = nullptr;
+  uint16_t* s_v = nullptr;
+  if constexpr (online_probs(G)) {
+    // 16-head units: [GP][tpad] 2-byte probabilities, then the tile region (K
+    // tile, V tile, O hand-off, merge weights); s_p points at the tile region
+    s_pb = reinterpret_cast<uint16_t*>(s_dyn);
+    s_v = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(s_dyn) + online_prob_bytes(tpad, GP));
+    s_p = reinterpret_cast<float*>(s_v);
+  } else if constexpr (kMma) {
+    // FP8 pools: [GP][tpad] 2-byte probabilities after the scores; pass 3's
+    // [16][kVRow] V tile reuses the scores' region (no longer read once the
+    // probabilities are out), which is sized to hold it
+    s_pb = reinterpret_cast<uint16_t*>(s_dyn + fast_score_floats(tpad, GP, true));
+    s_v = reinterpret_cast<uint16_t*>(s_dyn);
+  }
   int unit, part, ps = a.partition;
   if (a.num_seqs <= kInlineSchedMax) {
     // Small batch: every workgroup derives its item from seq_lens alone, in
@@ -1617,9 +1723,9 @@ int64_t fast_grid(const DecodeArgs& a, int64_t units) {
 int64_t fast_lds_bytes(int partition, int g, bool fp8, int d) {
   const int t = partition + 16 * ring_of(d, g);
   const int gp = pow2ceil(g);
-  const bool mma = mma_passes(fp8, g);
-  return (int64_t)fast_score_floats(t, gp, mma, mma_pv_2byte(d, g), g, d) * 4 +
-         (mma ? fast_prob_bytes(t, gp) : 0);
+  if (online_probs(g)) return (int64_t)online_prob_bytes(t, gp) + online_tile_bytes(g, gp, d);
+  return (int64_t)fast_score_floats(t, gp, fp8, mma_pv_2byte(d, g)) * 4 +
+         (fp8 ? fast_prob_bytes(t, gp) : 0);
 }
 
 template <class TT, int D, int G, int SPB, bool kF8 = false>

@@ -50,14 +50,7 @@ V_ROW = 128 + 16   # elements per row of the FP8 pass-3 V tile in LDS (kVRow)
 K_ROW = 128 + 8    # elements per row of the FP8 pass-1 K tile in LDS (kKRow)
 
 
-def fast_prob_bytes(t: int, gp: int) -> int:
-    """fast_prob_bytes: the FP8 probability region, at least the K tile."""
-    return 16 * K_ROW * 2 if t * gp * 2 < 16 * K_ROW * 2 else t * gp * 2
-
-
 MMA_PV_MIN_G = 5   # kMmaPvMinG: 2-byte pools at head dim 128 from this group size
-
-
 WIDE_GROUP = 16    # kWideGroup: heads of a unit whose passes both run on the matrix cores
 
 
@@ -66,16 +59,35 @@ def mma_passes(fp8: bool, g: int) -> bool:
     return fp8 or g > 8
 
 
-def fast_score_floats(t: int, gp: int, mma: bool, mma_pv: bool = False, g: int = 8,
-                      d: int = 128) -> int:
-    """fast_score_floats: the score region; for the MFMA passes at least the
-    V tile and the G x D floats of the O hand-off, and for a 2-byte MFMA pass 3
-    the in-place probabilities plus the V tile."""
-    if mma:
-        return max(t * gp, 16 * V_ROW // 2, g * d)
+def fast_score_floats(t: int, gp: int, fp8: bool, mma_pv: bool = False) -> int:
+    """fast_score_floats: the score region; at least the FP8 V tile (and the
+    O hand-off), and for a 2-byte MFMA pass 3 the in-place probabilities plus
+    the V tile."""
+    if fp8:
+        return 16 * V_ROW // 2 if t * gp < 16 * V_ROW // 2 else t * gp
     if mma_pv:
         return max(t * gp, t * gp // 2 + 16 * V_ROW // 2)
     return t * gp
+
+
+def fast_prob_bytes(t: int, gp: int) -> int:
+    """fast_prob_bytes: the FP8 probability region, at least the K tile."""
+    return 16 * K_ROW * 2 if t * gp * 2 < 16 * K_ROW * 2 else t * gp * 2
+
+
+def online_probs(g: int) -> bool:
+    """online_probs: 16-head units form their probabilities in pass 1."""
+    return g > 8
+
+
+def online_prob_bytes(t: int, gp: int) -> int:
+    """online_prob_bytes: the [GP][t] 2-byte probabilities (16-byte multiple)."""
+    return (t * gp * 2 + 15) // 16 * 16
+
+
+def online_tile_bytes(g: int, gp: int, d: int) -> int:
+    """online_tile_bytes: K tile, V tile, O hand-off and merge weights, one after another."""
+    return max(16 * K_ROW * 2, 16 * V_ROW * 2, g * d * 4, 64 * gp * 4)
 
 
 WIDE_RING = 2      # NPD_WIDE_RING: ring multiple of 16-head units
@@ -314,10 +326,11 @@ def decode_host(S, H, KV, bs, max_bps, fp8, D=128) -> DecodeLaunch:
     L.grid = n
     gp = pow2ceil(G)
     t = L.partition + 16 * ring_of(D, G)
-    mma = mma_passes(fp8, G)
     mma_pv = D == 128 and MMA_PV_MIN_G <= G <= 8
-    L.lds_floats = (fast_score_floats(t, gp, mma, mma_pv, G, D)
-                    + (fast_prob_bytes(t, gp) // 4 if mma else 0))
+    if online_probs(G):
+        L.lds_floats = (online_prob_bytes(t, gp) + online_tile_bytes(G, gp, D)) // 4
+    else:
+        L.lds_floats = fast_score_floats(t, gp, fp8, mma_pv) + (fast_prob_bytes(t, gp) // 4 if fp8 else 0)
     return L
 
 
@@ -465,24 +478,35 @@ def decode(W: Writes, L: DecodeLaunch, out: Buf, ws: Buf, seq_lens: np.ndarray,
     ring = ring_of(D, L.G)
     nsteps = _ceil(_ceil(np.maximum(ntok, 0), 16), ring) * ring
     if run.any():
-        W.index(nsteps[run] * 16 * gp - 1, L.partition * gp + 16 * ring * gp, "decode LDS scores")
-        if mma_passes(L.fp8, L.G):
-            tpad = L.partition + 16 * ring
-            pb0 = fast_score_floats(tpad, gp, True, False, L.G, D) * 4   # bytes
+        tpad = L.partition + 16 * ring
+        if online_probs(L.G):
+            # 16-head units: probabilities s_pb[h * tpad + tl] (2 bytes) from
+            # pass 1 to pass 3, then the tile region: K tile (pass 1), V tile
+            # (pass 3), O hand-off, merge weights s_w[lane * GP + h]
+            pb = online_prob_bytes(tpad, gp)
+            W.index(2 * ((L.G - 1) * tpad + nsteps[run] * 16 - 1) + 1, pb,
+                    "decode LDS probabilities (bytes)")
+            W.index([pb + 2 * (15 * K_ROW + 127) + 1, pb + 2 * (15 * V_ROW + 127) + 1,
+                     pb + 4 * L.G * D, pb + 4 * 64 * gp], L.lds_floats * 4 + 1,
+                    "decode LDS K / V tiles, O hand-off, merge weights (bytes)")
+        else:
+            W.index(nsteps[run] * 16 * gp - 1, L.partition * gp + 16 * ring * gp, "decode LDS scores")
+        if L.fp8 and not online_probs(L.G):
+            # FP8 pools: 2-byte probabilities s_pb[h * tpad + tl] after the
+            # scores, pass 1's K tile in that region first; pass 3's V tile and
+            # the O exchange in the score region
+            pb0 = fast_score_floats(tpad, gp, True) * 4   # bytes
             W.index(pb0 + 2 * ((L.G - 1) * tpad + nsteps[run] * 16 - 1) + 1, L.lds_floats * 4,
                     "decode LDS probabilities (bytes)")
-            # pass 1's K tile reuses the probability region
             W.index([pb0 + 2 * (15 * K_ROW + 127) + 1], L.lds_floats * 4,
                     "decode LDS K tile in the probability region (bytes)")
             W.index([2 * (15 * K_ROW + 127) + 1], fast_prob_bytes(tpad, gp),
                     "decode K tile within the probability region (bytes)")
-            # the V tile and the O exchange reuse the score region
             W.index([2 * (15 * V_ROW + 127) + 1, 4 * L.G * D - 1], pb0,
                     "decode LDS V tile / O exchange in the score region (bytes)")
-        elif D == 128 and MMA_PV_MIN_G <= L.G <= 8:
+        if not L.fp8 and D == 128 and MMA_PV_MIN_G <= L.G <= 8:
             # MFMA pass 3 of 2-byte pools: probabilities in place as pairs
             # (word t * GP/2 + k), then the V tile / O exchange after them
-            tpad = L.partition + 16 * ring
             W.index(nsteps[run] * 16 * (gp // 2) - 1, tpad * (gp // 2), "decode in-place probabilities")
             v0 = tpad * (gp // 2) * 4   # bytes
             W.index([v0 + 2 * (15 * V_ROW + 127) + 1, v0 + 4 * L.G * D - 1], L.lds_floats * 4,

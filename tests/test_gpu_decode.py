@@ -166,6 +166,38 @@ def test_sixteen_head_units_short_contexts(device):
         check(run(*args, 16), q, kc, vc, bt, sl, scale)
 
 
+def jumping_scores_case(device, G, kvh, lens, dtype, seed):
+    """Every query head of a group has the same vector u, and the K rows of a
+    few tokens are multiples of u: their scores jump far above the earlier
+    ones (log2 units: the first by about 16, the second by about 33) in the
+    middle of a partition, so that a probability reference formed from the
+    first steps must move twice. V rows random."""
+    q, kc, vc, bt, sl, scale, mb = make_inputs(len(lens), G * kvh, kvh, 128, lens, 16, dtype,
+                                               device, seed=seed)
+    g = torch.Generator().manual_seed(seed)
+    u = torch.randn(kvh, 128, generator=g)
+    q.copy_(u.repeat_interleave(G, 0)[None].expand(q.shape).to(dtype))
+    for s_, n in enumerate(lens):
+        for tok, alpha in ((n // 3, 1.0), ((2 * n) // 3, 2.0)):
+            if n < 48:
+                continue
+            b, o = int(bt[s_, tok // 16]), tok % 16
+            kc[b, :, o, :] = (alpha * u).to(dtype).to(device)
+    return q, kc, vc, bt, sl, scale, mb
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_sixteen_head_units_rescale_mid_partition(device, dtype):
+    """16-head units form probabilities against a per-head reference that
+    moves only when a step's max exceeds it by more than 2^8; a move after
+    the first step rescales the probabilities already stored. Scores that
+    jump twice inside a partition exercise that path (contexts shorter and
+    longer than a partition)."""
+    lens = [200, 700, 3000, 40]
+    q, kc, vc, bt, sl, scale, mb = jumping_scores_case(device, 16, 2, lens, dtype, seed=77)
+    check(run(q, kc, vc, bt, sl, scale, mb, 16), q, kc, vc, bt, sl, scale)
+
+
 @pytest.mark.parametrize("D,bs", [(64, 8), (256, 8), (128, 8)])
 def test_group_of_16_generic_path(device, D, bs):
     """G = 16 on the generic kernel (block size 8)."""

@@ -128,6 +128,24 @@ def test_decode_group_of_16_long_context(device, H, kvh, bs):
     _run_and_check(device, *args, bs, torch.bfloat16)
 
 
+@pytest.mark.parametrize("G", [4, 16])
+def test_decode_rescale_mid_partition(device, G):
+    """Scores that jump far above the earlier ones twice inside a partition
+    (the first by about 2^16, the second by about 2^33 in log2 units of the
+    softmax), over an FP8 pool: the probability reference formed from the
+    first steps moves, and the probabilities already stored are rescaled."""
+    from tests.test_gpu_decode import jumping_scores_case
+    dtype = torch.bfloat16
+    kvh = 2
+    q, kc, vc, bt, sl, scale, mb = jumping_scores_case(device, G, kvh, [200, 700, 3000, 40], dtype,
+                                                       seed=78 + G)
+    ks = (kc.float().abs().amax(dim=(0, 2, 3)) / 448).clamp_min(1e-8).cpu()
+    vs = (vc.float().abs().amax(dim=(0, 2, 3)) / 448).clamp_min(1e-8).cpu()
+    k8 = (kc.float().cpu() / ks[None, :, None, None]).to(torch.float8_e4m3fn).view(torch.uint8)
+    v8 = (vc.float().cpu() / vs[None, :, None, None]).to(torch.float8_e4m3fn).view(torch.uint8)
+    _run_and_check(device, q.cpu(), k8, v8, bt.cpu(), sl.cpu(), ks, vs, mb, 16, dtype)
+
+
 def test_decode_long_context_merge_groups(device):
     """80 units with a 32769-token context: partitions of 256 tokens (the FP8
     rule), 129 of them, merged in 9 groups (the last a group of one)."""
