@@ -156,6 +156,22 @@ __device__ __forceinline__ float wave_max_f(float x) {
   x = fmaxf(x, dpp<kDppMirror>(x));
   return fmaxf(fmaxf(lane_f(x, 0), lane_f(x, 16)), fmaxf(lane_f(x, 32), lane_f(x, 48)));
 }
+// Max / sum over the 4 lanes l, l^16, l^32, l^48 (the 4 rows of 16 lanes),
+// with the gfx950 row-swap permutes: v_permlane16_swap with both operands x
+// hands every lane {x, x of lane^16} in some order, and v_permlane32_swap
+// {x, x of lane^32}.
+__device__ __forceinline__ float row_max4(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float row_sum4(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 __device__ __forceinline__ int wave_max_i(int x) {
   x = max(x, dpp_i<kDppXor1>(x));
   x = max(x, dpp_i<kDppXor2>(x));

@@ -61,6 +61,27 @@ struct Mfma16<npd::F16> {
                                                  __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
   }
 };
+// S^T = K . Q^T of 16-head units on v_mfma_f32_16x16x32_{bf16,f16}:
+// A[m = lane%16][k = 8*(lane/16) + e], B[k = 8*(lane/16) + e][n = lane%16],
+// D[m = 4*(lane/16) + i][n = lane%16].
+template <class TT>
+struct MfmaK32;
+template <>
+struct MfmaK32<npd::BF16> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b),
+                                                   c, 0, 0, 0);
+  }
+};
+template <>
+struct MfmaK32<npd::F16> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b),
+                                                  c, 0, 0, 0);
+  }
+};
 // ds_read_b64_tr_b16 on an LDS address given as a generic pointer to LDS: in
 // a group of 16 lanes, lane j receives element j%4 of the 8-byte chunks
 // addressed by lanes 4e + j/4, e = 0..3
@@ -88,14 +109,17 @@ constexpr int kStep = 16;            // tokens per step
 constexpr int kRing = NPD_DECODE_RING;   // fast path: K/V steps in flight per wave
 // head dim 64: rows of 128 bytes, half the bytes per step; twice the steps in
 // flight keep the same bytes in flight (and the same ring registers)
-// 16-head units (more than 8 heads): their LDS leaves room for 5 waves per
-// CU, so each wave keeps twice the steps in flight
-#ifndef NPD_WIDE_RING
-#define NPD_WIDE_RING 2
+constexpr int ring_of(int d) { return d == 64 ? 2 * kRing : kRing; }
+// 16-head units: steps of K and V in flight per wave (FP8 rows are half the
+// bytes, so twice the steps keep the same bytes in flight)
+#ifndef NPD_WIDE_RING_2B
+#define NPD_WIDE_RING_2B 2
 #endif
-constexpr int ring_of(int d, int g = 1) {
-  return d == 64 ? 2 * kRing : (g > 8 ? NPD_WIDE_RING * kRing : kRing);
-}
+#ifndef NPD_WIDE_RING_FP8
+#define NPD_WIDE_RING_FP8 4
+#endif
+constexpr int wide_ring(bool fp8) { return fp8 ? NPD_WIDE_RING_FP8 : NPD_WIDE_RING_2B; }
+
 #ifndef NPD_FAST_MAX_PARTITION
 #define NPD_FAST_MAX_PARTITION 2048
 #endif
@@ -487,6 +511,8 @@ using npd::kDppRor8;
 using npd::kDppXor1;
 using npd::kDppXor2;
 using npd::lane_f;
+using npd::row_max4;
+using npd::row_sum4;
 using npd::uniform_f;
 using npd::wave_max_f;
 using npd::wave_max_i;
@@ -604,7 +630,7 @@ using npd::st_coherent2;
 // relative to the merged max, not normalised), written to slot dst; else the
 // normalised rows of (sequence s, kv-head kh) go to the output.
 constexpr int kMergeFlight = 4;
-// MFMA passes: a head's probability reference moves only when a step's max
+// 16-head units: a head's probability reference moves only when a step's max
 // exceeds it by more than this (log2 units), so probabilities stay <= 2^8
 constexpr float kTauDecode = 8.f;
 constexpr int kMergeGroup = 16;   // partitions per first-level merge (long contexts)
@@ -740,12 +766,13 @@ constexpr int kMmaPvMinG = 5;
 __host__ __device__ constexpr bool mma_pv_2byte(int d, int g) {
   return d == 128 && g >= kMmaPvMinG && g <= 8;
 }
-// Groups of more than 8 heads in one unit (16 per unit, head dim 128): both
-// passes on the matrix cores, as FP8 pools run them, since the v_mfma_f32_16x16x16
-// tiles that pad a group to 16 heads serve 16 heads as cheaply as 8, and the
-// kv head's K/V rows are read once instead of once per 8-head sub-group.
+// Groups of more than 8 heads in one unit (16 per unit, head dim 128:
+// decode_wide_item): S and P.V on the matrix cores, whose 16-wide tiles serve
+// 16 heads as cheaply as 8, and the kv head's K/V rows are read once instead
+// of once per 8-head sub-group.
 constexpr int kWideGroup = 16;
-__host__ __device__ constexpr bool mma_passes(bool fp8, int g) { return fp8 || g > 8; }
+// decode_fast_item runs passes 1 and 3 on the matrix cores for FP8 pools
+__host__ __device__ constexpr bool mma_passes(bool fp8, int) { return fp8; }
 // Floats of the fast path's score region for t tokens (incl. ring padding):
 // FP8 pools' pass 3 stages its 16 x kVRow V tile there, and the O hand-off
 // after it needs G x D floats of it; 2-byte pools with an MFMA pass 3 keep
@@ -755,22 +782,20 @@ __host__ __device__ constexpr int fast_score_floats(int t, int gp, bool fp8, boo
              : mma_pv ? (t * gp < t * gp / 2 + 16 * kVRow / 2 ? t * gp / 2 + 16 * kVRow / 2 : t * gp)
                       : t * gp;
 }
-// Bytes of FP8 pools' probability region ([GP][t] 2-byte values): pass 1
-// stages its 16 x kKRow K tile there first.
+// Row (elements) of the [GP][t] 2-byte probabilities: at least t, and 8 more
+// than a multiple of 16, so that a row is an odd multiple of 16 bytes modulo
+// 32. Pass 3 reads 8 bytes per lane, lane (g4, n16) at row n16, column 4*g4:
+// in each 32-lane half the 16 rows then start on distinct even 8-byte bank
+// pairs and the two columns fill the odd ones, 256 distinct bytes (the same
+// rule as the K tile's kKRow); a power-of-two row put all 16 rows on the same
+// banks.
+__host__ __device__ constexpr int prob_row(int t) { return (t + 7) / 16 * 16 + 8; }
+// Bytes of FP8 pools' probability region ([GP][prob_row(t)] 2-byte values):
+// pass 1 stages its 16 x kKRow K tile there first.
 __host__ __device__ constexpr int fast_prob_bytes(int t, int gp) {
-  return t * gp * 2 < 16 * kKRow * 2 ? 16 * kKRow * 2 : t * gp * 2;
+  return prob_row(t) * gp * 2 < 16 * kKRow * 2 ? 16 * kKRow * 2 : prob_row(t) * gp * 2;
 }
-// 16-head units form their probabilities in pass 1 (see decode_fast_item).
-__host__ __device__ constexpr bool online_probs(int g) { return g > 8; }
-// LDS of 16-head units: the [GP][t] 2-byte probabilities (pass 1 to pass 3),
-// then a tile region that holds pass 1's 16 x kKRow K tile, pass 3's
-// 16 x kVRow V tile, the G x D floats of the O hand-off after pass 3 and the
-// merge's [64][GP] weights, one after another.
-__host__ __device__ constexpr int online_prob_bytes(int t, int gp) { return (t * gp * 2 + 15) / 16 * 16; }
 __host__ __device__ constexpr int cmax(int a, int b) { return a > b ? a : b; }
-__host__ __device__ constexpr int online_tile_bytes(int g, int gp, int d) {
-  return cmax(cmax(16 * kKRow * 2, 16 * kVRow * 2), cmax(g * d * 4, 64 * gp * 4));
-}
 
 // Element source of the fast path. 2-byte pools: a lane's 8 elements are one
 // 16-byte load, used as 4 packed pairs. FP8 pools (kF8): 8 e4m3 bytes, one
@@ -798,6 +823,69 @@ struct KvSrc<TT, true> {
   }
 };
 
+// Slot of partition `part`'s partial: its own slot, or its merge group's
+// result slot when long contexts merge in groups and its group has only it.
+__device__ __forceinline__ int64_t partial_slot(const DecodeArgs& a, int unit, int part, int nparts) {
+  const int64_t ubase = (int64_t)unit * a.max_parts;
+  const bool grouped = a.max_groups > 0 && nparts > kMergeGroup;
+  const int g = part / kMergeGroup;
+  const int gsize = min(kMergeGroup, nparts - g * kMergeGroup);
+  const int64_t gbase =
+      (int64_t)a.num_seqs * a.num_kv_heads * a.max_parts + (int64_t)unit * a.max_groups;
+  return grouped && gsize == 1 ? gbase + g : ubase + part;
+}
+
+// After a wave has issued the stores of its partial (partial_slot): waits for
+// them, takes the merge ticket of its partition and, when it is the last of
+// the unit's partitions (or of its merge group) to arrive, merges them (then
+// the group results, when its group completes them) and resets the counter.
+// s_w: the merge's [64][GP] weights in LDS.
+template <class TT, int D, int G>
+__device__ __forceinline__ void merge_tail(const DecodeArgs& a, int unit, int part, int nparts,
+                                           int s, int kh, int lane, float* s_w, float out_scale) {
+  const int64_t ubase = (int64_t)unit * a.max_parts;
+  const bool grouped = a.max_groups > 0 && nparts > kMergeGroup;
+  const int ngroups = (nparts + kMergeGroup - 1) / kMergeGroup;
+  const int g = part / kMergeGroup;
+  const int gsize = min(kMergeGroup, nparts - g * kMergeGroup);
+  const int64_t gbase =
+      (int64_t)a.num_seqs * a.num_kv_heads * a.max_parts + (int64_t)unit * a.max_groups;
+  auto ticket_of = [&](int* counter) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);   // every store of this wave has completed
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    int t = 0;
+    if (lane == 0) t = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __shfl(t, 0, 64);
+  };
+  // one merge call site, so that its registers are allocated once
+  int* counter = a.counters + unit;
+  int64_t slot0 = ubase, dst = -1;
+  int n = nparts;
+  if (grouped) {
+    if (gsize > 1) {   // first level: this partition's group
+      counter = a.counters + a.num_seqs * a.num_kv_heads + unit * a.max_groups + g;
+      slot0 = ubase + g * kMergeGroup;
+      n = gsize;
+      dst = gbase + g;
+    } else {
+      slot0 = gbase;
+      n = ngroups;
+    }
+  }
+  for (;;) {
+    if (ticket_of(counter) != n - 1) return;
+    merge_unit_fast<TT, D, G>(a, slot0, n, dst, s, kh, lane, s_w, dst >= 0 ? 1.f : out_scale);
+    if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (dst < 0) return;
+    // second level: the group results
+    counter = a.counters + unit;
+    slot0 = gbase;
+    n = ngroups;
+    dst = -1;
+  }
+}
+
 template <class TT, int D, int G, int SPB, bool kF8 = false>
 __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, int part,
                                                  int ps, float* s_p, uint16_t* s_pb,
@@ -819,21 +907,19 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
   constexpr int HELD = NV >> NH;
   constexpr int NTS = NH > LGP ? NH - LGP : 0;   // token bits split by stages
   constexpr int BS = 16 * SPB;
-  constexpr int NBUF = ring_of(D, G);   // steps in flight per pass
-  // passes 1 and 3 on the matrix cores for FP8 pools and for units of more
-  // than 8 heads (2-byte probabilities, K and V staged in LDS as TT; their
-  // short partitions leave LDS room for both), else on the VALU with fp32
-  // probabilities
+  constexpr int NBUF = ring_of(D);   // steps in flight per pass
+  // passes 1 and 3 on the matrix cores for FP8 pools (2-byte probabilities,
+  // K and V staged in LDS as TT; their short partitions leave LDS room for
+  // both), else on the VALU with fp32 probabilities
   constexpr bool kMma = mma_passes(kF8, G);
-  // 16-head units: probabilities formed in pass 1 (online_probs)
-  constexpr bool kOnline = online_probs(G);
-  static_assert(G <= kWideGroup && (G <= 8 || D == 128), "group sizes of the fast path");
+  static_assert(G <= 8, "group sizes of decode_fast_item (16-head units: decode_wide_item)");
   // 2-byte pools with 5-8 heads: pass 3 on the matrix cores too, with the
   // probabilities rounded to TT in place (token-major pairs in the first half
   // of the score region) and the V tile after them
   constexpr bool kMmaPv2 = !kMma && mma_pv_2byte(D, G);
   constexpr bool kMmaPv = kMma || kMmaPv2;
-  const int tmax = a.partition + 16 * NBUF;   // row of s_pb: tokens incl. ring padding
+  const int tmax = a.partition + 16 * NBUF;   // tokens incl. ring padding
+  const int prow = prob_row(tmax);             // row of s_pb (elements)
   constexpr int MAXT = kFastMaxPartition + 16 * NBUF;   // tokens incl. ring padding
 
   (void)MAXT;
@@ -923,36 +1009,25 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
 
   // ---------------- pass 1: scores ----------------
   float runmax = -INFINITY;   // max of the scores this lane stored (its head: headmask)
-  // MFMA passes (FP8 pools, 16-head units): S = Q . K^T on the matrix cores.
+  // MFMA passes (FP8 pools): S = Q . K^T on the matrix cores.
   // A = Q[head n16][dims c*16 + 4*g4 .. +3] (zeros past the group), B = K^T
   // from the step's K rows staged in LDS (row = token of the step),
   // D[head 4*g4 + i][token n16]: each lane ends with the scores of 4 heads of
-  // one token, no reduce-scatter. FP8 pools with up to 8 heads store the
-  // scores (fp32) for pass 2. 16-head units (kOnline) form the probabilities
-  // in the same step, against a per-head reference that only moves up when a
-  // step's max exceeds it by more than 2^kTauDecode (probabilities <=
-  // 2^kTauDecode, rounded to TT), so they need no fp32 score buffer and no
-  // softmax pass over LDS: that LDS is what held them to 5 waves per CU.
-  // When the reference moves after the first step, the probabilities already
-  // stored for that head are rescaled in LDS (a rare event: the first step's
-  // max is usually within 2^kTauDecode of the partition's). For FP8 pools with
-  // up to 8 heads, which are not held by their LDS, the step's row reductions
-  // cost more than the pass they remove (52.6 against 50.9 us at config 2).
+  // one token, no reduce-scatter; the scores (fp32) are stored for pass 2.
+  // (Forming the probabilities in the same step against a moving reference,
+  // as 16-head units do, costs these units more in row reductions than the
+  // pass it removes: 52.6 against 50.9 us at config 2.)
   const int g4 = lane >> 4, n16 = lane & 15;
   constexpr int NQC = kMma ? D / 16 : 1;
   u32x2 qa[NQC];
-  float mref[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};   // heads 4*g4 + i (row-uniform)
-  float lp[4] = {0.f, 0.f, 0.f, 0.f};   // this lane's sums of its rounded probabilities
   if constexpr (kMma) {
     const uint16_t* qrow = a.q + s * a.q_stride_seq + (kh * G + n16) * a.q_stride_head + 4 * g4;
 #pragma unroll
     for (int c = 0; c < NQC; ++c)
       qa[c] = n16 < G ? *reinterpret_cast<const u32x2*>(qrow + c * 16) : u32x2{0, 0};
   }
-  // pass 1's K tile: with online probabilities the tile region, which pass
-  // 3's V tile reuses (the probabilities live in s_pb from pass 1 to pass 3);
-  // else the probability region, which pass 2 fills afterwards
-  uint16_t* s_k = kOnline ? s_v : s_pb;
+  // pass 1's K tile: the probability region, which pass 2 fills afterwards
+  uint16_t* s_k = s_pb;
   float runmax4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};   // stored scores: heads 4*g4 + i
   auto score_step_mma = [&](const raw_t* kraw, int st) {
 #pragma unroll
@@ -964,63 +1039,15 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
       sacc = Mfma16<TT>::mma(qa[c], *reinterpret_cast<const u32x2*>(&s_k[n16 * kKRow + c * 16 + 4 * g4]),
                              sacc);
     const int tl = st * 16 + n16;
-    if constexpr (!kOnline) {
-      // scores to LDS; pass 2 forms the probabilities against the exact maxima
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int h = 4 * g4 + i;
-        if (h < G) {
-          // rows past the context may hold anything: select, not scale
-          const float sv = (tl < ntok) ? sacc[i] * score_scale : -INFINITY;
-          s_p[tl * GP + h] = sv;
-          runmax4[i] = fmaxf(runmax4[i], sv);
-        }
-      }
-      return;
-    }
-    float sv[4], f[4];
-    bool moved = false;   // a reference of this lane's heads moved after earlier probabilities
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      // rows past the context may hold anything: select, not scale
-      sv[i] = (tl < ntok) ? sacc[i] * score_scale : -INFINITY;
-      // the step's max over the row's 16 tokens (DPP within the 16-lane row)
-      float x = sv[i];
-      x = fmaxf(x, dpp<kDppXor1>(x));
-      x = fmaxf(x, dpp<kDppXor2>(x));
-      x = fmaxf(x, dpp<kDppHalfMirror>(x));
-      x = fmaxf(x, dpp<kDppMirror>(x));
-      const bool up = x > mref[i] + kTauDecode;
-      f[i] = 1.f;
-      if (up) {
-        f[i] = mref[i] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mref[i] - x);
-        moved = moved || (mref[i] != -INFINITY);
-        lp[i] *= f[i];
-        mref[i] = x;
-      }
-    }
-    if (__ballot(moved) != 0) {
-      // rare: rescale the probabilities already stored for the heads whose
-      // reference moved (tokens of the earlier steps)
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        const float fh = lane_f(f[h % 4], 16 * (h / 4));
-        if (fh != 1.f) {
-          for (int t = lane; t < st * 16; t += 64) {
-            uint16_t* pp = &s_pb[h * tmax + t];
-            *pp = (uint16_t)TT::from_float(TT::lo(*pp) * fh);
-          }
-        }
-      }
-    }
+    // scores to LDS; pass 2 forms the probabilities against the exact maxima
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int h = 4 * g4 + i;
-      const float ref = mref[i] == -INFINITY ? 0.f : mref[i];
-      const uint32_t u = TT::from_float(__builtin_amdgcn_exp2f(sv[i] - ref));
       if (h < G) {
-        s_pb[h * tmax + tl] = (uint16_t)u;
-        lp[i] += TT::lo(u);
+        // rows past the context may hold anything: select, not scale
+        const float sv = (tl < ntok) ? sacc[i] * score_scale : -INFINITY;
+        s_p[tl * GP + h] = sv;
+        runmax4[i] = fmaxf(runmax4[i], sv);
       }
     }
   };
@@ -1087,20 +1114,11 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
 
   // ---------------- pass 2: softmax statistics over the partition ----------------
   // the maxima come from pass 1's running maxima (DPP wave reductions, one
-  // per head over the lanes that stored that head's scores); the MFMA passes
-  // have their references and probability sums from pass 1 already
+  // per head over the lanes that stored that head's scores)
   float m[GP], l[GP];
 #pragma unroll
   for (int h = 0; h < GP; ++h) {
-    if constexpr (kOnline) {
-      float lr = lp[h % 4];   // the row's sum of head h's probabilities
-      lr += dpp<kDppXor1>(lr);
-      lr += dpp<kDppXor2>(lr);
-      lr += dpp<kDppHalfMirror>(lr);
-      lr += dpp<kDppMirror>(lr);
-      m[h] = h < G ? lane_f(mref[h % 4], 16 * (h / 4)) : -INFINITY;
-      l[h] = h < G ? lane_f(lr, 16 * (h / 4)) : 0.f;
-    } else if constexpr (kMma) {
+    if constexpr (kMma) {
       m[h] = h < G ? wave_max_f(g4 == h / 4 ? runmax4[h % 4] : -INFINITY) : -INFINITY;
       l[h] = 0.f;
     } else {
@@ -1109,17 +1127,15 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
     }
   }
   const int ntl = nsteps * 16;
-  if constexpr (kOnline) {
-    // nothing left to do: pass 1 wrote the probabilities
-  } else if constexpr (kMma) {
-  // 2-byte probabilities, head-major (s_pb[h * tmax + t]): the B operand of
+  if constexpr (kMma) {
+  // 2-byte probabilities, head-major (s_pb[h * prow + t]): the B operand of
   // pass 3's MFMAs. l sums the rounded values, so the normalisation matches.
   for (int t = lane; t < ntl; t += 64) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
       const uint32_t u = TT::from_float(__builtin_amdgcn_exp2f(s_p[t * GP + h] - m[h]));
       l[h] += TT::lo(u);
-      s_pb[h * tmax + t] = (uint16_t)u;
+      s_pb[h * prow + t] = (uint16_t)u;
     }
   }
   } else if constexpr (kMmaPv2) {
@@ -1157,16 +1173,12 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
     }
   }
   }
-  if constexpr (!kOnline) {
 #pragma unroll
-    for (int h = 0; h < G; ++h) l[h] = wave_sum_f(l[h]);
-  }
+  for (int h = 0; h < G; ++h) l[h] = wave_sum_f(l[h]);
   __syncthreads();
 
   // ---------------- pass 3: probabilities x V ----------------
-  // (units of more than 8 heads keep O only in the MFMA accumulators and
-  // hand it over through LDS at the end: acc is for groups of up to 8)
-  constexpr int GA = G <= 8 ? G : 1;
+  constexpr int GA = G;
   float acc[GA][8];
 #pragma unroll
   for (int h = 0; h < GA; ++h)
@@ -1196,7 +1208,7 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
     // B: probabilities of tokens st*16 + 4*g4 .. +3 for head n16 (0 past the group)
     u32x2 pbv = u32x2{0, 0};
     if constexpr (kMma) {
-      if (n16 < G) pbv = *reinterpret_cast<const u32x2*>(&s_pb[n16 * tmax + st * 16 + 4 * g4]);
+      if (n16 < G) pbv = *reinterpret_cast<const u32x2*>(&s_pb[n16 * prow + st * 16 + 4 * g4]);
     } else {
       if (n16 < G) {
         uint32_t w[4];
@@ -1256,8 +1268,9 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
   }
   // the unit's O through LDS (MFMA pass 3): O^T blocks (lane (g4, n16): dims
   // nb*16 + 4*g4 .. +3 of head n16) -> s_o[h][D], read back below per (head,
-  // 8-dim chunk). The staged V tile is no longer read; the region holds G x D
-  // floats (online_tile_bytes for 16-head units, fast_score_floats otherwise)
+  // 8-dim chunk). The staged V tile is no longer read (the last MFMAs, which
+  // consume it, feed these stores); the region holds G x D floats
+  // (fast_score_floats)
   float* s_o = reinterpret_cast<float*>(s_vt);
   if constexpr (kMmaPv) {
     if (n16 < G) {
@@ -1265,37 +1278,6 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
       for (int nb = 0; nb < NOB; ++nb) *reinterpret_cast<f32x4*>(&s_o[n16 * D + nb * 16 + 4 * g4]) = oacc[nb];
     }
   }
-  if constexpr (G > 8) {
-    // 16-head units: row r of the wave (TPL rows of LPT lanes) writes heads
-    // r, r + TPL, ... straight from s_o, to the output or as a partial
-    const int64_t base_p = nparts == 1 ? -1 : (int64_t)unit * a.max_parts + part;
-    const bool grouped1 = a.max_groups > 0 && nparts > kMergeGroup;
-    const int gq = part / kMergeGroup;
-    const int64_t base = base_p < 0 ? -1
-        : (grouped1 && min(kMergeGroup, nparts - gq * kMergeGroup) == 1
-               ? (int64_t)a.num_seqs * a.num_kv_heads * a.max_parts + (int64_t)unit * a.max_groups + gq
-               : base_p);
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      if ((h % TPL) != r) continue;
-      const f32x4 lo = *reinterpret_cast<const f32x4*>(&s_o[h * D + j * 8]);
-      const f32x4 hi = *reinterpret_cast<const f32x4*>(&s_o[h * D + j * 8 + 4]);
-      const float o[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-      if (base < 0) {
-        store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + j * 8, o,
-                       out_scale / l[h]);
-      } else {
-        float* dst = a.part_acc + (base * G + h) * D + j * 2;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) st_coherent2(dst + k * (2 * LPT), o[2 * k], o[2 * k + 1]);
-      }
-    }
-    if (base < 0) return;
-    if (lane == 0) {
-#pragma unroll
-      for (int h = 0; h < G; ++h) st_coherent2(a.part_ml + (base * G + h) * 2, m[h], l[h]);
-    }
-  } else {
   if constexpr (kMmaPv) {
 #pragma unroll
     for (int h = 0; h < GA; ++h) {
@@ -1335,7 +1317,6 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
     }
     return;
   }
-  }
   // Several partitions: publish this one's partial, then the last wave of the
   // (sequence, kv-head) to arrive merges them all and resets the counter.
   // Partials go out as agent-scope atomic stores (written through to the
@@ -1354,61 +1335,260 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
   // output. Group merges run as groups complete, so the merge left after the
   // last partition covers one group and the group results, not every
   // partition. Group result slots follow the partition slots of all units.
-  const int64_t ubase = (int64_t)unit * a.max_parts;
-  const bool grouped = a.max_groups > 0 && nparts > kMergeGroup;
-  const int ngroups = (nparts + kMergeGroup - 1) / kMergeGroup;
-  const int g = part / kMergeGroup;
-  const int gsize = min(kMergeGroup, nparts - g * kMergeGroup);
-  const int64_t gbase =
-      (int64_t)a.num_seqs * a.num_kv_heads * a.max_parts + (int64_t)unit * a.max_groups;
-  if constexpr (G <= 8) {
-    const int64_t base = grouped && gsize == 1 ? gbase + g : ubase + part;
+  const int64_t base = partial_slot(a, unit, part, nparts);
 #pragma unroll
-    for (int h = 0; h < GA; ++h) {
-      if ((h % TPL) != r) continue;
+  for (int h = 0; h < GA; ++h) {
+    if ((h % TPL) != r) continue;
+    float* dst = a.part_acc + (base * G + h) * D + j * 2;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) st_coherent2(dst + k * (2 * LPT), acc[h][2 * k], acc[h][2 * k + 1]);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) st_coherent2(a.part_ml + (base * G + h) * 2, m[h], l[h]);
+  }
+  merge_tail<TT, D, G>(a, unit, part, nparts, s, kh, lane, s_p, out_scale);
+}
+
+
+// LDS of a 16-head unit (decode_wide_item): the 16 x kVRow V tile, then the
+// G x D floats of the O hand-off and G (1/l) values after it, then the
+// merge's [64][GP] weights, each from byte 0 once the one before is no longer
+// read. Independent of the partition.
+constexpr int kWideLdsBytes =
+    cmax(cmax(16 * kVRow * 2, (kWideGroup * 128 + kWideGroup) * 4), 64 * kWideGroup * 4);
+
+// 16-head units (G = 16, D = 128): one pass over the partition. Per 16-token
+// step of the unit's kv head:
+//   S^T = K . Q^T on v_mfma_f32_16x16x32 (4 chunks of 32 dims). Its A
+//     operand comes straight from the pool: lane (g4, n16) loads the 16 bytes
+//     (8 bytes for FP8, converted) of token n16's row at dims 32c + 8*g4, so
+//     chunk c's load covers 64 bytes of each of the step's 16 rows and the
+//     four cover them whole. Lane (g4, n16) ends with the scores of tokens
+//     4*g4 + i of head n16.
+//   The head's step max (its 4 scores, then the 4 rows by v_permlane16/32_swap)
+//     moves the head's reference only when it exceeds it by more than
+//     2^kTauDecode, so probabilities stay <= 2^kTauDecode; a move rescales the
+//     head's O accumulators, which the same lanes hold (O^T column n16).
+//   The 4 probabilities, rounded to TT, are the B operand of O^T += V^T . P^T
+//     on v_mfma_f32_16x16x16 as they stand; the V tile goes through LDS for
+//     the transposing reads (ds_read_b64_tr_b16) of the A operand.
+// No probability or score buffer: LDS is the V tile and the hand-off, so the
+// partition is as long as the 2-byte path's and many waves fit a CU. K and V
+// loads run NBUF steps ahead in a register ring.
+template <class TT, int SPB, bool kF8>
+__device__ __forceinline__ void decode_wide_item(const DecodeArgs& a, int unit, int part, int ps,
+                                                 float* s_lds) {
+  typedef KvSrc<TT, kF8> Src;
+  constexpr int D = 128, G = kWideGroup;
+  constexpr int LPT = D / 8;        // 16-byte chunks (FP8: 8-byte) per row
+  constexpr int TPL = 64 / LPT;     // rows per coalesced load
+  constexpr int NL = 16 / TPL;      // coalesced V loads per step
+  constexpr int NKC = D / 32;       // S MFMAs (32-dim chunks) per step
+  constexpr int NKL = kF8 ? 2 : 4;  // 16-byte K loads per lane and step
+  constexpr int NVL = kF8 ? 2 : NL; // 16-byte V loads per lane and step
+  constexpr int NOB = D / 16;       // 16-dim blocks of O^T
+  constexpr int BS = 16 * SPB;
+  constexpr int NBUF = wide_ring(kF8);
+  const int lane = threadIdx.x;
+  const int r = lane / LPT, j = lane % LPT;
+  const int g4 = lane >> 4, n16 = lane & 15;
+  const int s = unit / a.num_kv_heads;
+  const int kh = unit - s * a.num_kv_heads;
+
+  int ctx = a.seq_lens[s];
+  const int cap = a.max_bps * BS;
+  ctx = ctx < cap ? ctx : cap;
+  if (ctx <= 0) {
+    if (part == 0) {
+      const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      for (int h = r; h < G; h += TPL)
+        store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + j * 8, z, 0.f);
+    }
+    return;
+  }
+  const int nparts = (ctx + ps - 1) / ps;
+  if (part >= nparts) return;
+  const int t0 = part * ps;
+  const int ntok = (ctx - t0) < ps ? (ctx - t0) : ps;
+  // steps rounded up to the ring size; steps past the context read a block of
+  // the pool (clamped ids) and are masked out
+  const int nsteps = (((ntok + 15) >> 4) + NBUF - 1) / NBUF * NBUF;
+  const int b0 = t0 / BS;
+  // lane e holds the block ids of blocks e and 64 + e of the partition
+  // (clamped; at most 128 blocks: kFastMaxPartition / 16)
+  static_assert(kFastMaxPartition / 16 <= 128, "two block ids per lane");
+  int myblk0 = 0, myblk1 = 0;
+  {
+    const int nb = (ntok + BS - 1) / BS;
+    const int32_t* row = a.block_tables + (int64_t)s * a.max_bps + b0;
+    auto clamp_blk = [&](int b) { return b < 0 ? 0 : (b >= a.num_blocks ? a.num_blocks - 1 : b); };
+    if (lane < nb) myblk0 = clamp_blk(row[lane]);
+    if (lane + 64 < nb) myblk1 = clamp_blk(row[lane + 64]);
+  }
+  const int pkh = kh / a.kv_split;   // the unit's kv head in the pool
+  const float score_scale = kF8 ? a.scale_log2 * a.k_scale[pkh] : a.scale_log2;
+  const float out_scale = kF8 ? a.v_scale[pkh] : 1.f;
+  const int64_t head_rows = (int64_t)pkh * BS;            // rows of head pkh in a block
+  const int64_t blk_rows = (int64_t)a.pool_kv_heads * BS; // rows per block
+  auto step_base = [&](int st) -> int64_t {              // chunk index of the step's first row
+    const int bi = st / SPB;   // wave-uniform
+    const int blk = __builtin_amdgcn_readlane(bi < 64 ? myblk0 : myblk1, bi & 63);
+    return ((int64_t)blk * blk_rows + head_rows + (st % SPB) * 16) * LPT;
+  };
+  // K in the MFMA layout, 16-byte loads: load c of lane (g4, n16) = row n16,
+  // 16-byte chunk 4c + g4 of the row, so each load covers 64 contiguous bytes
+  // of every row of the step. 2-byte pools: dims 32c + 8*g4 .. +7, the A
+  // operand of S MFMA c. FP8 (rows of 128 bytes, two loads): dims
+  // 64c + 16*g4 .. +15, converted in two halves, the A operands of S MFMAs
+  // 2c and 2c + 1 (the head dims are summed in another order; Q follows it)
+  auto load_k = [&](u32x4* buf, int st) {
+    const int64_t b = (kF8 ? step_base(st) / 2 + n16 * (LPT / 2) : step_base(st) + n16 * LPT) + g4;
+#pragma unroll
+    for (int c = 0; c < NKL; ++c) buf[c] = ld_stream(static_cast<const u32x4*>(a.k_cache) + b + 4 * c);
+  };
+  // V coalesced, 16-byte loads: 2-byte pools: load i of lane (r, j) = row
+  // i*TPL + r, chunk j (8 dims); FP8: load i of lane (r8, j8) = row 8i + r8,
+  // 16-byte chunk j8 (16 dims), 1 KB contiguous per load
+  auto load_v = [&](u32x4* buf, int st) {
+    const int64_t b = (kF8 ? step_base(st) / 2 : step_base(st)) + lane;
+#pragma unroll
+    for (int i = 0; i < NVL; ++i) buf[i] = ld_stream(static_cast<const u32x4*>(a.v_cache) + b + i * 64);
+  };
+  // Q^T as the B operand of S MFMA c: lane (g4, n16) = head n16, the dims of
+  // the K operand (2-byte pools: 32c + 8*g4 .. +7; FP8: 64(c/2) + 16*g4 +
+  // 8(c%2) .. +7)
+  u32x4 qb[NKC];
+  {
+    const uint16_t* qrow = a.q + s * a.q_stride_seq + (kh * G + n16) * a.q_stride_head;
+#pragma unroll
+    for (int c = 0; c < NKC; ++c)
+      qb[c] = *reinterpret_cast<const u32x4*>(qrow + (kF8 ? 64 * (c / 2) + 16 * g4 + 8 * (c % 2)
+                                                          : 32 * c + 8 * g4));
+  }
+  uint16_t* s_vt = reinterpret_cast<uint16_t*>(s_lds);
+  // A of the P.V MFMA: V^T[dim nb*16 + n16][tokens 4*g4 .. +3] by transposing
+  // reads (lane (g4, n16) addresses token 4*g4 + n16/4, dims nb*16 + 4*(n16%4) .. +3)
+  const uint16_t* vl = s_vt + (g4 * 4 + (n16 >> 2)) * kVRow + 4 * (n16 & 3);
+  f32x4 oacc[NOB];
+#pragma unroll
+  for (int nb = 0; nb < NOB; ++nb) oacc[nb] = f32x4{0, 0, 0, 0};
+  float mref = -INFINITY;   // head n16's reference (uniform over the 4 rows)
+  float lp = 0.f;           // this lane's sum of head n16's rounded probabilities
+
+  auto step = [&](const u32x4* kraw, const u32x4* vraw, int st) {
+    // the step's V rows into LDS first (row = token of the step, TT
+    // elements), so the writes complete under the S MFMAs and the softmax
+    // (the previous step's transposing reads were issued before them); in a
+    // tail step rows past the context may hold anything (0 x NaN): zeros
+    const bool tail = st * 16 + 16 > ntok;
+    if constexpr (kF8) {
+#pragma unroll
+      for (int i = 0; i < NVL; ++i) {
+        const int row = 8 * i + (lane >> 3), c16 = lane & 7;
+        u32x4 v0 = Src::pairs(u32x2{vraw[i].x, vraw[i].y});
+        u32x4 v1 = Src::pairs(u32x2{vraw[i].z, vraw[i].w});
+        if (tail && st * 16 + row >= ntok) v0 = v1 = u32x4{0, 0, 0, 0};
+        *reinterpret_cast<u32x4*>(&s_vt[row * kVRow + c16 * 16]) = v0;
+        *reinterpret_cast<u32x4*>(&s_vt[row * kVRow + c16 * 16 + 8]) = v1;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NL; ++i) {
+        u32x4 v = vraw[i];
+        if (tail && st * 16 + i * TPL + r >= ntok) v = u32x4{0, 0, 0, 0};
+        *reinterpret_cast<u32x4*>(&s_vt[(i * TPL + r) * kVRow + j * 8]) = v;
+      }
+    }
+    // S^T for the step's 16 tokens
+    f32x4 sacc = f32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < NKL; ++c) {
+      if constexpr (kF8) {
+        sacc = MfmaK32<TT>::mma(Src::pairs(u32x2{kraw[c].x, kraw[c].y}), qb[2 * c], sacc);
+        sacc = MfmaK32<TT>::mma(Src::pairs(u32x2{kraw[c].z, kraw[c].w}), qb[2 * c + 1], sacc);
+      } else {
+        sacc = MfmaK32<TT>::mma(kraw[c], qb[c], sacc);
+      }
+    }
+    float sv[4];
+    const int tl = st * 16 + 4 * g4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)   // rows past the context may hold anything: select, not scale
+      sv[i] = (tl + i < ntok) ? sacc[i] * score_scale : -INFINITY;
+    const float x = row_max4(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
+    float f = 1.f;
+    if (x > mref + kTauDecode) {
+      f = mref == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mref - x);
+      mref = x;
+    }
+    if (__ballot(f != 1.f) != 0) {   // the first step, then rarely
+      lp *= f;
+#pragma unroll
+      for (int nb = 0; nb < NOB; ++nb) oacc[nb] *= f;
+    }
+    const float ref = mref == -INFINITY ? 0.f : mref;
+    const uint32_t p01 = TT::pack2(__builtin_amdgcn_exp2f(sv[0] - ref), __builtin_amdgcn_exp2f(sv[1] - ref));
+    const uint32_t p23 = TT::pack2(__builtin_amdgcn_exp2f(sv[2] - ref), __builtin_amdgcn_exp2f(sv[3] - ref));
+    lp += (TT::lo(p01) + TT::hi(p01)) + (TT::lo(p23) + TT::hi(p23));
+    const u32x2 pbv = u32x2{p01, p23};
+#pragma unroll
+    for (int nb = 0; nb < NOB; ++nb) oacc[nb] = Mfma16<TT>::mma(lds_read_tr(vl + nb * 16), pbv, oacc[nb]);
+  };
+  {
+    // ring of NBUF steps in flight; the last round is peeled so the steady
+    // loop has no branches and each wait leaves the newer loads pending
+    u32x4 kb[NBUF][NKL];
+    u32x4 vb[NBUF][NVL];
+#pragma unroll
+    for (int b = 0; b < NBUF; ++b) {
+      load_k(kb[b], b);
+      load_v(vb[b], b);
+    }
+    auto round = [&](int st0) {
+#pragma unroll
+      for (int b = 0; b < NBUF; ++b) {
+        step(kb[b], vb[b], st0 + b);
+        load_k(kb[b], st0 + NBUF + b);
+        load_v(vb[b], st0 + NBUF + b);
+      }
+    };
+    int st0 = 0;
+    for (; st0 + NBUF < nsteps; st0 += NBUF) round(st0);
+#pragma unroll
+    for (int b = 0; b < NBUF; ++b) step(kb[b], vb[b], st0 + b);
+  }
+  const float lsum = row_sum4(lp);   // head n16's l (every row)
+
+  // O^T blocks (lane (g4, n16): dims nb*16 + 4*g4 .. +3 of head n16) ->
+  // s_o[h][D] and 1/l -> s_il[h], read back per (head, 8-dim chunk). The V
+  // tile is no longer read: the last MFMAs, which consume it, feed these
+  // stores.
+  float* s_o = s_lds;
+  float* s_il = s_lds + G * D;
+#pragma unroll
+  for (int nb = 0; nb < NOB; ++nb) *reinterpret_cast<f32x4*>(&s_o[n16 * D + nb * 16 + 4 * g4]) = oacc[nb];
+  if (g4 == 0) s_il[n16] = out_scale / lsum;
+  const int64_t base = nparts == 1 ? -1 : partial_slot(a, unit, part, nparts);
+  // row r of the wave (TPL rows of LPT lanes) writes heads r, r + TPL, ...
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    if ((h % TPL) != r) continue;
+    const f32x4 lo = *reinterpret_cast<const f32x4*>(&s_o[h * D + j * 8]);
+    const f32x4 hi = *reinterpret_cast<const f32x4*>(&s_o[h * D + j * 8 + 4]);
+    const float o[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    if (base < 0) {
+      store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + j * 8, o,
+                     s_il[h]);
+    } else {
       float* dst = a.part_acc + (base * G + h) * D + j * 2;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) st_coherent2(dst + k * (2 * LPT), acc[h][2 * k], acc[h][2 * k + 1]);
-    }
-    if (lane == 0) {
-#pragma unroll
-      for (int h = 0; h < G; ++h) st_coherent2(a.part_ml + (base * G + h) * 2, m[h], l[h]);
+      for (int k = 0; k < 4; ++k) st_coherent2(dst + k * (2 * LPT), o[2 * k], o[2 * k + 1]);
     }
   }
-  auto ticket_of = [&](int* counter) {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);   // every store of this wave has completed
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    int t = 0;
-    if (lane == 0) t = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return __shfl(t, 0, 64);
-  };
-  // one merge call site, so that its registers are allocated once
-  int* counter = a.counters + unit;
-  int64_t slot0 = ubase, dst = -1;
-  int n = nparts;
-  if (grouped) {
-    if (gsize > 1) {   // first level: this partition's group
-      counter = a.counters + a.num_seqs * a.num_kv_heads + unit * a.max_groups + g;
-      slot0 = ubase + g * kMergeGroup;
-      n = gsize;
-      dst = gbase + g;
-    } else {
-      slot0 = gbase;
-      n = ngroups;
-    }
-  }
-  for (;;) {
-    if (ticket_of(counter) != n - 1) return;
-    merge_unit_fast<TT, D, G>(a, slot0, n, dst, s, kh, lane, s_p, dst >= 0 ? 1.f : out_scale);
-    if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (dst < 0) return;
-    // second level: the group results
-    counter = a.counters + unit;
-    slot0 = gbase;
-    n = ngroups;
-    dst = -1;
-  }
+  if (base < 0) return;
+  if (g4 == 0) st_coherent2(a.part_ml + (base * G + n16) * 2, mref, lsum);
+  merge_tail<TT, D, G>(a, unit, part, nparts, s, kh, lane, s_lds, out_scale);
 }
 
 
@@ -1422,8 +1602,9 @@ template <class TT, int D, int G, int SPB, bool kF8>
 // FP8 pools with up to 4 heads per group: at most 128 VGPRs, four waves per
 // SIMD (the MFMA pass 3 would otherwise take the kernel to 148). Head dim 128
 // with 5-8 heads per group: at most 168, three waves per SIMD (1-4% faster
-// than 8 waves per CU at 180-212). 16-head units: at most 256 (their LDS
-// allows 5 waves per CU).
+// than 8 waves per CU at 180-212). 16-head units (decode_wide_item): at most
+// 256; they take 149 (2-byte) and 163 (FP8), three waves per SIMD (four, at
+// 128, ran 5% slower).
 __global__ __launch_bounds__(64)
 __attribute__((amdgpu_waves_per_eu(kF8 && G <= 4 ? 4 : (D == 128 && G >= 5 && G <= 8 ? 3 : (G > 8 ? 2 : 1)))))
 void decode_fast_kernel(DecodeArgs a) {
@@ -1433,18 +1614,12 @@ void decode_fast_kernel(DecodeArgs a) {
   // FP8 pools: [GP][partition + ring padding] 2-byte probabilities after the
   // scores; pass 3's [16][kVRow] V tile reuses the scores' region (no longer
   // read once the probabilities are out), which is sized to hold it
-  const int tpad = a.partition + 16 * ring_of(D, G);
+  const int tpad = a.partition + 16 * ring_of(D);
   constexpr bool kMma = mma_passes(kF8, G);
   uint16_t* s_pb = nullptr;
   uint16_t* s_v = nullptr;
-  if constexpr (online_probs(G)) {
-    // 16-head units: [GP][tpad] 2-byte probabilities, then the tile region (K
-    // tile, V tile, O hand-off, merge weights); s_p points at the tile region
-    s_pb = reinterpret_cast<uint16_t*>(s_dyn);
-    s_v = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(s_dyn) + online_prob_bytes(tpad, GP));
-    s_p = reinterpret_cast<float*>(s_v);
-  } else if constexpr (kMma) {
-    // FP8 pools: [GP][tpad] 2-byte probabilities after the scores; pass 3's
+  if constexpr (kMma) {
+    // FP8 pools: [GP][prob_row(tpad)] 2-byte probabilities after the scores; pass 3's
     // [16][kVRow] V tile reuses the scores' region (no longer read once the
     // probabilities are out), which is sized to hold it
     s_pb = reinterpret_cast<uint16_t*>(s_dyn + fast_score_floats(tpad, GP, true));
@@ -1554,7 +1729,10 @@ void decode_fast_kernel(DecodeArgs a) {
     unit = it.x;
     part = it.y;
   }
-  decode_fast_item<TT, D, G, SPB, kF8>(a, unit, part, ps, s_p, s_pb, s_v);
+  if constexpr (G == kWideGroup)
+    decode_wide_item<TT, SPB, kF8>(a, unit, part, ps, s_dyn);
+  else
+    decode_fast_item<TT, D, G, SPB, kF8>(a, unit, part, ps, s_p, s_pb, s_v);
 }
 
 // Builds the work list of decode_fast_kernel (one workgroup):
@@ -1673,11 +1851,16 @@ int choose_partition(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads, 
     if (NPD_DECODE_PARTITION >= block_size) return NPD_DECODE_PARTITION;
 #endif
     const int gp = pow2ceil((int)(num_heads / num_kv_heads));
-    const int top = fp8 ? kFastMaxPartitionFp8 : kFastMaxPartition;
-    const int64_t min_items = fp8 ? kFastMinItemsFp8 : kFastMinItems;
+    // 16-head units: LDS independent of the partition; FP8 pools' 16-byte
+    // loads cover whole rows, and the 2-byte rules serve them best too
+    // (57.6 against 72 us at 256 tokens and 4096 items, config 2 with 128 q
+    // heads; 88 against 94 us at 1024 tokens with 256 q heads)
+    const bool wide = gp == kWideGroup;
+    const int top = fp8 && !wide ? kFastMaxPartitionFp8 : kFastMaxPartition;
+    const int64_t min_items = fp8 && !wide ? kFastMinItemsFp8 : kFastMinItems;
     for (int ps = top; ps >= 64; ps >>= 1) {
       if (ps <= block_size) return (int)block_size;
-      if (ps * gp > kFastMaxScores) continue;
+      if (ps * gp > kFastMaxScores && !wide) continue;
       if (units * ((max_ctx + ps - 1) / ps) >= min_items) return ps;
     }
     return block_size > 64 ? (int)block_size : 64;
@@ -1719,11 +1902,11 @@ int64_t fast_grid(const DecodeArgs& a, int64_t units) {
 // token of the partition plus the ring padding (for FP8 pools at least the
 // 16-row V tile of pass 3's MFMAs, which reuses that region), then for FP8
 // pools the 2-byte probabilities (at least pass 1's 16-row K tile, which
-// reuses that region).
+// reuses that region). 16-head units: kWideLdsBytes, for any partition.
 int64_t fast_lds_bytes(int partition, int g, bool fp8, int d) {
-  const int t = partition + 16 * ring_of(d, g);
+  const int t = partition + 16 * ring_of(d);
   const int gp = pow2ceil(g);
-  if (online_probs(g)) return (int64_t)online_prob_bytes(t, gp) + online_tile_bytes(g, gp, d);
+  if (g == kWideGroup) return kWideLdsBytes;
   return (int64_t)fast_score_floats(t, gp, fp8, mma_pv_2byte(d, g)) * 4 +
          (fp8 ? fast_prob_bytes(t, gp) : 0);
 }

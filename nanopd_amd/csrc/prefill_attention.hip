@@ -128,22 +128,9 @@ struct Mfma<npd::F16> {
   }
 };
 
-// Max / sum over the 4 lanes l, l^16, l^32, l^48 (the 4 key groups of a query
-// row), with the gfx950 row-swap permutes: v_permlane16_swap with both
-// operands x hands every lane {x, x of lane^16} in some order, and
-// v_permlane32_swap {x, x of lane^32}.
-__device__ __forceinline__ float row_max4(float x) {
-  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-__device__ __forceinline__ float row_sum4(float x) {
-  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
+// Max / sum over the 4 key groups of a query row (lanes l, l^16, l^32, l^48).
+using npd::row_max4;
+using npd::row_sum4;
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 // ds_read_b64_tr_b16 on an LDS address given as a generic pointer to __shared__

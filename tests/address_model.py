@@ -70,32 +70,33 @@ def fast_score_floats(t: int, gp: int, fp8: bool, mma_pv: bool = False) -> int:
     return t * gp
 
 
+def prob_row(t: int) -> int:
+    """prob_row: row (elements) of the [GP][t] probabilities, 8 past a multiple of 16."""
+    return (t + 7) // 16 * 16 + 8
+
+
 def fast_prob_bytes(t: int, gp: int) -> int:
     """fast_prob_bytes: the FP8 probability region, at least the K tile."""
-    return 16 * K_ROW * 2 if t * gp * 2 < 16 * K_ROW * 2 else t * gp * 2
+    b = prob_row(t) * gp * 2
+    return 16 * K_ROW * 2 if b < 16 * K_ROW * 2 else b
 
 
-def online_probs(g: int) -> bool:
-    """online_probs: 16-head units form their probabilities in pass 1."""
-    return g > 8
+WIDE_LDS_BYTES = max(16 * V_ROW * 2, (WIDE_GROUP * 128 + WIDE_GROUP) * 4, 64 * WIDE_GROUP * 4)
+"""kWideLdsBytes: V tile, then O hand-off + 1/l, then merge weights, each from byte 0."""
+WIDE_RING_2B = 2   # NPD_WIDE_RING_2B: steps of K and V in flight, 16-head units
+WIDE_RING_FP8 = 4  # NPD_WIDE_RING_FP8
 
 
-def online_prob_bytes(t: int, gp: int) -> int:
-    """online_prob_bytes: the [GP][t] 2-byte probabilities (16-byte multiple)."""
-    return (t * gp * 2 + 15) // 16 * 16
+def wide_ring(fp8: bool) -> int:
+    """decode_attention.hip wide_ring."""
+    return WIDE_RING_FP8 if fp8 else WIDE_RING_2B
 
 
-def online_tile_bytes(g: int, gp: int, d: int) -> int:
-    """online_tile_bytes: K tile, V tile, O hand-off and merge weights, one after another."""
-    return max(16 * K_ROW * 2, 16 * V_ROW * 2, g * d * 4, 64 * gp * 4)
-
-
-WIDE_RING = 2      # NPD_WIDE_RING: ring multiple of 16-head units
-
-
-def ring_of(D: int, G: int = 1) -> int:
-    """decode_attention.hip ring_of: steps in flight per pass."""
-    return 2 * RING if D == 64 else (WIDE_RING * RING if G > 8 else RING)
+def ring_of(D: int, G: int = 1, fp8: bool = False) -> int:
+    """decode_attention.hip ring_of (wide_ring for 16-head units): steps in flight."""
+    if G == WIDE_GROUP:
+        return wide_ring(fp8)
+    return 2 * RING if D == 64 else RING
 
 # prefill_attention.hip constants
 KT = 64
@@ -232,13 +233,14 @@ def choose_partition(S, H, KV, D, bs, max_ctx, fp8) -> int:
     units = S * KV
     if use_fast_path(D, bs, S):
         gp = pow2ceil(H // KV)
-        top = FAST_MAX_PARTITION_FP8 if fp8 else FAST_MAX_PARTITION
-        min_items = FAST_MIN_ITEMS_FP8 if fp8 else FAST_MIN_ITEMS
+        wide = gp == WIDE_GROUP
+        top = FAST_MAX_PARTITION_FP8 if fp8 and not wide else FAST_MAX_PARTITION
+        min_items = FAST_MIN_ITEMS_FP8 if fp8 and not wide else FAST_MIN_ITEMS
         ps = top
         while ps >= 64:
             if ps <= bs:
                 return bs
-            if ps * gp <= FAST_MAX_SCORES and units * _ceil(max_ctx, ps) >= min_items:
+            if (ps * gp <= FAST_MAX_SCORES or wide) and units * _ceil(max_ctx, ps) >= min_items:
                 return ps
             ps >>= 1
         return bs if bs > 64 else 64
@@ -325,10 +327,10 @@ def decode_host(S, H, KV, bs, max_bps, fp8, D=128) -> DecodeLaunch:
         n = _ceil(n, 8 * split) * 8 * split
     L.grid = n
     gp = pow2ceil(G)
-    t = L.partition + 16 * ring_of(D, G)
+    t = L.partition + 16 * ring_of(D, G, fp8)
     mma_pv = D == 128 and MMA_PV_MIN_G <= G <= 8
-    if online_probs(G):
-        L.lds_floats = (online_prob_bytes(t, gp) + online_tile_bytes(G, gp, D)) // 4
+    if G == WIDE_GROUP:
+        L.lds_floats = WIDE_LDS_BYTES // 4
     else:
         L.lds_floats = fast_score_floats(t, gp, fp8, mma_pv) + (fast_prob_bytes(t, gp) // 4 if fp8 else 0)
     return L
@@ -473,30 +475,33 @@ def decode(W: Writes, L: DecodeLaunch, out: Buf, ws: Buf, seq_lens: np.ndarray,
     single = run & (nparts == 1)
     out_rows(single, "decode output rows")
     # LDS of the item's passes: scores s_p[tl * GP + h]; FP8 pools: 2-byte
-    # probabilities s_pb[h * tpad + tl] and pass 3's V tile / O exchange
+    # probabilities s_pb[h * prow + tl] and pass 3's V tile / O exchange
     ntok = np.minimum(ctx - part * ps, ps)   # ps: per item
-    ring = ring_of(D, L.G)
+    ring = ring_of(D, L.G, L.fp8)
     nsteps = _ceil(_ceil(np.maximum(ntok, 0), 16), ring) * ring
     if run.any():
         tpad = L.partition + 16 * ring
-        if online_probs(L.G):
-            # 16-head units: probabilities s_pb[h * tpad + tl] (2 bytes) from
-            # pass 1 to pass 3, then the tile region: K tile (pass 1), V tile
-            # (pass 3), O hand-off, merge weights s_w[lane * GP + h]
-            pb = online_prob_bytes(tpad, gp)
-            W.index(2 * ((L.G - 1) * tpad + nsteps[run] * 16 - 1) + 1, pb,
-                    "decode LDS probabilities (bytes)")
-            W.index([pb + 2 * (15 * K_ROW + 127) + 1, pb + 2 * (15 * V_ROW + 127) + 1,
-                     pb + 4 * L.G * D, pb + 4 * 64 * gp], L.lds_floats * 4 + 1,
-                    "decode LDS K / V tiles, O hand-off, merge weights (bytes)")
+        prow = prob_row(tpad)
+        if L.G == WIDE_GROUP:
+            # 16-head units (one pass): the V tile s_vt[row * V_ROW + col]
+            # (2 bytes), then from byte 0 the O hand-off s_o[h * D + d] and
+            # 1/l s_il[h] (4 bytes), then the merge weights s_w[lane * GP + h]
+            W.index([2 * (15 * V_ROW + 127) + 1, 4 * (L.G * D + L.G - 1) + 3, 4 * (63 * gp + L.G - 1) + 3],
+                    L.lds_floats * 4, "decode LDS V tile, O hand-off, 1/l, merge weights (bytes)")
+            # the transposing reads: lane (g4, n16) at row 4*g4 + n16/4, col
+            # nb*16 + 4*(n16%4) .. +3 (8 bytes)
+            lane = np.arange(64)
+            tr = 2 * (((lane >> 4) * 4 + ((lane & 15) >> 2)) * V_ROW + 4 * (lane & 3))
+            W.index(tr[:, None] + 2 * 16 * np.arange(D // 16)[None, :] + 7, L.lds_floats * 4,
+                    "decode LDS transposing V reads (bytes)")
         else:
             W.index(nsteps[run] * 16 * gp - 1, L.partition * gp + 16 * ring * gp, "decode LDS scores")
-        if L.fp8 and not online_probs(L.G):
-            # FP8 pools: 2-byte probabilities s_pb[h * tpad + tl] after the
+        if L.fp8 and L.G != WIDE_GROUP:
+            # FP8 pools: 2-byte probabilities s_pb[h * prow + tl] after the
             # scores, pass 1's K tile in that region first; pass 3's V tile and
             # the O exchange in the score region
             pb0 = fast_score_floats(tpad, gp, True) * 4   # bytes
-            W.index(pb0 + 2 * ((L.G - 1) * tpad + nsteps[run] * 16 - 1) + 1, L.lds_floats * 4,
+            W.index(pb0 + 2 * ((L.G - 1) * prow + nsteps[run] * 16 - 1) + 1, L.lds_floats * 4,
                     "decode LDS probabilities (bytes)")
             W.index([pb0 + 2 * (15 * K_ROW + 127) + 1], L.lds_floats * 4,
                     "decode LDS K tile in the probability region (bytes)")
