@@ -24,12 +24,13 @@
 // combines them (log-sum-exp merge). 2-byte pools with up to 4 heads per
 // group use no MFMA: at one query row per sequence the op is HBM-bound; with
 // 5-8 heads pass 3's fp32 products no longer keep up, and it runs on
-// v_mfma_f32_16x16x16 as below (the probabilities rounded to the pool type in
-// place). FP8 pools move half the bytes with
-// twice the conversions per byte, so their passes 1 and 3 stage each 16-token
-// step's converted K / V rows in LDS and run S = Q.K^T and O^T += V^T.P^T on
-// v_mfma_f32_16x16x16 (the G heads padded to 16): no reduce-scatter and no
-// per-element products on the VALU.
+// v_mfma_f32_16x16x16 (the probabilities rounded to the pool type in place).
+// Groups of 16 heads (2-byte pools) and every group of an FP8 pool run as
+// decode_wide_item units instead: one pass per partition with S^T = K.Q^T on
+// v_mfma_f32_16x16x32 (K read straight into the operand layout, the heads
+// padded to 16) and O^T += V^T.P^T on v_mfma_f32_16x16x16 (V staged in LDS),
+// probabilities formed against a per-head reference that moves only by more
+// than 2^8, and no score buffer.
 #include <type_traits>
 
 #include "common.h"
@@ -42,7 +43,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
-// O^T += V^T . P^T of FP8 pools' pass 3 on v_mfma_f32_16x16x16_{bf16,f16}:
+// O^T += V^T . P^T of the MFMA P.V steps on v_mfma_f32_16x16x16_{bf16,f16}:
 // A[m = lane%16][k = 4*(lane/16) + e], B[k = 4*(lane/16) + e][n = lane%16],
 // D[m = 4*(lane/16) + i][n = lane%16].
 template <class TT>
@@ -89,14 +90,10 @@ __device__ __forceinline__ u32x2 lds_read_tr(const uint16_t* p) {
   typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p)));
 }
-// LDS row (elements) of the 16-token V tile that FP8 pools' pass 3 stages: an
-// 8-bank shift per row, so the 4 rows x 32 bytes of a transposing read hit
-// distinct banks
+// LDS row (elements) of the 16-token V tile of the MFMA P.V steps: an 8-bank
+// shift per row, so the 4 rows x 32 bytes of a transposing read hit distinct
+// banks
 constexpr int kVRow = 128 + 16;
-// LDS row (elements) of the 16-token K tile of FP8 pools' pass 1: a 4-bank
-// shift per row, so the 16 rows x 8 bytes that 16 lanes read at one column
-// (and the two column groups of 32 lanes) hit distinct banks
-constexpr int kKRow = 128 + 8;
 
 constexpr int kMaxPartition = 512;   // tokens per partition, upper bound (LDS sizing)
 constexpr int kStep = 16;            // tokens per step
@@ -134,11 +131,6 @@ constexpr int64_t kFastMinItems = 1280;
 // fast path, at most 64 sequences: the kernel halves the host's partition
 // (down to a quarter of it) while the actual contexts give fewer items
 constexpr int kFastMinItemsActual = 1024;
-// FP8 pools: a row is half the bytes, so a wave has half the bytes in flight
-// and more, shorter items keep HBM busy: at least 4096 items, partitions of at
-// most 256 tokens
-constexpr int64_t kFastMinItemsFp8 = 4096;
-constexpr int kFastMaxPartitionFp8 = 256;
 #ifndef NPD_DECODE_INLINE_SCHED_MAX
 #define NPD_DECODE_INLINE_SCHED_MAX 64
 #endif
@@ -771,57 +763,28 @@ __host__ __device__ constexpr bool mma_pv_2byte(int d, int g) {
 // 16 heads as cheaply as 8, and the kv head's K/V rows are read once instead
 // of once per 8-head sub-group.
 constexpr int kWideGroup = 16;
-// decode_fast_item runs passes 1 and 3 on the matrix cores for FP8 pools
-__host__ __device__ constexpr bool mma_passes(bool fp8, int) { return fp8; }
+// FP8 pools run every group as decode_wide_item units too (padded to 16 MFMA
+// columns): its 16-byte loads cover whole rows, and at config 2 it beats the
+// LDS-staged two-pass form for every group size (48.0 against 51.0 us with 4
+// heads, 51.4 against 63.5 with 8).
+__host__ __device__ constexpr bool wide_item(bool fp8, int g) { return g == kWideGroup || fp8; }
 // Floats of the fast path's score region for t tokens (incl. ring padding):
-// FP8 pools' pass 3 stages its 16 x kVRow V tile there, and the O hand-off
-// after it needs G x D floats of it; 2-byte pools with an MFMA pass 3 keep
-// their 2-byte probabilities in its first half and the V tile after them.
-__host__ __device__ constexpr int fast_score_floats(int t, int gp, bool fp8, bool mma_pv = false) {
-  return fp8 ? (t * gp < 16 * kVRow / 2 ? 16 * kVRow / 2 : t * gp)
-             : mma_pv ? (t * gp < t * gp / 2 + 16 * kVRow / 2 ? t * gp / 2 + 16 * kVRow / 2 : t * gp)
-                      : t * gp;
-}
-// Row (elements) of the [GP][t] 2-byte probabilities: at least t, and 8 more
-// than a multiple of 16, so that a row is an odd multiple of 16 bytes modulo
-// 32. Pass 3 reads 8 bytes per lane, lane (g4, n16) at row n16, column 4*g4:
-// in each 32-lane half the 16 rows then start on distinct even 8-byte bank
-// pairs and the two columns fill the odd ones, 256 distinct bytes (the same
-// rule as the K tile's kKRow); a power-of-two row put all 16 rows on the same
-// banks.
-__host__ __device__ constexpr int prob_row(int t) { return (t + 7) / 16 * 16 + 8; }
-// Bytes of FP8 pools' probability region ([GP][prob_row(t)] 2-byte values):
-// pass 1 stages its 16 x kKRow K tile there first.
-__host__ __device__ constexpr int fast_prob_bytes(int t, int gp) {
-  return prob_row(t) * gp * 2 < 16 * kKRow * 2 ? 16 * kKRow * 2 : prob_row(t) * gp * 2;
+// 2-byte pools with an MFMA pass 3 keep their 2-byte probabilities in its
+// first half and the V tile after them.
+__host__ __device__ constexpr int fast_score_floats(int t, int gp, bool mma_pv = false) {
+  return mma_pv ? (t * gp < t * gp / 2 + 16 * kVRow / 2 ? t * gp / 2 + 16 * kVRow / 2 : t * gp)
+                : t * gp;
 }
 __host__ __device__ constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
-// Element source of the fast path. 2-byte pools: a lane's 8 elements are one
-// 16-byte load, used as 4 packed pairs. FP8 pools (kF8): 8 e4m3 bytes, one
-// 8-byte load (the same index arithmetic in 8-byte units, a head row being 128
-// bytes), converted exactly to 4 pairs of TT by v_cvt_scalef32_pk_*_fp8 with
-// scale 1 (the per-head scales are applied in fp32: to the scores and to the
-// output).
-template <class TT, bool kF8>
-struct KvSrc {
-  typedef u32x4 raw;
-  static __device__ __forceinline__ raw load(const void* base, int64_t idx) {
-    return ld_stream(static_cast<const u32x4*>(base) + idx);
-  }
-  static __device__ __forceinline__ u32x4 pairs(raw w) { return w; }
-};
+// FP8 (e4m3) element pairs: 8 bytes -> 4 pairs of TT, exact, by
+// v_cvt_scalef32_pk_*_fp8 with scale 1 (the per-head scales are applied in
+// fp32: to the scores and to the output).
 template <class TT>
-struct KvSrc<TT, true> {
-  typedef u32x2 raw;
-  static __device__ __forceinline__ raw load(const void* base, int64_t idx) {
-    return __builtin_nontemporal_load(static_cast<const u32x2*>(base) + idx);
-  }
-  static __device__ __forceinline__ u32x4 pairs(raw w) {
-    return u32x4{npd::e4m3x2_to<TT, false>(w.x), npd::e4m3x2_to<TT, true>(w.x),
-                 npd::e4m3x2_to<TT, false>(w.y), npd::e4m3x2_to<TT, true>(w.y)};
-  }
-};
+__device__ __forceinline__ u32x4 e4m3x8_to(u32x2 w) {
+  return u32x4{npd::e4m3x2_to<TT, false>(w.x), npd::e4m3x2_to<TT, true>(w.x),
+               npd::e4m3x2_to<TT, false>(w.y), npd::e4m3x2_to<TT, true>(w.y)};
+}
 
 // Slot of partition `part`'s partial: its own slot, or its merge group's
 // result slot when long contexts merge in groups and its group has only it.
@@ -886,14 +849,11 @@ __device__ __forceinline__ void merge_tail(const DecodeArgs& a, int unit, int pa
   }
 }
 
-template <class TT, int D, int G, int SPB, bool kF8 = false>
+template <class TT, int D, int G, int SPB>
 __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, int part,
-                                                 int ps, float* s_p, uint16_t* s_pb,
-                                                 uint16_t* s_v) {
-  typedef KvSrc<TT, kF8> Src;
-  typedef typename Src::raw raw_t;
+                                                 int ps, float* s_p) {
+  typedef u32x4 raw_t;
   static_assert(D == 64 || D == 128 || D == 256, "head dims of the fast path");
-  static_assert(!kF8 || D == 128, "FP8 pools: head_dim 128");
   constexpr int LPT = D / 8;            // lanes per token row (16-byte chunks)
   constexpr int TPL = 64 / LPT;         // token rows per load
   constexpr int NL = 16 / TPL;          // loads per 16-token step (token slots)
@@ -908,21 +868,12 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
   constexpr int NTS = NH > LGP ? NH - LGP : 0;   // token bits split by stages
   constexpr int BS = 16 * SPB;
   constexpr int NBUF = ring_of(D);   // steps in flight per pass
-  // passes 1 and 3 on the matrix cores for FP8 pools (2-byte probabilities,
-  // K and V staged in LDS as TT; their short partitions leave LDS room for
-  // both), else on the VALU with fp32 probabilities
-  constexpr bool kMma = mma_passes(kF8, G);
   static_assert(G <= 8, "group sizes of decode_fast_item (16-head units: decode_wide_item)");
-  // 2-byte pools with 5-8 heads: pass 3 on the matrix cores too, with the
+  // 5-8 heads (head dim 128): pass 3 on the matrix cores, with the
   // probabilities rounded to TT in place (token-major pairs in the first half
   // of the score region) and the V tile after them
-  constexpr bool kMmaPv2 = !kMma && mma_pv_2byte(D, G);
-  constexpr bool kMmaPv = kMma || kMmaPv2;
+  constexpr bool kMmaPv = mma_pv_2byte(D, G);
   const int tmax = a.partition + 16 * NBUF;   // tokens incl. ring padding
-  const int prow = prob_row(tmax);             // row of s_pb (elements)
-  constexpr int MAXT = kFastMaxPartition + 16 * NBUF;   // tokens incl. ring padding
-
-  (void)MAXT;
   const int lane = threadIdx.x;
   const int r = lane / LPT, j = lane % LPT;
   const int s = unit / a.num_kv_heads;
@@ -958,10 +909,9 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
 #pragma unroll
   for (int t = 0; t < NTS; ++t) tokhi |= stage_coord<D>(j, LGP + t) << (NLB - 1 - t);
 
-  // q slot h holds head h ^ headmask of the group (zeros for padding heads;
-  // VALU pass 1 only)
-  u32x4 qv[kMma ? 1 : GP];
-  if constexpr (!kMma) {
+  // q slot h holds head h ^ headmask of the group (zeros for padding heads)
+  u32x4 qv[GP];
+  {
     const uint16_t* qb = a.q + s * a.q_stride_seq + (kh * G) * a.q_stride_head + j * 8;
 #pragma unroll
     for (int h = 0; h < GP; ++h) {
@@ -982,10 +932,9 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
     if (lane + 64 < nb) myblk1 = clamp_blk(row[lane + 64]);
   }
   const int voff = lane;   // offset (in lane chunks) of the lane's chunk r * LPT + j: slot i is token i*TPL + r
-  // scores in log2 units (times the K scale of an fp8 pool); output scale
   const int pkh = kh / a.kv_split;   // the unit's kv head in the pool
-  const float score_scale = kF8 ? a.scale_log2 * a.k_scale[pkh] : a.scale_log2;
-  const float out_scale = kF8 ? a.v_scale[pkh] : 1.f;
+  const float score_scale = a.scale_log2;   // scores in log2 units
+  constexpr float out_scale = 1.f;
 
   const int64_t head_rows = (int64_t)pkh * BS;            // rows of head pkh in a block
   const int64_t blk_rows = (int64_t)a.pool_kv_heads * BS; // rows per block
@@ -999,66 +948,21 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
   auto load_k = [&](raw_t* buf, int st) {
     const int64_t b = step_base(st) + voff;
 #pragma unroll
-    for (int i = 0; i < NL; ++i) buf[i] = Src::load(a.k_cache, b + i * 64);
+    for (int i = 0; i < NL; ++i) buf[i] = ld_stream(static_cast<const u32x4*>(a.k_cache) + b + i * 64);
   };
   auto load_v = [&](raw_t* buf, int st) {
     const int64_t b = step_base(st) + voff;
 #pragma unroll
-    for (int i = 0; i < NL; ++i) buf[i] = Src::load(a.v_cache, b + i * 64);
+    for (int i = 0; i < NL; ++i) buf[i] = ld_stream(static_cast<const u32x4*>(a.v_cache) + b + i * 64);
   };
 
   // ---------------- pass 1: scores ----------------
   float runmax = -INFINITY;   // max of the scores this lane stored (its head: headmask)
-  // MFMA passes (FP8 pools): S = Q . K^T on the matrix cores.
-  // A = Q[head n16][dims c*16 + 4*g4 .. +3] (zeros past the group), B = K^T
-  // from the step's K rows staged in LDS (row = token of the step),
-  // D[head 4*g4 + i][token n16]: each lane ends with the scores of 4 heads of
-  // one token, no reduce-scatter; the scores (fp32) are stored for pass 2.
-  // (Forming the probabilities in the same step against a moving reference,
-  // as 16-head units do, costs these units more in row reductions than the
-  // pass it removes: 52.6 against 50.9 us at config 2.)
-  const int g4 = lane >> 4, n16 = lane & 15;
-  constexpr int NQC = kMma ? D / 16 : 1;
-  u32x2 qa[NQC];
-  if constexpr (kMma) {
-    const uint16_t* qrow = a.q + s * a.q_stride_seq + (kh * G + n16) * a.q_stride_head + 4 * g4;
-#pragma unroll
-    for (int c = 0; c < NQC; ++c)
-      qa[c] = n16 < G ? *reinterpret_cast<const u32x2*>(qrow + c * 16) : u32x2{0, 0};
-  }
-  // pass 1's K tile: the probability region, which pass 2 fills afterwards
-  uint16_t* s_k = s_pb;
-  float runmax4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};   // stored scores: heads 4*g4 + i
-  auto score_step_mma = [&](const raw_t* kraw, int st) {
-#pragma unroll
-    for (int i = 0; i < NL; ++i)
-      *reinterpret_cast<u32x4*>(&s_k[(i * TPL + r) * kKRow + j * 8]) = Src::pairs(kraw[i]);
-    f32x4 sacc = f32x4{0, 0, 0, 0};
-#pragma unroll
-    for (int c = 0; c < NQC; ++c)
-      sacc = Mfma16<TT>::mma(qa[c], *reinterpret_cast<const u32x2*>(&s_k[n16 * kKRow + c * 16 + 4 * g4]),
-                             sacc);
-    const int tl = st * 16 + n16;
-    // scores to LDS; pass 2 forms the probabilities against the exact maxima
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int h = 4 * g4 + i;
-      if (h < G) {
-        // rows past the context may hold anything: select, not scale
-        const float sv = (tl < ntok) ? sacc[i] * score_scale : -INFINITY;
-        s_p[tl * GP + h] = sv;
-        runmax4[i] = fmaxf(runmax4[i], sv);
-      }
-    }
-  };
   auto score_step = [&](const raw_t* kraw, int st) {
-    if constexpr (kMma) {
-      score_step_mma(kraw, st);
-    } else {
     float v[NV];   // v[h * NL + i]: q slot h . token slot i
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
-      const u32x4 kbi = Src::pairs(kraw[i]);
+      const u32x4 kbi = kraw[i];
 #pragma unroll
       for (int h = 0; h < GP; ++h) {
         float d = TT::dot2(kbi.x, qv[h].x, 0.f);
@@ -1085,7 +989,6 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
         s_p[tl * GP + h] = sv;
         runmax = fmaxf(runmax, sv);
       }
-    }
     }
   };
   {
@@ -1118,27 +1021,11 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
   float m[GP], l[GP];
 #pragma unroll
   for (int h = 0; h < GP; ++h) {
-    if constexpr (kMma) {
-      m[h] = h < G ? wave_max_f(g4 == h / 4 ? runmax4[h % 4] : -INFINITY) : -INFINITY;
-      l[h] = 0.f;
-    } else {
-      m[h] = h < G ? wave_max_f(headmask == h ? runmax : -INFINITY) : -INFINITY;
-      l[h] = 0.f;
-    }
+    m[h] = h < G ? wave_max_f(headmask == h ? runmax : -INFINITY) : -INFINITY;
+    l[h] = 0.f;
   }
   const int ntl = nsteps * 16;
-  if constexpr (kMma) {
-  // 2-byte probabilities, head-major (s_pb[h * prow + t]): the B operand of
-  // pass 3's MFMAs. l sums the rounded values, so the normalisation matches.
-  for (int t = lane; t < ntl; t += 64) {
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const uint32_t u = TT::from_float(__builtin_amdgcn_exp2f(s_p[t * GP + h] - m[h]));
-      l[h] += TT::lo(u);
-      s_pb[h * prow + t] = (uint16_t)u;
-    }
-  }
-  } else if constexpr (kMmaPv2) {
+  if constexpr (kMmaPv) {
   // probabilities rounded to TT, token-major pairs written in place: the word
   // t * GP/2 + k holds heads 2k, 2k + 1 of token t. A word lands on the
   // scores of token (t * GP/2 + k) / GP <= t/2, which every lane has read
@@ -1185,16 +1072,17 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[h][d] = 0.f;
   constexpr int NOB = kMmaPv ? D / 16 : 1;   // 16-dim blocks of O^T (MFMA path)
-  // V tile of an MFMA pass 3 (FP8: s_v; 2-byte pools: after the in-place
-  // probabilities, tmax * GP/2 floats into the score region)
-  uint16_t* s_vt = kMmaPv2 ? reinterpret_cast<uint16_t*>(s_p + tmax * (GP / 2)) : s_v;
+  // V tile of the MFMA pass 3: after the in-place probabilities, tmax * GP/2
+  // floats into the score region
+  uint16_t* s_vt = reinterpret_cast<uint16_t*>(s_p + tmax * (GP / 2));
+  const int g4 = lane >> 4, n16 = lane & 15;
   f32x4 oacc[NOB];
 #pragma unroll
   for (int nb = 0; nb < NOB; ++nb) oacc[nb] = f32x4{0, 0, 0, 0};
   auto pv_step = [&](const raw_t* vraw, int st) {
     u32x4 vbuf[NL];
 #pragma unroll
-    for (int i = 0; i < NL; ++i) vbuf[i] = Src::pairs(vraw[i]);
+    for (int i = 0; i < NL; ++i) vbuf[i] = vraw[i];
     if (st * 16 + 16 > ntok) {   // tail step: rows past the context may hold anything
 #pragma unroll
       for (int i = 0; i < NL; ++i)
@@ -1207,18 +1095,14 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
       *reinterpret_cast<u32x4*>(&s_vt[(i * TPL + r) * kVRow + j * 8]) = vbuf[i];
     // B: probabilities of tokens st*16 + 4*g4 .. +3 for head n16 (0 past the group)
     u32x2 pbv = u32x2{0, 0};
-    if constexpr (kMma) {
-      if (n16 < G) pbv = *reinterpret_cast<const u32x2*>(&s_pb[n16 * prow + st * 16 + 4 * g4]);
-    } else {
-      if (n16 < G) {
-        uint32_t w[4];
+    if (n16 < G) {
+      uint32_t w[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t pr = __float_as_uint(s_p[(st * 16 + 4 * g4 + e) * (GP / 2) + (n16 >> 1)]);
-          w[e] = (n16 & 1) ? (pr >> 16) : (pr & 0xffffu);
-        }
-        pbv = u32x2{w[0] | (w[1] << 16), w[2] | (w[3] << 16)};
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t pr = __float_as_uint(s_p[(st * 16 + 4 * g4 + e) * (GP / 2) + (n16 >> 1)]);
+        w[e] = (n16 & 1) ? (pr >> 16) : (pr & 0xffffu);
       }
+      pbv = u32x2{w[0] | (w[1] << 16), w[2] | (w[3] << 16)};
     }
     // A: V^T[dim nb*16 + n16][tokens 4*g4 .. +3] by transposing reads (lane
     // (g4, n16) addresses token 4*g4 + n16/4, dims nb*16 + 4*(n16%4) .. +3)
@@ -1358,13 +1242,13 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
 constexpr int kWideLdsBytes =
     cmax(cmax(16 * kVRow * 2, (kWideGroup * 128 + kWideGroup) * 4), 64 * kWideGroup * 4);
 
-// 16-head units (G = 16, D = 128): one pass over the partition. Per 16-token
+// Units of 16 heads of a 2-byte pool, and any group of an FP8 pool (padded to
+// 16 with zero queries), D = 128: one pass over the partition. Per 16-token
 // step of the unit's kv head:
 //   S^T = K . Q^T on v_mfma_f32_16x16x32 (4 chunks of 32 dims). Its A
-//     operand comes straight from the pool: lane (g4, n16) loads the 16 bytes
-//     (8 bytes for FP8, converted) of token n16's row at dims 32c + 8*g4, so
-//     chunk c's load covers 64 bytes of each of the step's 16 rows and the
-//     four cover them whole. Lane (g4, n16) ends with the scores of tokens
+//     operand comes straight from the pool: lane (g4, n16) loads 16 bytes of
+//     token n16's row (see load_k), so each load covers 64 contiguous bytes of
+//     every row of the step. Lane (g4, n16) ends with the scores of tokens
 //     4*g4 + i of head n16.
 //   The head's step max (its 4 scores, then the 4 rows by v_permlane16/32_swap)
 //     moves the head's reference only when it exceeds it by more than
@@ -1376,11 +1260,11 @@ constexpr int kWideLdsBytes =
 // No probability or score buffer: LDS is the V tile and the hand-off, so the
 // partition is as long as the 2-byte path's and many waves fit a CU. K and V
 // loads run NBUF steps ahead in a register ring.
-template <class TT, int SPB, bool kF8>
+template <class TT, int G, int SPB, bool kF8>
 __device__ __forceinline__ void decode_wide_item(const DecodeArgs& a, int unit, int part, int ps,
                                                  float* s_lds) {
-  typedef KvSrc<TT, kF8> Src;
-  constexpr int D = 128, G = kWideGroup;
+  constexpr int D = 128;
+  static_assert(G <= kWideGroup, "a unit's heads fill at most the 16 MFMA columns");
   constexpr int LPT = D / 8;        // 16-byte chunks (FP8: 8-byte) per row
   constexpr int TPL = 64 / LPT;     // rows per coalesced load
   constexpr int NL = 16 / TPL;      // coalesced V loads per step
@@ -1462,9 +1346,10 @@ __device__ __forceinline__ void decode_wide_item(const DecodeArgs& a, int unit, 
   {
     const uint16_t* qrow = a.q + s * a.q_stride_seq + (kh * G + n16) * a.q_stride_head;
 #pragma unroll
-    for (int c = 0; c < NKC; ++c)
-      qb[c] = *reinterpret_cast<const u32x4*>(qrow + (kF8 ? 64 * (c / 2) + 16 * g4 + 8 * (c % 2)
-                                                          : 32 * c + 8 * g4));
+    for (int c = 0; c < NKC; ++c)   // zeros past the group
+      qb[c] = n16 < G ? *reinterpret_cast<const u32x4*>(
+                            qrow + (kF8 ? 64 * (c / 2) + 16 * g4 + 8 * (c % 2) : 32 * c + 8 * g4))
+                      : u32x4{0, 0, 0, 0};
   }
   uint16_t* s_vt = reinterpret_cast<uint16_t*>(s_lds);
   // A of the P.V MFMA: V^T[dim nb*16 + n16][tokens 4*g4 .. +3] by transposing
@@ -1486,8 +1371,8 @@ __device__ __forceinline__ void decode_wide_item(const DecodeArgs& a, int unit, 
 #pragma unroll
       for (int i = 0; i < NVL; ++i) {
         const int row = 8 * i + (lane >> 3), c16 = lane & 7;
-        u32x4 v0 = Src::pairs(u32x2{vraw[i].x, vraw[i].y});
-        u32x4 v1 = Src::pairs(u32x2{vraw[i].z, vraw[i].w});
+        u32x4 v0 = e4m3x8_to<TT>(u32x2{vraw[i].x, vraw[i].y});
+        u32x4 v1 = e4m3x8_to<TT>(u32x2{vraw[i].z, vraw[i].w});
         if (tail && st * 16 + row >= ntok) v0 = v1 = u32x4{0, 0, 0, 0};
         *reinterpret_cast<u32x4*>(&s_vt[row * kVRow + c16 * 16]) = v0;
         *reinterpret_cast<u32x4*>(&s_vt[row * kVRow + c16 * 16 + 8]) = v1;
@@ -1505,8 +1390,8 @@ __device__ __forceinline__ void decode_wide_item(const DecodeArgs& a, int unit, 
 #pragma unroll
     for (int c = 0; c < NKL; ++c) {
       if constexpr (kF8) {
-        sacc = MfmaK32<TT>::mma(Src::pairs(u32x2{kraw[c].x, kraw[c].y}), qb[2 * c], sacc);
-        sacc = MfmaK32<TT>::mma(Src::pairs(u32x2{kraw[c].z, kraw[c].w}), qb[2 * c + 1], sacc);
+        sacc = MfmaK32<TT>::mma(e4m3x8_to<TT>(u32x2{kraw[c].x, kraw[c].y}), qb[2 * c], sacc);
+        sacc = MfmaK32<TT>::mma(e4m3x8_to<TT>(u32x2{kraw[c].z, kraw[c].w}), qb[2 * c + 1], sacc);
       } else {
         sacc = MfmaK32<TT>::mma(kraw[c], qb[c], sacc);
       }
@@ -1587,7 +1472,7 @@ __device__ __forceinline__ void decode_wide_item(const DecodeArgs& a, int unit, 
     }
   }
   if (base < 0) return;
-  if (g4 == 0) st_coherent2(a.part_ml + (base * G + n16) * 2, mref, lsum);
+  if (g4 == 0 && n16 < G) st_coherent2(a.part_ml + (base * G + n16) * 2, mref, lsum);
   merge_tail<TT, D, G>(a, unit, part, nparts, s, kh, lane, s_lds, out_scale);
 }
 
@@ -1599,32 +1484,14 @@ __device__ __forceinline__ void decode_wide_item(const DecodeArgs& a, int unit, 
 // workgroups past the list (all at the end of the grid) exit at once.
 // LDS is dynamic, sized for the launch's partition (fast_lds_bytes).
 template <class TT, int D, int G, int SPB, bool kF8>
-// FP8 pools with up to 4 heads per group: at most 128 VGPRs, four waves per
-// SIMD (the MFMA pass 3 would otherwise take the kernel to 148). Head dim 128
-// with 5-8 heads per group: at most 168, three waves per SIMD (1-4% faster
-// than 8 waves per CU at 180-212). 16-head units (decode_wide_item): at most
-// 256; they take 149 (2-byte) and 163 (FP8), three waves per SIMD (four, at
-// 128, ran 5% slower).
+// Head dim 128 with 5-8 heads per group: at most 168 VGPRs, three waves per
+// SIMD (1-4% faster than 8 waves per CU at 180-212). decode_wide_item units:
+// at most 256; they take 149 (2-byte) and 163 (FP8), three waves per SIMD
+// (four, at 128, ran 5% slower).
 __global__ __launch_bounds__(64)
-__attribute__((amdgpu_waves_per_eu(kF8 && G <= 4 ? 4 : (D == 128 && G >= 5 && G <= 8 ? 3 : (G > 8 ? 2 : 1)))))
+__attribute__((amdgpu_waves_per_eu(wide_item(kF8, G) ? 2 : (D == 128 && G >= 5 && G <= 8 ? 3 : 1))))
 void decode_fast_kernel(DecodeArgs a) {
-  constexpr int GP = pow2ceil(G);
   extern __shared__ __attribute__((aligned(16))) float s_dyn[];
-  float* s_p = s_dyn;   // [partition + ring padding][GP] scores
-  // FP8 pools: [GP][partition + ring padding] 2-byte probabilities after the
-  // scores; pass 3's [16][kVRow] V tile reuses the scores' region (no longer
-  // read once the probabilities are out), which is sized to hold it
-  const int tpad = a.partition + 16 * ring_of(D);
-  constexpr bool kMma = mma_passes(kF8, G);
-  uint16_t* s_pb = nullptr;
-  uint16_t* s_v = nullptr;
-  if constexpr (kMma) {
-    // FP8 pools: [GP][prob_row(tpad)] 2-byte probabilities after the scores; pass 3's
-    // [16][kVRow] V tile reuses the scores' region (no longer read once the
-    // probabilities are out), which is sized to hold it
-    s_pb = reinterpret_cast<uint16_t*>(s_dyn + fast_score_floats(tpad, GP, true));
-    s_v = reinterpret_cast<uint16_t*>(s_dyn);
-  }
   int unit, part, ps = a.partition;
   if (a.num_seqs <= kInlineSchedMax) {
     // Small batch: every workgroup derives its item from seq_lens alone, in
@@ -1729,10 +1596,10 @@ void decode_fast_kernel(DecodeArgs a) {
     unit = it.x;
     part = it.y;
   }
-  if constexpr (G == kWideGroup)
-    decode_wide_item<TT, SPB, kF8>(a, unit, part, ps, s_dyn);
+  if constexpr (wide_item(kF8, G))
+    decode_wide_item<TT, G, SPB, kF8>(a, unit, part, ps, s_dyn);
   else
-    decode_fast_item<TT, D, G, SPB, kF8>(a, unit, part, ps, s_p, s_pb, s_v);
+    decode_fast_item<TT, D, G, SPB>(a, unit, part, ps, s_dyn);
 }
 
 // Builds the work list of decode_fast_kernel (one workgroup):
@@ -1841,7 +1708,10 @@ bool use_fast_path(int64_t head_dim, int64_t block_size, int64_t num_seqs) {
 // latency (work-list lookup, q load, the softmax pass over LDS, publishing
 // its partial) that the streaming loops of other waves hide only in part,
 // and 1280 waves with two 16-token steps in flight each still keep HBM busy.
-// FP8 pools follow kFastMinItemsFp8 / kFastMaxPartitionFp8. The generic path
+// decode_wide_item units (16 heads; every FP8 group) have no score buffer,
+// so no score limit: for FP8 pools the 2-byte rules beat shorter partitions
+// (57.6 against 72 us at 256 tokens and 4096 items, config 2 with 128 q
+// heads; 88 against 94 us at 1024 tokens with 256 q heads). The generic path
 // uses 512 or 256. The workspace is sized with the same rule.
 int choose_partition(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
                      int64_t block_size, int64_t max_ctx, bool fp8) {
@@ -1851,17 +1721,11 @@ int choose_partition(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads, 
     if (NPD_DECODE_PARTITION >= block_size) return NPD_DECODE_PARTITION;
 #endif
     const int gp = pow2ceil((int)(num_heads / num_kv_heads));
-    // 16-head units: LDS independent of the partition; FP8 pools' 16-byte
-    // loads cover whole rows, and the 2-byte rules serve them best too
-    // (57.6 against 72 us at 256 tokens and 4096 items, config 2 with 128 q
-    // heads; 88 against 94 us at 1024 tokens with 256 q heads)
-    const bool wide = gp == kWideGroup;
-    const int top = fp8 && !wide ? kFastMaxPartitionFp8 : kFastMaxPartition;
-    const int64_t min_items = fp8 && !wide ? kFastMinItemsFp8 : kFastMinItems;
-    for (int ps = top; ps >= 64; ps >>= 1) {
+    const bool wide = wide_item(fp8, (int)(num_heads / num_kv_heads));
+    for (int ps = kFastMaxPartition; ps >= 64; ps >>= 1) {
       if (ps <= block_size) return (int)block_size;
       if (ps * gp > kFastMaxScores && !wide) continue;
-      if (units * ((max_ctx + ps - 1) / ps) >= min_items) return ps;
+      if (units * ((max_ctx + ps - 1) / ps) >= kFastMinItems) return ps;
     }
     return block_size > 64 ? (int)block_size : 64;
   }
@@ -1869,10 +1733,9 @@ int choose_partition(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads, 
 }
 
 // Shortest partition the fast path's kernel may take for a host partition ps
-// (2-byte pools: down to ps / 4, never below 64 tokens or the block); the
-// workspace and the grid are sized for it.
-int fast_min_partition(int ps, int64_t block_size, bool fp8) {
-  if (fp8) return ps;
+// (down to ps / 4, never below 64 tokens or the block); the workspace and the
+// grid are sized for it.
+int fast_min_partition(int ps, int64_t block_size) {
   int lo = ps / 4;
   lo = lo < 64 ? 64 : lo;
   lo = lo < block_size ? (int)block_size : lo;
@@ -1899,16 +1762,13 @@ int64_t fast_grid(const DecodeArgs& a, int64_t units) {
 }
 
 // Dynamic LDS of decode_fast_kernel for a partition: scores (fp32) of every
-// token of the partition plus the ring padding (for FP8 pools at least the
-// 16-row V tile of pass 3's MFMAs, which reuses that region), then for FP8
-// pools the 2-byte probabilities (at least pass 1's 16-row K tile, which
-// reuses that region). 16-head units: kWideLdsBytes, for any partition.
+// token of the partition plus the ring padding (decode_fast_item; see
+// fast_score_floats), or kWideLdsBytes for decode_wide_item units, for any
+// partition.
 int64_t fast_lds_bytes(int partition, int g, bool fp8, int d) {
+  if (wide_item(fp8, g)) return kWideLdsBytes;
   const int t = partition + 16 * ring_of(d);
-  const int gp = pow2ceil(g);
-  if (g == kWideGroup) return kWideLdsBytes;
-  return (int64_t)fast_score_floats(t, gp, fp8, mma_pv_2byte(d, g)) * 4 +
-         (fp8 ? fast_prob_bytes(t, gp) : 0);
+  return (int64_t)fast_score_floats(t, pow2ceil(g), mma_pv_2byte(d, g)) * 4;
 }
 
 template <class TT, int D, int G, int SPB, bool kF8 = false>
@@ -2080,12 +1940,12 @@ extern "C" int64_t npd_paged_attention_workspace_size(int64_t num_seqs, int64_t 
   // fast path: counter region, item count (16 B), work list, partials of the
   // partitions and of the merge groups; enough for a 2-byte pool and, for the
   // block sizes the FP8 entry point takes, an FP8 pool (whose partitions may
-  // be shorter)
+  // differ: no score limit)
   const int64_t units = num_seqs * num_kv_heads;
   auto need = [&](bool fp8) {
     const int ps = fast_min_partition(
         choose_partition(num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_ctx, fp8),
-        block_size, fp8);
+        block_size);
     const int64_t parts = (max_ctx + ps - 1) / ps;
     const int64_t slots = parts + merge_groups(true, units, parts);
     return (npd::kCounterBytes + 16 + units * parts * 8 + 255) / 256 * 256 +
@@ -2159,7 +2019,7 @@ int attention_check(const void* out, const void* query, const void* key_cache,
   if (partition > limit)
     return fail(NPD_E_INVALID, "%s: block_size %lld is above %d", name, (long long)block_size,
                 limit);
-  const int min_partition = fast ? fast_min_partition(partition, block_size, fp8) : partition;
+  const int min_partition = fast ? fast_min_partition(partition, block_size) : partition;
   if ((max_ctx + min_partition - 1) / min_partition > 65535)
     return fail(NPD_E_INVALID, "%s: context too long", name);
   if (num_seqs * num_kv_heads > kMaxCounters)
@@ -2195,7 +2055,7 @@ int attention_impl(void* out, const void* query, const void* key_cache, const vo
   const int partition =
       choose_partition(num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_ctx, fp8);
   const bool fast = use_fast_path(head_dim, block_size, num_seqs);
-  const int min_partition = fast ? fast_min_partition(partition, block_size, fp8) : partition;
+  const int min_partition = fast ? fast_min_partition(partition, block_size) : partition;
   // partial slots per unit: for the shortest partition the kernel may take
   const int64_t max_parts = (max_ctx + min_partition - 1) / min_partition;
   const int64_t need = npd_paged_attention_workspace_size(num_seqs, num_heads, pool_kv_heads,

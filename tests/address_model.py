@@ -36,49 +36,30 @@ FAST_MAX_PARTITION = 2048
 FAST_MAX_SCORES = 4096
 FAST_MIN_ITEMS = 1280
 FAST_MIN_ITEMS_ACTUAL = 1024
-FAST_MIN_ITEMS_FP8 = 4096
-FAST_MAX_PARTITION_FP8 = 256
 INLINE_SCHED_MAX = 64
 SCHED_MAX_SEQS = 4096
 MERGE_GROUP = 16
 RING = 2
 
 
-V_ROW = 128 + 16   # elements per row of the FP8 pass-3 V tile in LDS (kVRow)
-
-
-K_ROW = 128 + 8    # elements per row of the FP8 pass-1 K tile in LDS (kKRow)
+V_ROW = 128 + 16   # elements per row of the MFMA P.V steps' V tile in LDS (kVRow)
 
 
 MMA_PV_MIN_G = 5   # kMmaPvMinG: 2-byte pools at head dim 128 from this group size
-WIDE_GROUP = 16    # kWideGroup: heads of a unit whose passes both run on the matrix cores
+WIDE_GROUP = 16    # kWideGroup: heads of a decode_wide_item unit
 
 
-def mma_passes(fp8: bool, g: int) -> bool:
-    """mma_passes: passes 1 and 3 on the matrix cores (FP8 pools, 16-head units)."""
-    return fp8 or g > 8
+def wide_item(fp8: bool, g: int) -> bool:
+    """wide_item: 16-head units of 2-byte pools and every group of an FP8 pool."""
+    return g == WIDE_GROUP or fp8
 
 
-def fast_score_floats(t: int, gp: int, fp8: bool, mma_pv: bool = False) -> int:
-    """fast_score_floats: the score region; at least the FP8 V tile (and the
-    O hand-off), and for a 2-byte MFMA pass 3 the in-place probabilities plus
-    the V tile."""
-    if fp8:
-        return 16 * V_ROW // 2 if t * gp < 16 * V_ROW // 2 else t * gp
+def fast_score_floats(t: int, gp: int, mma_pv: bool = False) -> int:
+    """fast_score_floats: the score region; for a 2-byte MFMA pass 3 at least
+    the in-place probabilities plus the V tile."""
     if mma_pv:
         return max(t * gp, t * gp // 2 + 16 * V_ROW // 2)
     return t * gp
-
-
-def prob_row(t: int) -> int:
-    """prob_row: row (elements) of the [GP][t] probabilities, 8 past a multiple of 16."""
-    return (t + 7) // 16 * 16 + 8
-
-
-def fast_prob_bytes(t: int, gp: int) -> int:
-    """fast_prob_bytes: the FP8 probability region, at least the K tile."""
-    b = prob_row(t) * gp * 2
-    return 16 * K_ROW * 2 if b < 16 * K_ROW * 2 else b
 
 
 WIDE_LDS_BYTES = max(16 * V_ROW * 2, (WIDE_GROUP * 128 + WIDE_GROUP) * 4, 64 * WIDE_GROUP * 4)
@@ -93,8 +74,8 @@ def wide_ring(fp8: bool) -> int:
 
 
 def ring_of(D: int, G: int = 1, fp8: bool = False) -> int:
-    """decode_attention.hip ring_of (wide_ring for 16-head units): steps in flight."""
-    if G == WIDE_GROUP:
+    """decode_attention.hip ring_of (wide_ring for decode_wide_item units): steps in flight."""
+    if wide_item(fp8, G):
         return wide_ring(fp8)
     return 2 * RING if D == 64 else RING
 
@@ -233,24 +214,20 @@ def choose_partition(S, H, KV, D, bs, max_ctx, fp8) -> int:
     units = S * KV
     if use_fast_path(D, bs, S):
         gp = pow2ceil(H // KV)
-        wide = gp == WIDE_GROUP
-        top = FAST_MAX_PARTITION_FP8 if fp8 and not wide else FAST_MAX_PARTITION
-        min_items = FAST_MIN_ITEMS_FP8 if fp8 and not wide else FAST_MIN_ITEMS
-        ps = top
+        wide = wide_item(fp8, H // KV)
+        ps = FAST_MAX_PARTITION
         while ps >= 64:
             if ps <= bs:
                 return bs
-            if (ps * gp <= FAST_MAX_SCORES or wide) and units * _ceil(max_ctx, ps) >= min_items:
+            if (ps * gp <= FAST_MAX_SCORES or wide) and units * _ceil(max_ctx, ps) >= FAST_MIN_ITEMS:
                 return ps
             ps >>= 1
         return bs if bs > 64 else 64
     return 512 if units * _ceil(max_ctx, 512) >= 4096 else 256
 
 
-def fast_min_partition(ps: int, bs: int, fp8: bool) -> int:
-    """decode_attention.hip:1224-1230."""
-    if fp8:
-        return ps
+def fast_min_partition(ps: int, bs: int) -> int:
+    """decode_attention.hip fast_min_partition."""
     lo = max(ps // 4, 64)
     lo = max(lo, bs)
     return min(lo, ps)
@@ -312,7 +289,7 @@ def decode_host(S, H, KV, bs, max_bps, fp8, D=128) -> DecodeLaunch:
     L = DecodeLaunch(S, H, KV, bs, max_bps, fp8, split)
     max_ctx = bs * max_bps
     L.partition = choose_partition(S, H, KV, D, bs, max_ctx, fp8)
-    L.min_partition = fast_min_partition(L.partition, bs, fp8)
+    L.min_partition = fast_min_partition(L.partition, bs)
     L.max_parts = _ceil(max_ctx, L.min_partition)
     units = S * KV
     L.part_off = _ceil(K_COUNTER_BYTES + 16 + units * L.max_parts * 8, 256) * 256
@@ -329,10 +306,10 @@ def decode_host(S, H, KV, bs, max_bps, fp8, D=128) -> DecodeLaunch:
     gp = pow2ceil(G)
     t = L.partition + 16 * ring_of(D, G, fp8)
     mma_pv = D == 128 and MMA_PV_MIN_G <= G <= 8
-    if G == WIDE_GROUP:
+    if wide_item(fp8, G):
         L.lds_floats = WIDE_LDS_BYTES // 4
     else:
-        L.lds_floats = fast_score_floats(t, gp, fp8, mma_pv) + (fast_prob_bytes(t, gp) // 4 if fp8 else 0)
+        L.lds_floats = fast_score_floats(t, gp, mma_pv)
     return L
 
 
@@ -474,19 +451,20 @@ def decode(W: Writes, L: DecodeLaunch, out: Buf, ws: Buf, seq_lens: np.ndarray,
         pass   # such items return at once (decode_attention.hip:646)
     single = run & (nparts == 1)
     out_rows(single, "decode output rows")
-    # LDS of the item's passes: scores s_p[tl * GP + h]; FP8 pools: 2-byte
-    # probabilities s_pb[h * prow + tl] and pass 3's V tile / O exchange
+    # LDS of the item: decode_fast_item's scores s_p[tl * GP + h] (and for an
+    # MFMA pass 3 the in-place probabilities and the V tile); decode_wide_item's
+    # V tile, O hand-off, 1/l and merge weights
     ntok = np.minimum(ctx - part * ps, ps)   # ps: per item
     ring = ring_of(D, L.G, L.fp8)
     nsteps = _ceil(_ceil(np.maximum(ntok, 0), 16), ring) * ring
     if run.any():
         tpad = L.partition + 16 * ring
-        prow = prob_row(tpad)
-        if L.G == WIDE_GROUP:
-            # 16-head units (one pass): the V tile s_vt[row * V_ROW + col]
-            # (2 bytes), then from byte 0 the O hand-off s_o[h * D + d] and
-            # 1/l s_il[h] (4 bytes), then the merge weights s_w[lane * GP + h]
-            W.index([2 * (15 * V_ROW + 127) + 1, 4 * (L.G * D + L.G - 1) + 3, 4 * (63 * gp + L.G - 1) + 3],
+        if wide_item(L.fp8, L.G):
+            # one pass: the V tile s_vt[row * V_ROW + col] (2 bytes), then from
+            # byte 0 the O hand-off s_o[h * D + d] (all 16 MFMA columns) and
+            # 1/l s_il[n16] (4 bytes), then the merge weights s_w[lane * GP + h]
+            W.index([2 * (15 * V_ROW + 127) + 1, 4 * (WIDE_GROUP * D + WIDE_GROUP - 1) + 3,
+                     4 * (63 * gp + L.G - 1) + 3],
                     L.lds_floats * 4, "decode LDS V tile, O hand-off, 1/l, merge weights (bytes)")
             # the transposing reads: lane (g4, n16) at row 4*g4 + n16/4, col
             # nb*16 + 4*(n16%4) .. +3 (8 bytes)
@@ -496,20 +474,7 @@ def decode(W: Writes, L: DecodeLaunch, out: Buf, ws: Buf, seq_lens: np.ndarray,
                     "decode LDS transposing V reads (bytes)")
         else:
             W.index(nsteps[run] * 16 * gp - 1, L.partition * gp + 16 * ring * gp, "decode LDS scores")
-        if L.fp8 and L.G != WIDE_GROUP:
-            # FP8 pools: 2-byte probabilities s_pb[h * prow + tl] after the
-            # scores, pass 1's K tile in that region first; pass 3's V tile and
-            # the O exchange in the score region
-            pb0 = fast_score_floats(tpad, gp, True) * 4   # bytes
-            W.index(pb0 + 2 * ((L.G - 1) * prow + nsteps[run] * 16 - 1) + 1, L.lds_floats * 4,
-                    "decode LDS probabilities (bytes)")
-            W.index([pb0 + 2 * (15 * K_ROW + 127) + 1], L.lds_floats * 4,
-                    "decode LDS K tile in the probability region (bytes)")
-            W.index([2 * (15 * K_ROW + 127) + 1], fast_prob_bytes(tpad, gp),
-                    "decode K tile within the probability region (bytes)")
-            W.index([2 * (15 * V_ROW + 127) + 1, 4 * L.G * D - 1], pb0,
-                    "decode LDS V tile / O exchange in the score region (bytes)")
-        if not L.fp8 and D == 128 and MMA_PV_MIN_G <= L.G <= 8:
+        if not wide_item(L.fp8, L.G) and D == 128 and MMA_PV_MIN_G <= L.G <= 8:
             # MFMA pass 3 of 2-byte pools: probabilities in place as pairs
             # (word t * GP/2 + k), then the V tile / O exchange after them
             W.index(nsteps[run] * 16 * (gp // 2) - 1, tpad * (gp // 2), "decode in-place probabilities")

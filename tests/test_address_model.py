@@ -235,7 +235,7 @@ def test_group_sizes_above_8():
     (three units of 3), 48 / 4 (two units of 6), and groups of 5 and 8 (the
     2-byte pools' MFMA pass 3 with its in-place probabilities): the decode
     stores and LDS accesses stay inside their buffers, in both work-list forms
-    and both pool types."""
+    and both pool types (every FP8 group runs as a 16-column unit)."""
     W = A.Writes()
     rng = np.random.default_rng(16)
     assert A.kv_split_of(64, 4) == 1 and A.kv_split_of(128, 4) == 2 and A.kv_split_of(48, 4) == 2
@@ -246,34 +246,6 @@ def test_group_sizes_above_8():
             check_decode(W, 70, 400, rng.integers(0, 6400, 70), fp8, h=h, kv=kv)
             check_decode(W, 16, 576, [9216] * 16, fp8, h=h, kv=kv)
     W.check()
-
-
-def test_probability_rows_spread_over_the_banks():
-    """Pass 3's B operand reads 8 bytes per lane from the [GP][row] 2-byte
-    probabilities, lane (g4, n16) at row n16, column st*16 + 4*g4. For every
-    row length the kernel can use (partitions 64..2048 tokens plus 2..8 steps
-    of ring padding), each 32-lane half of the read covers 32 distinct 8-byte
-    slots of a 256-byte bank window (64 banks of 4 bytes), at every step. The
-    unpadded row (a multiple of 64 elements at ring 4) puts 8 rows on one
-    slot, which the check reports."""
-    def slots(row, st):
-        lane = np.arange(64)
-        g4, n16 = lane >> 4, lane & 15
-        byte = 2 * (n16 * row + st * 16 + 4 * g4)
-        assert (byte % 8 == 0).all()
-        return (byte % 256) // 8
-
-    def worst(row):
-        return max(np.bincount(slots(row, st)[h * 32:(h + 1) * 32], minlength=32).max()
-                   for st in range(8) for h in (0, 1))
-
-    for ps in (64, 128, 256, 512, 1024, 2048):
-        for ring in (2, 4, 8):
-            t = ps + 16 * ring
-            row = A.prob_row(t)
-            assert t <= row < t + 16 and row % 16 == 8
-            assert worst(row) == 1, (ps, ring, row)
-    assert worst(256 + 64) >= 8   # the unpadded row of a 256-token partition at ring 4
 
 
 def test_planted_mistakes_are_reported():
