@@ -484,7 +484,7 @@ def bench_decode_fp8(args, w) -> int:
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp8e4m3/bf16",
         "data": "synthetic (configuration 2's seeded pool quantised per kv head)",
-        "config": {"workload": "cfg2_qwen3_8b_decode_b64_fp8", "num_seqs": w.num_seqs,
+        "config": {"workload": f"{w.name}_fp8", "num_seqs": w.num_seqs,
                    "num_heads": w.num_heads, "num_kv_heads": kvh, "head_dim": w.head_dim,
                    "block_size": w.block_size, "context_tokens": ctx,
                    "step": "fp8 kv store (1 token/seq) + fp8 paged decode attention"},
