@@ -752,28 +752,20 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int64_t slo
   }
 }
 
-// Head-group sizes from which 2-byte pools (head dim 128) run pass 3 on the
-// matrix cores: below it the fp32 VALU products keep up with HBM.
-constexpr int kMmaPvMinG = 5;
-__host__ __device__ constexpr bool mma_pv_2byte(int d, int g) {
-  return d == 128 && g >= kMmaPvMinG && g <= 8;
-}
-// Groups of more than 8 heads in one unit (16 per unit, head dim 128:
-// decode_wide_item): S and P.V on the matrix cores, whose 16-wide tiles serve
-// 16 heads as cheaply as 8, and the kv head's K/V rows are read once instead
-// of once per 8-head sub-group.
-constexpr int kWideGroup = 16;
-// FP8 pools run every group as decode_wide_item units too (padded to 16 MFMA
+// decode_wide_item units (head dim 128): S and P.V on the matrix cores, whose
+// 16-wide tiles serve 16 heads as cheaply as 8. Groups of 16 heads (also each
+// 16 of a multiple of 16) read the kv head's K/V rows once instead of once
+// per 8-head sub-group. FP8 pools run every group this way (padded to 16
 // columns): its 16-byte loads cover whole rows, and at config 2 it beats the
 // LDS-staged two-pass form for every group size (48.0 against 51.0 us with 4
-// heads, 51.4 against 63.5 with 8).
-__host__ __device__ constexpr bool wide_item(bool fp8, int g) { return g == kWideGroup || fp8; }
-// Floats of the fast path's score region for t tokens (incl. ring padding):
-// 2-byte pools with an MFMA pass 3 keep their 2-byte probabilities in its
-// first half and the V tile after them.
-__host__ __device__ constexpr int fast_score_floats(int t, int gp, bool mma_pv = false) {
-  return mma_pv ? (t * gp < t * gp / 2 + 16 * kVRow / 2 ? t * gp / 2 + 16 * kVRow / 2 : t * gp)
-                : t * gp;
+// heads, 51.4 against 63.5 with 8). 2-byte pools from 5 heads on (88.0
+// against 91.8 us with 6 heads, 90.0 against 93.2 with 8, where the VALU
+// kernel ran pass 3 on the matrix cores); with up to 4 heads the VALU kernel
+// keeps up with HBM (84.3 against 85.4 us).
+constexpr int kWideGroup = 16;
+constexpr int kWideMinG2B = 5;
+__host__ __device__ constexpr bool wide_item(bool fp8, int g, int d) {
+  return d == 128 && (g == kWideGroup || fp8 || (g >= kWideMinG2B && g <= 8));
 }
 __host__ __device__ constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
@@ -868,12 +860,7 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
   constexpr int NTS = NH > LGP ? NH - LGP : 0;   // token bits split by stages
   constexpr int BS = 16 * SPB;
   constexpr int NBUF = ring_of(D);   // steps in flight per pass
-  static_assert(G <= 8, "group sizes of decode_fast_item (16-head units: decode_wide_item)");
-  // 5-8 heads (head dim 128): pass 3 on the matrix cores, with the
-  // probabilities rounded to TT in place (token-major pairs in the first half
-  // of the score region) and the V tile after them
-  constexpr bool kMmaPv = mma_pv_2byte(D, G);
-  const int tmax = a.partition + 16 * NBUF;   // tokens incl. ring padding
+  static_assert(G <= 8 && !wide_item(false, G, D), "group sizes of decode_fast_item (else decode_wide_item)");
   const int lane = threadIdx.x;
   const int r = lane / LPT, j = lane % LPT;
   const int s = unit / a.num_kv_heads;
@@ -1025,32 +1012,6 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
     l[h] = 0.f;
   }
   const int ntl = nsteps * 16;
-  if constexpr (kMmaPv) {
-  // probabilities rounded to TT, token-major pairs written in place: the word
-  // t * GP/2 + k holds heads 2k, 2k + 1 of token t. A word lands on the
-  // scores of token (t * GP/2 + k) / GP <= t/2, which every lane has read
-  // before (this iteration's reads precede its writes; the compiler barrier
-  // keeps them so). l sums the rounded values.
-  for (int t0 = 0; t0 < ntl; t0 += 64) {
-    const int t = t0 + lane;
-    uint32_t u[GP];
-#pragma unroll
-    for (int h = 0; h < GP; ++h) u[h] = 0u;
-    if (t < ntl) {
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        u[h] = TT::from_float(__builtin_amdgcn_exp2f(s_p[t * GP + h] - m[h]));
-        l[h] += TT::lo(u[h]);
-      }
-    }
-    asm volatile("" ::: "memory");
-    if (t < ntl) {
-#pragma unroll
-      for (int k = 0; k < GP / 2; ++k) s_p[t * (GP / 2) + k] = __uint_as_float(u[2 * k] | (u[2 * k + 1] << 16));
-    }
-    asm volatile("" ::: "memory");
-  }
-  } else {
   for (int t = lane; t < ntl; t += 64) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -1058,7 +1019,6 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
       s_p[t * GP + h] = p;
       l[h] += p;
     }
-  }
   }
 #pragma unroll
   for (int h = 0; h < G; ++h) l[h] = wave_sum_f(l[h]);
@@ -1071,14 +1031,6 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
   for (int h = 0; h < GA; ++h)
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[h][d] = 0.f;
-  constexpr int NOB = kMmaPv ? D / 16 : 1;   // 16-dim blocks of O^T (MFMA path)
-  // V tile of the MFMA pass 3: after the in-place probabilities, tmax * GP/2
-  // floats into the score region
-  uint16_t* s_vt = reinterpret_cast<uint16_t*>(s_p + tmax * (GP / 2));
-  const int g4 = lane >> 4, n16 = lane & 15;
-  f32x4 oacc[NOB];
-#pragma unroll
-  for (int nb = 0; nb < NOB; ++nb) oacc[nb] = f32x4{0, 0, 0, 0};
   auto pv_step = [&](const raw_t* vraw, int st) {
     u32x4 vbuf[NL];
 #pragma unroll
@@ -1088,28 +1040,6 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
       for (int i = 0; i < NL; ++i)
         if (st * 16 + i * TPL + r >= ntok) vbuf[i] = u32x4{0, 0, 0, 0};
     }
-  if constexpr (kMmaPv) {
-    // the step's 16 rows into LDS (row = token of the step, TT elements)
-#pragma unroll
-    for (int i = 0; i < NL; ++i)
-      *reinterpret_cast<u32x4*>(&s_vt[(i * TPL + r) * kVRow + j * 8]) = vbuf[i];
-    // B: probabilities of tokens st*16 + 4*g4 .. +3 for head n16 (0 past the group)
-    u32x2 pbv = u32x2{0, 0};
-    if (n16 < G) {
-      uint32_t w[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t pr = __float_as_uint(s_p[(st * 16 + 4 * g4 + e) * (GP / 2) + (n16 >> 1)]);
-        w[e] = (n16 & 1) ? (pr >> 16) : (pr & 0xffffu);
-      }
-      pbv = u32x2{w[0] | (w[1] << 16), w[2] | (w[3] << 16)};
-    }
-    // A: V^T[dim nb*16 + n16][tokens 4*g4 .. +3] by transposing reads (lane
-    // (g4, n16) addresses token 4*g4 + n16/4, dims nb*16 + 4*(n16%4) .. +3)
-    const uint16_t* vl = s_vt + (g4 * 4 + (n16 >> 2)) * kVRow + 4 * (n16 & 3);
-#pragma unroll
-    for (int nb = 0; nb < NOB; ++nb) oacc[nb] = Mfma16<TT>::mma(lds_read_tr(vl + nb * 16), pbv, oacc[nb]);
-  } else {
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int tl = st * 16 + i * TPL + r;
@@ -1135,7 +1065,6 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
         }
       }
     }
-  }
   };
   {
     auto round = [&](int st0) {
@@ -1150,27 +1079,6 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
 #pragma unroll
     for (int b = 0; b < NBUF; ++b) pv_step(vb[b], st0 + b);
   }
-  // the unit's O through LDS (MFMA pass 3): O^T blocks (lane (g4, n16): dims
-  // nb*16 + 4*g4 .. +3 of head n16) -> s_o[h][D], read back below per (head,
-  // 8-dim chunk). The staged V tile is no longer read (the last MFMAs, which
-  // consume it, feed these stores); the region holds G x D floats
-  // (fast_score_floats)
-  float* s_o = reinterpret_cast<float*>(s_vt);
-  if constexpr (kMmaPv) {
-    if (n16 < G) {
-#pragma unroll
-      for (int nb = 0; nb < NOB; ++nb) *reinterpret_cast<f32x4*>(&s_o[n16 * D + nb * 16 + 4 * g4]) = oacc[nb];
-    }
-  }
-  if constexpr (kMmaPv) {
-#pragma unroll
-    for (int h = 0; h < GA; ++h) {
-      const f32x4 lo = *reinterpret_cast<const f32x4*>(&s_o[h * D + j * 8]);
-      const f32x4 hi = *reinterpret_cast<const f32x4*>(&s_o[h * D + j * 8 + 4]);
-      acc[h][0] = lo.x; acc[h][1] = lo.y; acc[h][2] = lo.z; acc[h][3] = lo.w;
-      acc[h][4] = hi.x; acc[h][5] = hi.y; acc[h][6] = hi.z; acc[h][7] = hi.w;
-    }
-  } else {
   // sum over the TPL rows of the wave (lanes equal in j): lane ^ 8 by DPP
   // (D 64), then the gfx950 row swaps: v_permlane16_swap / v_permlane32_swap
   // with both operands x hand every lane {x, x of lane ^ 16} (^ 32) in some
@@ -1190,7 +1098,6 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
                                                         false, false);
       acc[h][d] = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
     }
-  }
 
   if (nparts == 1) {
     if (lane < LPT) {
@@ -1496,7 +1403,7 @@ template <class TT, int D, int G, int SPB, bool kF8>
 // at most 256; they take 149 (2-byte) and 163 (FP8), three waves per SIMD
 // (four, at 128, ran 5% slower).
 __global__ __launch_bounds__(64)
-__attribute__((amdgpu_waves_per_eu(wide_item(kF8, G) ? 2 : (D == 128 && G >= 5 && G <= 8 ? 3 : 1))))
+__attribute__((amdgpu_waves_per_eu(wide_item(kF8, G, D) ? 2 : 1)))
 void decode_fast_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) float s_dyn[];
   int unit, part, ps = a.partition;
@@ -1603,7 +1510,7 @@ void decode_fast_kernel(DecodeArgs a) {
     unit = it.x;
     part = it.y;
   }
-  if constexpr (wide_item(kF8, G))
+  if constexpr (wide_item(kF8, G, D))
     decode_wide_item<TT, G, SPB, kF8>(a, unit, part, ps, s_dyn);
   else
     decode_fast_item<TT, D, G, SPB>(a, unit, part, ps, s_dyn);
@@ -1728,7 +1635,7 @@ int choose_partition(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads, 
     if (NPD_DECODE_PARTITION >= block_size) return NPD_DECODE_PARTITION;
 #endif
     const int gp = pow2ceil((int)(num_heads / num_kv_heads));
-    const bool wide = wide_item(fp8, (int)(num_heads / num_kv_heads));
+    const bool wide = wide_item(fp8, (int)(num_heads / num_kv_heads), (int)head_dim);
     for (int ps = kFastMaxPartition; ps >= 64; ps >>= 1) {
       if (ps <= block_size) return (int)block_size;
       if (ps * gp > kFastMaxScores && !wide) continue;
@@ -1773,9 +1680,9 @@ int64_t fast_grid(const DecodeArgs& a, int64_t units) {
 // fast_score_floats), or kWideLdsBytes for decode_wide_item units, for any
 // partition.
 int64_t fast_lds_bytes(int partition, int g, bool fp8, int d) {
-  if (wide_item(fp8, g)) return kWideLdsBytes;
+  if (wide_item(fp8, g, d)) return kWideLdsBytes;
   const int t = partition + 16 * ring_of(d);
-  return (int64_t)fast_score_floats(t, pow2ceil(g), mma_pv_2byte(d, g)) * 4;
+  return (int64_t)t * pow2ceil(g) * 4;
 }
 
 template <class TT, int D, int G, int SPB, bool kF8 = false>

@@ -45,21 +45,14 @@ RING = 2
 V_ROW = 128 + 16   # elements per row of the MFMA P.V steps' V tile in LDS (kVRow)
 
 
-MMA_PV_MIN_G = 5   # kMmaPvMinG: 2-byte pools at head dim 128 from this group size
 WIDE_GROUP = 16    # kWideGroup: heads of a decode_wide_item unit
+WIDE_MIN_G_2B = 5  # kWideMinG2B: 2-byte groups of 5-8 heads run as decode_wide_item units
 
 
-def wide_item(fp8: bool, g: int) -> bool:
-    """wide_item: 16-head units of 2-byte pools and every group of an FP8 pool."""
-    return g == WIDE_GROUP or fp8
-
-
-def fast_score_floats(t: int, gp: int, mma_pv: bool = False) -> int:
-    """fast_score_floats: the score region; for a 2-byte MFMA pass 3 at least
-    the in-place probabilities plus the V tile."""
-    if mma_pv:
-        return max(t * gp, t * gp // 2 + 16 * V_ROW // 2)
-    return t * gp
+def wide_item(fp8: bool, g: int, d: int = 128) -> bool:
+    """wide_item: at head dim 128, 16-head units, every FP8 group, and 2-byte
+    groups of 5-8 heads."""
+    return d == 128 and (g == WIDE_GROUP or fp8 or WIDE_MIN_G_2B <= g <= 8)
 
 
 WIDE_LDS_BYTES = max(16 * V_ROW * 2, (WIDE_GROUP * 128 + WIDE_GROUP) * 4, 64 * WIDE_GROUP * 4)
@@ -75,7 +68,7 @@ def wide_ring(fp8: bool) -> int:
 
 def ring_of(D: int, G: int = 1, fp8: bool = False) -> int:
     """decode_attention.hip ring_of (wide_ring for decode_wide_item units): steps in flight."""
-    if wide_item(fp8, G):
+    if wide_item(fp8, G, D):
         return wide_ring(fp8)
     return 2 * RING if D == 64 else RING
 
@@ -214,7 +207,7 @@ def choose_partition(S, H, KV, D, bs, max_ctx, fp8) -> int:
     units = S * KV
     if use_fast_path(D, bs, S):
         gp = pow2ceil(H // KV)
-        wide = wide_item(fp8, H // KV)
+        wide = wide_item(fp8, H // KV, D)
         ps = FAST_MAX_PARTITION
         while ps >= 64:
             if ps <= bs:
@@ -305,11 +298,10 @@ def decode_host(S, H, KV, bs, max_bps, fp8, D=128) -> DecodeLaunch:
     L.grid = n
     gp = pow2ceil(G)
     t = L.partition + 16 * ring_of(D, G, fp8)
-    mma_pv = D == 128 and MMA_PV_MIN_G <= G <= 8
-    if wide_item(fp8, G):
+    if wide_item(fp8, G, D):
         L.lds_floats = WIDE_LDS_BYTES // 4
     else:
-        L.lds_floats = fast_score_floats(t, gp, mma_pv)
+        L.lds_floats = t * gp
     return L
 
 
@@ -451,15 +443,14 @@ def decode(W: Writes, L: DecodeLaunch, out: Buf, ws: Buf, seq_lens: np.ndarray,
         pass   # such items return at once (decode_attention.hip:646)
     single = run & (nparts == 1)
     out_rows(single, "decode output rows")
-    # LDS of the item: decode_fast_item's scores s_p[tl * GP + h] (and for an
-    # MFMA pass 3 the in-place probabilities and the V tile); decode_wide_item's
-    # V tile, O hand-off, 1/l and merge weights
+    # LDS of the item: decode_fast_item's scores s_p[tl * GP + h];
+    # decode_wide_item's V tile, O hand-off, 1/l and merge weights
     ntok = np.minimum(ctx - part * ps, ps)   # ps: per item
     ring = ring_of(D, L.G, L.fp8)
     nsteps = _ceil(_ceil(np.maximum(ntok, 0), 16), ring) * ring
     if run.any():
         tpad = L.partition + 16 * ring
-        if wide_item(L.fp8, L.G):
+        if wide_item(L.fp8, L.G, D):
             # one pass: the V tile s_vt[row * V_ROW + col] (2 bytes), then from
             # byte 0 the O hand-off s_o[h * D + d] (all 16 MFMA columns) and
             # 1/l s_il[n16] (4 bytes), then the merge weights s_w[lane * GP + h]
@@ -474,13 +465,6 @@ def decode(W: Writes, L: DecodeLaunch, out: Buf, ws: Buf, seq_lens: np.ndarray,
                     "decode LDS transposing V reads (bytes)")
         else:
             W.index(nsteps[run] * 16 * gp - 1, L.partition * gp + 16 * ring * gp, "decode LDS scores")
-        if not wide_item(L.fp8, L.G) and D == 128 and MMA_PV_MIN_G <= L.G <= 8:
-            # MFMA pass 3 of 2-byte pools: probabilities in place as pairs
-            # (word t * GP/2 + k), then the V tile / O exchange after them
-            W.index(nsteps[run] * 16 * (gp // 2) - 1, tpad * (gp // 2), "decode in-place probabilities")
-            v0 = tpad * (gp // 2) * 4   # bytes
-            W.index([v0 + 2 * (15 * V_ROW + 127) + 1, v0 + 4 * L.G * D - 1], L.lds_floats * 4,
-                    "decode LDS V tile / O exchange after the probabilities (bytes)")
         nb = _ceil(ntok[run], L.bs)
         W.index(nb - 1, 128, "decode block ids per lane")
         # block-table reads of the partition

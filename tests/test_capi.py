@@ -167,11 +167,14 @@ def test_workspace_size():
         return (2**20 + 16 + units * P * 8 + 255) // 256 * 256 + S * H * (P + groups) * 130 * 4
     ws = lib.npd_paged_attention_workspace_size
     # 2-byte pools (block size 64 here, a size the FP8 entry point does not
-    # take): the host partition is the longest of 2048 .. 64 tokens (at most
-    # 4096 / G tokens for G query heads per kv head, G rounded up to a power of
-    # two) that gives >= 1280 work items at the longest context. The kernel
-    # may halve it for shorter actual contexts, down to a quarter (and not
-    # below 64 tokens or the block): the partials are sized for that one.
+    # take): the host partition is the longest of 2048 .. 64 tokens that gives
+    # >= 1280 work items at the longest context, and for the two-pass kernel
+    # (head dim 128 with up to 4 query heads per kv head, head dims 64 / 256)
+    # at most 4096 / G tokens for G query heads per kv head, G rounded up to a
+    # power of two; the one-pass units (head dim 128 from 5 heads on, every
+    # FP8 group) keep no scores and have no such cap. The kernel may halve it
+    # for shorter actual contexts, down to a quarter (and not below 64 tokens
+    # or the block): the partials are sized for that one.
     # 1024 seqs x 8 kv heads x 256 tokens: one partition each
     assert ws(1024, 32, 8, 128, 64, 4) == fast(1024, 32, 8, 1)
     # 64 seqs x 8 kv heads x 256 tokens: 512 units -> the block (64), 4 each
@@ -180,9 +183,9 @@ def test_workspace_size():
     # 2048 -> 1024, slots for 256-token partitions (128)
     assert ws(8, 32, 8, 128, 64, 512) == fast(8, 32, 8, 128)
     # 10 seqs x 8 kv heads x 32832 tokens: G = 4 caps the partition at 1024
-    # (slots for 256: 129), G = 8 at 512 (128: 257); G = 2 takes 2048 (512: 65)
+    # (slots for 256: 129); G = 8 (a one-pass unit) and G = 2 take 2048 (512: 65)
     assert ws(10, 32, 8, 128, 64, 513) == fast(10, 32, 8, 129)
-    assert ws(10, 64, 8, 128, 64, 513) == fast(10, 64, 8, 257)
+    assert ws(10, 64, 8, 128, 64, 513) == fast(10, 64, 8, 65)
     assert ws(10, 16, 8, 128, 64, 513) == fast(10, 16, 8, 65)
     # 1 seq x 8 kv heads x 4k tokens: too few items at any length -> the block
     assert ws(1, 32, 8, 128, 64, 64) == fast(1, 32, 8, 64)
@@ -192,8 +195,8 @@ def test_workspace_size():
     assert ws(4096, 32, 8, 128, 64, 2048) == fast(4096, 32, 8, 512) - 4096 * 32 * 32 * 130 * 4
     assert ws(512, 32, 8, 128, 64, 2048) == fast(512, 32, 8, 512)
     # Blocks of 16 or 32 (which the FP8 entry point takes): the workspace also
-    # covers the FP8 rule (>= 4096 items, at most 256 tokens, not halved);
-    # here both give 128 slots of 256 tokens
+    # covers an FP8 pool's partition (one-pass units: no score cap); here both
+    # give 128 slots of 256 tokens
     assert ws(8, 32, 8, 128, 16, 2048) == fast(8, 32, 8, 128)
     assert ws(8, 32, 8, 128, 32, 1024) == fast(8, 32, 8, 128)
     # 1024 seqs x 256 tokens: both rules give one partition
