@@ -430,10 +430,11 @@ def bench_copy(args, dev) -> int:
 
 
 def bench_decode_fp8(args, w) -> int:
-    """Configuration 2 over an FP8 (e4m3) pool: the same sequences, tables and
-    queries, the bf16 pool's values quantised with per-kv-head scales
-    (amax / 448). One step = the fp8 store of one new token per sequence + fp8
-    decode attention. Algorithmic bytes count 1 byte per K/V element."""
+    """Configuration 2 (or 4: `--workload long-fp8`) over an FP8 (e4m3) pool:
+    the same sequences, tables and queries, the bf16 pool's values quantised
+    with per-kv-head scales (amax / 448). One step = the fp8 store of one new
+    token per sequence + fp8 decode attention. Algorithmic bytes count 1 byte
+    per K/V element of each distinct pool row."""
     from nanopd_amd import paged_kernels as pk
     dev = w.k_cache.device
     kvh = w.num_kv_heads
@@ -473,8 +474,10 @@ def bench_decode_fp8(args, w) -> int:
     attn_ms = _launch_avg_ms(attend, args.steps)
     elt = 2
     ctx = sum(w.seq_lens_list)
-    attn_bytes = (ctx * kvh * w.head_dim * 2 + 2 * w.num_seqs * w.num_heads * w.head_dim * elt
-                  + w.num_seqs * w.max_blocks_per_seq * 4 + w.num_seqs * 4)
+    # K/V rows at 1 byte per element, each distinct pool row once (a block
+    # that a fork shares with its parent counts once), plus the bf16 q and out
+    # rows, tables and seq_lens
+    attn_bytes = w.unique_kv_bytes() // elt + w._qo_meta_bytes()
     t = len(pos)
     store_bytes = 2 * t * kvh * w.head_dim * (elt + 1) + 4 * t
     achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
@@ -483,7 +486,7 @@ def bench_decode_fp8(args, w) -> int:
         "value": round((attn_bytes + store_bytes) / (ms * 1e-3) / 1e9, 1), "unit": "GB/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp8e4m3/bf16",
-        "data": "synthetic (configuration 2's seeded pool quantised per kv head)",
+        "data": f"synthetic ({w.name}'s seeded pool quantised per kv head)",
         "config": {"workload": f"{w.name}_fp8", "num_seqs": w.num_seqs,
                    "num_heads": w.num_heads, "num_kv_heads": kvh, "head_dim": w.head_dim,
                    "block_size": w.block_size, "context_tokens": ctx,
@@ -661,14 +664,16 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=["decode", "decode-fp8", "long", "prefill", "store",
-                                           "copy", "e2e", "transfer"],
+    ap.add_argument("--workload", choices=["decode", "decode-fp8", "long", "long-fp8", "prefill",
+                                           "store", "copy", "e2e", "transfer"],
                     default="decode",
                     help="decode: config 2 (default); long: config 4 (8 seqs, 8k-32k); "
                          "prefill: config 3 (4 chunks of 512 on paged prefixes + 48 decodes); "
                          "store: config 3's KV store (2096 tokens into the pool by slot); "
                          "e2e: config 5 (Qwen3-8B collocated serving, tok/s); "
                          "decode-fp8: config 2 over an FP8 (e4m3) pool; "
+                         "long-fp8: config 4 over an FP8 pool (its forks' shared "
+                         "partitions read once); "
                          "transfer: KV transfer pack + unpack of a 4096-token Qwen3-8B sequence; "
                          "copy: a plain 256 MiB device copy, the calibration kernel for "
                          "the FETCH_SIZE / WRITE_SIZE counters")
@@ -713,6 +718,8 @@ def main() -> int:
         pk.paged_kv_store(w.k_cache, w.v_cache, w.store_k, w.store_v, w.store_tables,
                           w.store_positions)
         pk.copy_blocks(w.k_cache, w.v_cache, w.cow_pairs)
+        if args.workload == "long-fp8":
+            return bench_decode_fp8(args, w)
     res = bench_decode(args, w)
     line = {
         "metric": "Decode paged-attn achieved HBM GB/s (% peak); collocated tok/s, Qwen3-8B",

@@ -1210,61 +1210,12 @@ __device__ __forceinline__ void decode_wide_item(const DecodeArgs& a, int unit, 
   // (clamped; at most 128 blocks: kFastMaxPartition / 16)
   static_assert(kFastMaxPartition / 16 <= 128, "two block ids per lane");
   int myblk0 = 0, myblk1 = 0;
-  const int nb = (ntok + BS - 1) / BS;
-  auto clamp_blk = [&](int b) { return b < 0 ? 0 : (b >= a.num_blocks ? a.num_blocks - 1 : b); };
   {
+    const int nb = (ntok + BS - 1) / BS;
     const int32_t* row = a.block_tables + (int64_t)s * a.max_bps + b0;
+    auto clamp_blk = [&](int b) { return b < 0 ? 0 : (b >= a.num_blocks ? a.num_blocks - 1 : b); };
     if (lane < nb) myblk0 = clamp_blk(row[lane]);
     if (lane + 64 < nb) myblk1 = clamp_blk(row[lane + 64]);
-  }
-  // Shared partitions (copy-on-write forks, common prefixes): sequences whose
-  // tables hold the same blocks over this partition, with as many tokens in
-  // it, read the same K/V rows. With at most 64 sequences the item finds its
-  // set: lane i compares sequence i's token count and first block id of the
-  // partition, then every block id of each candidate. The set's lowest
-  // sequence serves the first kMaxMembers of them, G MFMA columns each, and
-  // publishes each one's partial (or output) into that sequence's own merge;
-  // the others of those kMaxMembers exit. Members past kMaxMembers run alone.
-  // mseq[k]: the k-th member's sequence (wave-uniform), nmem members.
-  constexpr int kMaxMembers = kWideGroup / G;
-  int mseq[kMaxMembers];
-  mseq[0] = s;
-#pragma unroll
-  for (int k = 1; k < kMaxMembers; ++k) mseq[k] = -1;
-  int nmem = 1;
-  if constexpr (kMaxMembers >= 2) {
-    if (a.num_seqs <= kInlineSchedMax) {
-      const int first = __builtin_amdgcn_readfirstlane(myblk0);   // lane 0: block b0
-      bool cand = false;
-      if (lane < a.num_seqs && lane != s) {
-        int ci = a.seq_lens[lane];
-        ci = ci < cap ? ci : cap;
-        const int ti = ci - t0 < ps ? ci - t0 : ps;
-        cand = ti == ntok && clamp_blk(a.block_tables[(int64_t)lane * a.max_bps + b0]) == first;
-      }
-      uint64_t set = 1ull << s;
-      for (uint64_t cm = __ballot(cand); cm != 0; cm &= cm - 1) {
-        const int i = __builtin_ctzll(cm);
-        const int32_t* rowi = a.block_tables + (int64_t)i * a.max_bps + b0;
-        bool diff = false;
-        if (lane < nb) diff = clamp_blk(rowi[lane]) != myblk0;
-        if (lane + 64 < nb) diff = diff || clamp_blk(rowi[lane + 64]) != myblk1;
-        if (__ballot(diff) == 0) set |= 1ull << i;
-      }
-      const int rank = __popcll(set & ((1ull << s) - 1));
-      if (rank != 0 && rank < kMaxMembers) return;   // the set's lowest sequence serves it
-      if (rank == 0) {
-        uint64_t rest = set & (set - 1);   // the set without s (its lowest)
-#pragma unroll
-        for (int k = 1; k < kMaxMembers; ++k) {
-          if (rest != 0) {
-            mseq[k] = __builtin_ctzll(rest);
-            rest &= rest - 1;
-            ++nmem;
-          }
-        }
-      }
-    }
   }
   const int pkh = kh / a.kv_split;   // the unit's kv head in the pool
   const float score_scale = kF8 ? a.scale_log2 * a.k_scale[pkh] : a.scale_log2;
@@ -1302,24 +1253,17 @@ __device__ __forceinline__ void decode_wide_item(const DecodeArgs& a, int unit, 
 #pragma unroll
     for (int i = 0; i < NVL; ++i) buf[i] = ld_kv(static_cast<const u32x4*>(a.v_cache) + b + i * 64);
   };
-  // Q^T as the B operand of S MFMA c: lane (g4, n16) = column n16, head
-  // n16 % G of member n16 / G, the dims of the K operand (2-byte pools:
-  // 32c + 8*g4 .. +7; FP8: 64(c/2) + 16*g4 + 8(c%2) .. +7); zeros past the
-  // members' columns
-  const int qk = n16 / G, qh = n16 - qk * G;
-  int qseq = -1;
-#pragma unroll
-  for (int k = 0; k < kMaxMembers; ++k)
-    if (qk == k && k < nmem) qseq = mseq[k];
+  // Q^T as the B operand of S MFMA c: lane (g4, n16) = head n16, the dims of
+  // the K operand (2-byte pools: 32c + 8*g4 .. +7; FP8: 64(c/2) + 16*g4 +
+  // 8(c%2) .. +7)
   u32x4 qb[NKC];
   {
-    const uint16_t* qrow = a.q + (int64_t)(qseq < 0 ? 0 : qseq) * a.q_stride_seq +
-                           (kh * G + qh) * a.q_stride_head;
+    const uint16_t* qrow = a.q + s * a.q_stride_seq + (kh * G + n16) * a.q_stride_head;
 #pragma unroll
-    for (int c = 0; c < NKC; ++c)
-      qb[c] = qseq >= 0 ? *reinterpret_cast<const u32x4*>(
-                              qrow + (kF8 ? 64 * (c / 2) + 16 * g4 + 8 * (c % 2) : 32 * c + 8 * g4))
-                        : u32x4{0, 0, 0, 0};
+    for (int c = 0; c < NKC; ++c)   // zeros past the group
+      qb[c] = n16 < G ? *reinterpret_cast<const u32x4*>(
+                            qrow + (kF8 ? 64 * (c / 2) + 16 * g4 + 8 * (c % 2) : 32 * c + 8 * g4))
+                      : u32x4{0, 0, 0, 0};
   }
   uint16_t* s_vt = reinterpret_cast<uint16_t*>(s_lds);
   // A of the P.V MFMA: V^T[dim nb*16 + n16][tokens 4*g4 .. +3] by transposing
@@ -1415,68 +1359,35 @@ __device__ __forceinline__ void decode_wide_item(const DecodeArgs& a, int unit, 
   }
   const float lsum = row_sum4(lp);   // head n16's l (every row)
 
-  // O^T blocks (lane (g4, n16): dims nb*16 + 4*g4 .. +3 of column n16) ->
-  // s_o[column][D] and 1/l -> s_il[column], read back per (column, 8-dim
-  // chunk). The V tile is no longer read: the last MFMAs, which consume it,
-  // feed these stores.
+  // O^T blocks (lane (g4, n16): dims nb*16 + 4*g4 .. +3 of head n16) ->
+  // s_o[h][D] and 1/l -> s_il[h], read back per (head, 8-dim chunk). The V
+  // tile is no longer read: the last MFMAs, which consume it, feed these
+  // stores.
   float* s_o = s_lds;
-  float* s_il = s_lds + kWideGroup * D;
+  float* s_il = s_lds + kWideGroup * D;   // past all 16 columns' rows
 #pragma unroll
   for (int nb = 0; nb < NOB; ++nb) *reinterpret_cast<f32x4*>(&s_o[n16 * D + nb * 16 + 4 * g4]) = oacc[nb];
   if (g4 == 0) s_il[n16] = out_scale / lsum;
-  // each member's partitions and slot for this partition (-1: a single
-  // partition, whose output is written directly)
-  int np_m[kMaxMembers];
-  int64_t base_m[kMaxMembers];
+  const int64_t base = nparts == 1 ? -1 : partial_slot(a, unit, part, nparts);
+  // row r of the wave (TPL rows of LPT lanes) writes heads r, r + TPL, ...
 #pragma unroll
-  for (int k = 0; k < kMaxMembers; ++k) {
-    np_m[k] = 0;
-    base_m[k] = -1;
-    if (k < nmem) {
-      int ck = a.seq_lens[mseq[k]];
-      ck = ck < cap ? ck : cap;
-      np_m[k] = (ck + ps - 1) / ps;
-      base_m[k] = np_m[k] == 1 ? -1 : partial_slot(a, mseq[k] * a.num_kv_heads + kh, part, np_m[k]);
-    }
-  }
-  // row r of the wave (TPL rows of LPT lanes) writes columns r, r + TPL, ...
-#pragma unroll
-  for (int c = 0; c < kWideGroup; ++c) {
-    const int k = c / G, h = c - k * G;
-    if (k >= nmem || (c % TPL) != r) continue;
-    const f32x4 lo = *reinterpret_cast<const f32x4*>(&s_o[c * D + j * 8]);
-    const f32x4 hi = *reinterpret_cast<const f32x4*>(&s_o[c * D + j * 8 + 4]);
+  for (int h = 0; h < G; ++h) {
+    if ((h % TPL) != r) continue;
+    const f32x4 lo = *reinterpret_cast<const f32x4*>(&s_o[h * D + j * 8]);
+    const f32x4 hi = *reinterpret_cast<const f32x4*>(&s_o[h * D + j * 8 + 4]);
     const float o[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-    if (base_m[k] < 0) {
-      store_row8<TT>(a.out + mseq[k] * a.out_stride_seq + (kh * G + h) * a.out_stride_head + j * 8, o,
-                     s_il[c]);
+    if (base < 0) {
+      store_row8<TT>(a.out + s * a.out_stride_seq + (kh * G + h) * a.out_stride_head + j * 8, o,
+                     s_il[h]);
     } else {
-      float* dst = a.part_acc + (base_m[k] * G + h) * D + j * 2;
+      float* dst = a.part_acc + (base * G + h) * D + j * 2;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) st_coherent2(dst + q * (2 * LPT), o[2 * q], o[2 * q + 1]);
+      for (int k = 0; k < 4; ++k) st_coherent2(dst + k * (2 * LPT), o[2 * k], o[2 * k + 1]);
     }
   }
-  if (g4 == 0 && qseq >= 0) {   // (m, l) of column n16
-    int64_t bk = -1;
-#pragma unroll
-    for (int k = 0; k < kMaxMembers; ++k)
-      if (qk == k) bk = base_m[k];
-    if (bk >= 0) st_coherent2(a.part_ml + (bk * G + qh) * 2, mref, lsum);
-  }
-  // the members' merges, one call site (its code and registers once)
-#pragma unroll 1
-  for (int k = 0; k < nmem; ++k) {
-    int sk = s, npk = 0;
-    int64_t bk = -1;
-#pragma unroll
-    for (int kk = 0; kk < kMaxMembers; ++kk)
-      if (kk == k) {
-        sk = mseq[kk];
-        npk = np_m[kk];
-        bk = base_m[kk];
-      }
-    if (bk >= 0) merge_tail<TT, D, G>(a, sk * a.num_kv_heads + kh, part, npk, sk, kh, lane, s_lds, out_scale);
-  }
+  if (base < 0) return;
+  if (g4 == 0 && n16 < G) st_coherent2(a.part_ml + (base * G + n16) * 2, mref, lsum);
+  merge_tail<TT, D, G>(a, unit, part, nparts, s, kh, lane, s_lds, out_scale);
 }
 
 

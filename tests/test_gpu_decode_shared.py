@@ -1,22 +1,20 @@
 """Decode over sequences whose tables share blocks: copy-on-write forks,
 forks that grew past the fork point, and identical tables.
 
-At head dim 128 the one-pass decode units (2-byte groups of 5-8 query heads,
-every FP8 group) serve a partition that several sequences' tables hold alike
-(the same block ids, as many tokens in it) in one work item. The first of the
-set fills the MFMA columns with up to 16 / G of those sequences' query heads,
-reads the rows once, and publishes each sequence's partial into that
-sequence's own merge. Groups the two-pass kernel runs (2-byte, up to 4 heads)
-share nothing and must agree all the same.
+Each sequence's items read their own table, so a block two tables hold is read
+by both (at config 4 the second reads mostly come from L2: over the FP8 pool,
+whose loads are not nontemporal, the fetch counters read the distinct bytes).
+A form in which the first sequence of such a set served the others' query
+heads in its idle MFMA columns was built, passed these tests and was dropped:
+it read each row once but left fewer waves streaming (config 4 over the FP8
+pool: 81.1 against 73.4 us in the trace, the same bytes fetched).
 
-Checks:
+Checks, for the one-pass units (head dim 128: 2-byte groups of 5-8 heads,
+every FP8 group) and the two-pass kernel (2-byte, 4 heads):
 - every row against the float64 oracle, at the decode tests' tolerance;
-- bit-equality with the same batch over unshared tables: every block of the
-  forks copied to a block of its own, so that no partition is shared (a
-  column's arithmetic does not depend on which sequence leads the set, nor on
-  the column it takes);
-- sets larger than the 16 columns hold (5 identical tables at 4 heads: 4
-  share an item, the 5th runs alone; at 8 heads pairs).
+- bit-equality with the same batch over unshared tables (every block of the
+  forks copied to a block of its own);
+- bit-equality when the sequences come in reverse order.
 
 Reference: the fork and the copy-on-write of the last block,
 nanoPD/block_manager/block_manager.py:100-105 and :72-98."""
@@ -116,8 +114,7 @@ def run(device, q, kc, vc, bt, sl, mb, bs, fp8, ks=None, vs=None):
 @pytest.mark.parametrize("H,dtype,bs", [(48, torch.bfloat16, 16), (64, torch.bfloat16, 32),
                                         (40, torch.float16, 16), (32, torch.bfloat16, 16)])
 def test_shared_blocks_2byte(device, H, dtype, bs):
-    """G 6 / 8 / 5 (one-pass units, sets of up to 2 or 3 sequences) and G 4
-    (the two-pass kernel, no sharing), 8 kv heads."""
+    """G 6 / 8 / 5 (one-pass units) and G 4 (the two-pass kernel), 8 kv heads."""
     print(f"shared blocks: H={H} G={H // 8} {dtype} bs={bs}", flush=True)
     kc, vc, bt, ubt, sl, mb = build(bs, False, seed=H + bs)
     kc, vc = kc.to(dtype).to(device), vc.to(dtype).to(device)
@@ -134,7 +131,7 @@ def test_shared_blocks_2byte(device, H, dtype, bs):
 
 @pytest.mark.parametrize("G,bs", [(1, 16), (4, 16), (4, 32), (8, 16), (16, 16)])
 def test_shared_blocks_fp8(device, G, bs):
-    """FP8 pools: G 1 (sets of up to 16 sequences), 4 (4), 8 (2), 16 (none)."""
+    """FP8 pools, G 1 / 4 / 8 / 16."""
     print(f"shared blocks fp8: G={G} bs={bs}", flush=True)
     kc, vc, bt, ubt, sl, mb = build(bs, True, seed=100 + G + bs)
     g = torch.Generator().manual_seed(G)
@@ -154,8 +151,8 @@ def test_shared_blocks_fp8(device, G, bs):
 
 
 def test_leader_order_does_not_matter(device):
-    """The same batch with its sequences in reverse order (another sequence
-    leads each set): every row bit-equal (FP8, G 4, and bf16, G 8)."""
+    """The same batch with its sequences in reverse order: every row bit-equal
+    (FP8, G 4, and bf16, G 8)."""
     for fp8, H in ((True, 32), (False, 64)):
         kc, vc, bt, _, sl, mb = build(16, fp8, seed=7)
         g = torch.Generator().manual_seed(3)
