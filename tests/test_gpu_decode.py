@@ -242,6 +242,34 @@ def test_group_of_16_scheduled_path(device):
     check(run(*args, 16), q, kc, vc, bt, sl, scale)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("G", [5, 8])
+@pytest.mark.parametrize("bs", [64, 128, 256])
+def test_one_pass_units_large_blocks(device, dtype, G, bs):
+    """Head dim 128 with 5-8 heads per group runs as one-pass matrix-core
+    units at every fast-path block size (a 16-token step inside a block of up
+    to 256 tokens): contexts inside one block, across blocks and partitions,
+    and rows past the context holding NaN."""
+    lens = [1, 300, 1100, 5000, 17]
+    q, kc, vc, bt, sl, scale, mb = make_inputs(len(lens), G * 2, 2, 128, lens, bs, dtype, device,
+                                               seed=G * bs)
+    for i, n in enumerate(lens):
+        if n % bs:
+            b = int(bt[i, (n - 1) // bs])
+            kc[b, :, n % bs:, :] = float("nan")
+            vc[b, :, n % bs:, :] = float("nan")
+    check(run(q, kc, vc, bt, sl, scale, mb, bs), q, kc, vc, bt, sl, scale)
+
+
+@pytest.mark.parametrize("lens", [[1025], [2049], [100, 1025, 3000, 5000, 17]])
+def test_two_level_merge_one_pass_units(device, lens):
+    """The two-level merge of the one-pass units (8 heads per group): 64- and
+    128-token partitions, groups of 16 with a last group of one."""
+    args = make_inputs(len(lens), 64, 8, 128, lens, 16, torch.bfloat16, device, seed=sum(lens) + 1)
+    q, kc, vc, bt, sl, scale, mb = args
+    check(run(*args, 16), q, kc, vc, bt, sl, scale)
+
+
 @pytest.mark.parametrize("lens", [[1024], [1025], [2048], [2049], [100, 1025, 3000, 5000, 17]])
 def test_two_level_merge_group_boundaries(device, lens):
     """A (sequence, kv-head) with more than 16 partitions merges in two
