@@ -765,7 +765,7 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int64_t slo
 constexpr int kWideGroup = 16;
 constexpr int kWideMinG2B = 5;
 __host__ __device__ constexpr bool wide_item(bool fp8, int g, int d) {
-  return d == 128 && (g == kWideGroup || fp8 || (g >= kWideMinG2B && g <= 8));
+  return d == 128 && g <= kWideGroup && (fp8 || g >= kWideMinG2B);
 }
 __host__ __device__ constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
@@ -1729,6 +1729,13 @@ int dispatch_fp8(int g, const DecodeArgs& a, int64_t units, hipStream_t st) {
     case 5: launch_fast_fp8<TT, 5>(a, ns, mi, st); break;
     case 6: launch_fast_fp8<TT, 6>(a, ns, mi, st); break;
     case 7: launch_fast_fp8<TT, 7>(a, ns, mi, st); break;
+    case 9: launch_fast_fp8<TT, 9>(a, ns, mi, st); break;
+    case 10: launch_fast_fp8<TT, 10>(a, ns, mi, st); break;
+    case 11: launch_fast_fp8<TT, 11>(a, ns, mi, st); break;
+    case 12: launch_fast_fp8<TT, 12>(a, ns, mi, st); break;
+    case 13: launch_fast_fp8<TT, 13>(a, ns, mi, st); break;
+    case 14: launch_fast_fp8<TT, 14>(a, ns, mi, st); break;
+    case 15: launch_fast_fp8<TT, 15>(a, ns, mi, st); break;
     case kWideGroup: launch_fast_fp8<TT, kWideGroup>(a, ns, mi, st); break;
     default: launch_fast_fp8<TT, 8>(a, ns, mi, st); break;
   }
@@ -1761,7 +1768,7 @@ int launch_decode(const DecodeArgs& a, int64_t units, hipStream_t st) {
     if (rc != NPD_OK) return rc;
     return npd::check_launch("npd_paged_attention");
   }
-  if constexpr (G > 8)   // kv_split_of forms 16-head units on the fast path only
+  if constexpr (G > 8)   // kv_split_of forms units of 9-16 heads on the fast path only
     return npd::fail(NPD_E_INVALID, "npd_paged_attention: no kernel for %d-head units here", G);
   else
     return launch_generic<TT, G>(a, units, st);
@@ -1770,7 +1777,17 @@ int launch_decode(const DecodeArgs& a, int64_t units, hipStream_t st) {
 template <class TT, int D>
 int dispatch_g(int g, const DecodeArgs& a, int64_t units, hipStream_t st) {
   if constexpr (D == 128) {
-    if (g == kWideGroup) return launch_decode<TT, 128, kWideGroup>(a, units, st);
+    switch (g) {   // one-pass units of 9-16 heads (kv_split_of: blocks of 16 or 32)
+      case 9: return launch_decode<TT, 128, 9>(a, units, st);
+      case 10: return launch_decode<TT, 128, 10>(a, units, st);
+      case 11: return launch_decode<TT, 128, 11>(a, units, st);
+      case 12: return launch_decode<TT, 128, 12>(a, units, st);
+      case 13: return launch_decode<TT, 128, 13>(a, units, st);
+      case 14: return launch_decode<TT, 128, 14>(a, units, st);
+      case 15: return launch_decode<TT, 128, 15>(a, units, st);
+      case kWideGroup: return launch_decode<TT, 128, kWideGroup>(a, units, st);
+      default: break;
+    }
   }
   switch (g) {
     case 1: return launch_decode<TT, D, 1>(a, units, st);
@@ -1808,20 +1825,22 @@ int dispatch_d(int64_t d, int g, const DecodeArgs& a, int64_t units, hipStream_t
   }
 }
 
-// Work units per pool kv head. Groups that are a multiple of 16 heads at head
-// dim 128 with blocks of 16 or 32 (the fast path) run as units of 16 heads,
-// whose passes run on the matrix cores and read each K/V row once. Otherwise
-// the kernels keep a group's queries and accumulators in registers for at
-// most 8 query heads: a larger group is served as kv_split equal groups of
-// at most 8 heads (the smallest such split), each reading the kv head's K/V.
+// Work units per pool kv head. At head dim 128 with blocks of 16 or 32 (the
+// fast path) the one-pass units serve up to 16 heads in their MFMA columns, so
+// a group of more than 8 heads runs as the fewest equal units of at most 16
+// heads (one for 9-16, two of 12 for 24, two of 16 for 32), each reading the
+// kv head's K/V rows once. Otherwise the kernels keep a group's queries and
+// accumulators in registers for at most 8 query heads: a larger group is
+// served as kv_split equal groups of at most 8 heads (the smallest such
+// split), each reading the kv head's K/V.
 int kv_split_of(int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
                 int64_t num_seqs) {
   const int64_t g = num_kv_heads > 0 ? num_heads / num_kv_heads : 1;
-  if (g > 8 && g % kWideGroup == 0 && head_dim == 128 && (block_size == 16 || block_size == 32) &&
-      use_fast_path(head_dim, block_size, num_seqs))
-    return (int)(g / kWideGroup);
+  const int64_t cap = g > 8 && head_dim == 128 && (block_size == 16 || block_size == 32) &&
+                              use_fast_path(head_dim, block_size, num_seqs)
+                          ? kWideGroup : 8;
   int64_t k = 1;
-  while (k < g && (g / k > 8 || g % k != 0)) ++k;
+  while (k < g && (g / k > cap || g % k != 0)) ++k;
   return (int)k;
 }
 

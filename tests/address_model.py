@@ -52,7 +52,7 @@ WIDE_MIN_G_2B = 5  # kWideMinG2B: 2-byte groups of 5-8 heads run as decode_wide_
 def wide_item(fp8: bool, g: int, d: int = 128) -> bool:
     """wide_item: at head dim 128, 16-head units, every FP8 group, and 2-byte
     groups of 5-8 heads."""
-    return d == 128 and (g == WIDE_GROUP or fp8 or WIDE_MIN_G_2B <= g <= 8)
+    return d == 128 and g <= WIDE_GROUP and (fp8 or g >= WIDE_MIN_G_2B)
 
 
 WIDE_LDS_BYTES = max(16 * V_ROW * 2, (WIDE_GROUP * 128 + WIDE_GROUP) * 4, 64 * WIDE_GROUP * 4)
@@ -227,15 +227,14 @@ def fast_min_partition(ps: int, bs: int) -> int:
 
 
 def kv_split_of(H: int, KV: int, D: int = 128, bs: int = 16, S: int = 1) -> int:
-    """decode_attention.hip kv_split_of: groups that are a multiple of 16 heads
-    (head dim 128, blocks of 16 or 32, the fast path) run as 16-head units;
-    other groups of more than 8 query heads as the smallest number of equal
-    groups of at most 8."""
+    """decode_attention.hip kv_split_of: at head dim 128 with blocks of 16 or
+    32 (the fast path) a group of more than 8 heads runs as the fewest equal
+    units of at most 16 heads; other groups of more than 8 query heads as the
+    smallest number of equal groups of at most 8."""
     g = H // KV
-    if g > 8 and g % WIDE_GROUP == 0 and D == 128 and bs in (16, 32) and use_fast_path(D, bs, S):
-        return g // WIDE_GROUP
+    cap = WIDE_GROUP if g > 8 and D == 128 and bs in (16, 32) and use_fast_path(D, bs, S) else 8
     k = 1
-    while k < g and (g // k > 8 or g % k):
+    while k < g and (g // k > cap or g % k):
         k += 1
     return k
 

@@ -230,17 +230,19 @@ def test_configs_1_to_4_and_large_batches():
 
 
 def test_group_sizes_above_8():
-    """64 q / 4 kv heads (G = 16: one 16-head unit per pool kv head, both
-    passes on the matrix cores), 128 / 4 (G = 32: two 16-head units), 9 / 1
-    (three units of 3), 48 / 4 (two units of 6), and groups of 5 and 8 (the
-    2-byte pools' MFMA pass 3 with its in-place probabilities): the decode
-    stores and LDS accesses stay inside their buffers, in both work-list forms
-    and both pool types (every FP8 group runs as a 16-column unit)."""
+    """One-pass units at head dim 128: 64 q / 4 kv heads (G = 16: one unit
+    per pool kv head), 128 / 4 (G = 32: two units of 16), 96 / 4 (two of 12),
+    9 / 1 and 48 / 4 (one unit of 9 or 12, padded to 16 columns), and groups
+    of 5 and 8: the decode stores and LDS accesses stay inside their buffers,
+    in both work-list forms and both pool types (every FP8 group runs as a
+    16-column unit)."""
     W = A.Writes()
     rng = np.random.default_rng(16)
-    assert A.kv_split_of(64, 4) == 1 and A.kv_split_of(128, 4) == 2 and A.kv_split_of(48, 4) == 2
+    assert A.kv_split_of(64, 4) == 1 and A.kv_split_of(128, 4) == 2 and A.kv_split_of(48, 4) == 1
+    assert A.kv_split_of(96, 4) == 2 and A.kv_split_of(9, 1) == 1 and A.kv_split_of(17, 1) == 17
     assert A.kv_split_of(64, 4, D=64) == 2 and A.kv_split_of(64, 4, bs=8) == 2
-    for h, kv in ((64, 4), (128, 4), (9, 1), (48, 4), (40, 8), (64, 8)):
+    assert A.kv_split_of(48, 4, D=64) == 2 and A.kv_split_of(9, 1, bs=64) == 3
+    for h, kv in ((64, 4), (128, 4), (96, 4), (9, 1), (48, 4), (40, 8), (64, 8)):
         for fp8 in (False, True):
             check_decode(W, 6, 2048, [1, 17, 300, 4097, 32768, 0], fp8, h=h, kv=kv)
             check_decode(W, 70, 400, rng.integers(0, 6400, 70), fp8, h=h, kv=kv)
