@@ -107,15 +107,25 @@ constexpr int kRing = NPD_DECODE_RING;   // fast path: K/V steps in flight per w
 // head dim 64: rows of 128 bytes, half the bytes per step; twice the steps in
 // flight keep the same bytes in flight (and the same ring registers)
 constexpr int ring_of(int d) { return d == 64 ? 2 * kRing : kRing; }
-// 16-head units: steps of K and V in flight per wave (FP8 rows are half the
-// bytes, so twice the steps keep the same bytes in flight)
+// decode_wide_item units: steps of K and V in flight per wave. FP8 rows are
+// half the bytes, so twice the steps keep the same bytes in flight (three
+// waves per SIMD); the FP8 form for many units (kHiOcc) keeps two steps and
+// four waves per SIMD instead.
 #ifndef NPD_WIDE_RING_2B
 #define NPD_WIDE_RING_2B 2
 #endif
 #ifndef NPD_WIDE_RING_FP8
 #define NPD_WIDE_RING_FP8 4
 #endif
-constexpr int wide_ring(bool fp8) { return fp8 ? NPD_WIDE_RING_FP8 : NPD_WIDE_RING_2B; }
+constexpr int wide_ring(bool fp8, bool hi_occ = false) {
+  return fp8 ? (hi_occ ? 2 : NPD_WIDE_RING_FP8) : NPD_WIDE_RING_2B;
+}
+// FP8 pools with up to 8 heads per group: launches of at least this many work
+// units ((sequence, kv-head) pairs) take the four-wave form. Config 2 (512
+// units): 43.8 against 46.0 us at 4 heads, 43.1 against 44.4 at 1, 46.0
+// against 46.5 at 8; config 4 (80 units of 8k-32k tokens, every wave a long
+// stream): 87.5 against 74.3 us, so few units keep the deeper ring.
+constexpr int64_t kFp8HiOccUnits = 256;
 
 #ifndef NPD_FAST_MAX_PARTITION
 #define NPD_FAST_MAX_PARTITION 2048
@@ -1167,7 +1177,7 @@ constexpr int kWideLdsBytes =
 // No probability or score buffer: LDS is the V tile and the hand-off, so the
 // partition is as long as the 2-byte path's and many waves fit a CU. K and V
 // loads run NBUF steps ahead in a register ring.
-template <class TT, int G, int SPB, bool kF8>
+template <class TT, int G, int SPB, bool kF8, bool kHiOcc = false>
 __device__ __forceinline__ void decode_wide_item(const DecodeArgs& a, int unit, int part, int ps,
                                                  float* s_lds) {
   constexpr int D = 128;
@@ -1180,7 +1190,7 @@ __device__ __forceinline__ void decode_wide_item(const DecodeArgs& a, int unit, 
   constexpr int NVL = kF8 ? 2 : NL; // 16-byte V loads per lane and step
   constexpr int NOB = D / 16;       // 16-dim blocks of O^T
   constexpr int BS = 16 * SPB;
-  constexpr int NBUF = wide_ring(kF8);
+  constexpr int NBUF = wide_ring(kF8, kHiOcc);
   const int lane = threadIdx.x;
   const int r = lane / LPT, j = lane % LPT;
   const int g4 = lane >> 4, n16 = lane & 15;
@@ -1397,13 +1407,12 @@ __device__ __forceinline__ void decode_wide_item(const DecodeArgs& a, int unit, 
 // short ones fill the tail. The grid is sized for the most items possible;
 // workgroups past the list (all at the end of the grid) exit at once.
 // LDS is dynamic, sized for the launch's partition (fast_lds_bytes).
-template <class TT, int D, int G, int SPB, bool kF8>
-// Head dim 128 with 5-8 heads per group: at most 168 VGPRs, three waves per
-// SIMD (1-4% faster than 8 waves per CU at 180-212). decode_wide_item units:
-// at most 256; they take 149 (2-byte) and 163 (FP8), three waves per SIMD
-// (four, at 128, ran 5% slower).
+template <class TT, int D, int G, int SPB, bool kF8, bool kHiOcc = false>
+// decode_wide_item units: at most 256 VGPRs; they take 149 (2-byte) and 163
+// (FP8), three waves per SIMD (four, at 128, ran 5% slower at 16 heads); the
+// FP8 four-wave form (kHiOcc, a ring of two steps) takes 118.
 __global__ __launch_bounds__(64)
-__attribute__((amdgpu_waves_per_eu(wide_item(kF8, G, D) ? 2 : 1)))
+__attribute__((amdgpu_waves_per_eu(wide_item(kF8, G, D) ? (kHiOcc ? 4 : 2) : 1)))
 void decode_fast_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) float s_dyn[];
   int unit, part, ps = a.partition;
@@ -1511,7 +1520,7 @@ void decode_fast_kernel(DecodeArgs a) {
     part = it.y;
   }
   if constexpr (wide_item(kF8, G, D))
-    decode_wide_item<TT, G, SPB, kF8>(a, unit, part, ps, s_dyn);
+    decode_wide_item<TT, G, SPB, kF8, kHiOcc>(a, unit, part, ps, s_dyn);
   else
     decode_fast_item<TT, D, G, SPB>(a, unit, part, ps, s_dyn);
 }
@@ -1685,11 +1694,11 @@ int64_t fast_lds_bytes(int partition, int g, bool fp8, int d) {
   return (int64_t)t * pow2ceil(g) * 4;
 }
 
-template <class TT, int D, int G, int SPB, bool kF8 = false>
+template <class TT, int D, int G, int SPB, bool kF8 = false, bool kHiOcc = false>
 int launch_fast_bs(const DecodeArgs& a, int num_seqs, int64_t max_items, hipStream_t st) {
   if (num_seqs > kInlineSchedMax)
     hipLaunchKernelGGL(decode_schedule_kernel, dim3(1), dim3(kSchedThreads), 0, st, a, num_seqs);
-  hipLaunchKernelGGL((decode_fast_kernel<TT, D, G, SPB, kF8>), dim3((unsigned)max_items), dim3(64),
+  hipLaunchKernelGGL((decode_fast_kernel<TT, D, G, SPB, kF8, kHiOcc>), dim3((unsigned)max_items), dim3(64),
                      (unsigned)fast_lds_bytes(a.partition, G, kF8, D), st, a);
   return NPD_OK;
 }
@@ -1710,9 +1719,16 @@ int launch_fast(const DecodeArgs& a, int num_seqs, int64_t max_items, hipStream_
   }
 }
 
-// FP8 pools: the fast path only, head_dim 128, block sizes 16 and 32
+// FP8 pools: the fast path only, head_dim 128, block sizes 16 and 32; with up
+// to 8 heads per group and at least kFp8HiOccUnits units, the four-wave form
 template <class TT, int G>
 int launch_fast_fp8(const DecodeArgs& a, int num_seqs, int64_t max_items, hipStream_t st) {
+  if constexpr (G <= 8) {
+    if ((int64_t)num_seqs * a.num_kv_heads >= kFp8HiOccUnits) {
+      if (a.block_size == 16) return launch_fast_bs<TT, 128, G, 1, true, true>(a, num_seqs, max_items, st);
+      return launch_fast_bs<TT, 128, G, 2, true, true>(a, num_seqs, max_items, st);
+    }
+  }
   if (a.block_size == 16) return launch_fast_bs<TT, 128, G, 1, true>(a, num_seqs, max_items, st);
   return launch_fast_bs<TT, 128, G, 2, true>(a, num_seqs, max_items, st);
 }

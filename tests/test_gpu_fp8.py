@@ -146,9 +146,28 @@ def test_decode_rescale_mid_partition(device, G):
     _run_and_check(device, q.cpu(), k8, v8, bt.cpu(), sl.cpu(), ks, vs, mb, 16, dtype)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("G,bs", [(1, 16), (4, 16), (4, 32), (8, 16), (12, 16)])
+def test_decode_many_units(device, dtype, G, bs):
+    """40 sequences x 8 kv heads = 320 work units: groups of up to 8 heads
+    take the four-wave form (two steps in flight), 12 heads the three-wave
+    one; contexts from 0 to 9000 tokens, some past several partitions, rows
+    past the context holding NaN codes."""
+    g = np.random.default_rng(G * bs)
+    lens = [int(x) for x in g.integers(0, 9000, 40)]
+    lens[:4] = [0, 1, 17, 9000]
+    q, kc, vc, bt, sl, ks, vs, mb = _fp8_case(device, lens, G * 8, 8, bs, dtype, seed=300 + G + bs)
+    for i, n in enumerate(sl.tolist()):
+        if n % bs:
+            b = int(bt[i, (n - 1) // bs])
+            kc[b, :, n % bs:, :] = 0x7F
+            vc[b, :, n % bs:, :] = 0xFF
+    _run_and_check(device, q, kc, vc, bt, sl, ks, vs, mb, bs, dtype)
+
+
 def test_decode_long_context_merge_groups(device):
-    """80 units with a 32769-token context: partitions of 256 tokens (the FP8
-    rule), 129 of them, merged in 9 groups (the last a group of one)."""
+    """80 units with a 32769-token context and 9 other lengths: many
+    partitions merged in groups of 16 (the last a group of one)."""
     lens = [32769, 5000, 17, 1, 2048, 2049, 4097, 100, 0, 9000]
     args = _fp8_case(device, lens, 16, 8, 16, torch.bfloat16, seed=2048)
     _run_and_check(device, *args, 16, torch.bfloat16)
