@@ -1177,7 +1177,7 @@ constexpr int kWideLdsBytes =
 // No probability or score buffer: LDS is the V tile and the hand-off, so the
 // partition is as long as the 2-byte path's and many waves fit a CU. K and V
 // loads run NBUF steps ahead in a register ring.
-template <class TT, int G, int SPB, bool kF8, bool kHiOcc = false>
+template <class TT, int G, int SPB, bool kF8, bool kHiOcc = false, bool kL2 = false>
 __device__ __forceinline__ void decode_wide_item(const DecodeArgs& a, int unit, int part, int ps,
                                                  float* s_lds) {
   constexpr int D = 128;
@@ -1244,10 +1244,13 @@ __device__ __forceinline__ void decode_wide_item(const DecodeArgs& a, int unit, 
   // 64c + 16*g4 .. +15, converted in two halves, the A operands of S MFMAs
   // 2c and 2c + 1 (the head dims are summed in another order; Q follows it)
   // 2-byte pools: nontemporal loads (98.6 us, against 107.3 with plain loads,
-  // config 2 with 128 q heads); FP8 pools: plain loads (46.6 us, against 47.3
-  // with nontemporal ones, config 2)
+  // config 2 with 128 q heads), except where several units read one kv
+  // head's rows (kL2: groups above 16 heads; the units' items sit on one XCD,
+  // and plain loads let the later ones find the rows in its L2: 256 q heads
+  // 154.6 -> 126.3 us, 384 223.2 -> 158.5); FP8 pools: plain loads (46.6 us,
+  // against 47.3 with nontemporal ones, config 2)
   auto ld_kv = [](const u32x4* p) -> u32x4 {
-    if constexpr (kF8) return *p;
+    if constexpr (kF8 || kL2) return *p;
     else return ld_stream(p);
   };
   auto load_k = [&](u32x4* buf, int st) {
@@ -1407,7 +1410,7 @@ __device__ __forceinline__ void decode_wide_item(const DecodeArgs& a, int unit, 
 // short ones fill the tail. The grid is sized for the most items possible;
 // workgroups past the list (all at the end of the grid) exit at once.
 // LDS is dynamic, sized for the launch's partition (fast_lds_bytes).
-template <class TT, int D, int G, int SPB, bool kF8, bool kHiOcc = false>
+template <class TT, int D, int G, int SPB, bool kF8, bool kHiOcc = false, bool kL2 = false>
 // decode_wide_item units: at most 256 VGPRs; they take 149 (2-byte) and 163
 // (FP8), three waves per SIMD (four, at 128, ran 5% slower at 16 heads); the
 // FP8 four-wave form (kHiOcc, a ring of two steps) takes 118.
@@ -1520,7 +1523,7 @@ void decode_fast_kernel(DecodeArgs a) {
     part = it.y;
   }
   if constexpr (wide_item(kF8, G, D))
-    decode_wide_item<TT, G, SPB, kF8, kHiOcc>(a, unit, part, ps, s_dyn);
+    decode_wide_item<TT, G, SPB, kF8, kHiOcc, kL2>(a, unit, part, ps, s_dyn);
   else
     decode_fast_item<TT, D, G, SPB>(a, unit, part, ps, s_dyn);
 }
@@ -1694,18 +1697,24 @@ int64_t fast_lds_bytes(int partition, int g, bool fp8, int d) {
   return (int64_t)t * pow2ceil(g) * 4;
 }
 
-template <class TT, int D, int G, int SPB, bool kF8 = false, bool kHiOcc = false>
+template <class TT, int D, int G, int SPB, bool kF8 = false, bool kHiOcc = false, bool kL2 = false>
 int launch_fast_bs(const DecodeArgs& a, int num_seqs, int64_t max_items, hipStream_t st) {
   if (num_seqs > kInlineSchedMax)
     hipLaunchKernelGGL(decode_schedule_kernel, dim3(1), dim3(kSchedThreads), 0, st, a, num_seqs);
-  hipLaunchKernelGGL((decode_fast_kernel<TT, D, G, SPB, kF8, kHiOcc>), dim3((unsigned)max_items), dim3(64),
+  hipLaunchKernelGGL((decode_fast_kernel<TT, D, G, SPB, kF8, kHiOcc, kL2>), dim3((unsigned)max_items), dim3(64),
                      (unsigned)fast_lds_bytes(a.partition, G, kF8, D), st, a);
   return NPD_OK;
 }
 
 template <class TT, int D, int G>
 int launch_fast(const DecodeArgs& a, int num_seqs, int64_t max_items, hipStream_t st) {
-  if constexpr (D != 128 || G > 8) {   // block sizes 16 and 32 (use_fast_path, wide_group)
+  if constexpr (D != 128 || G > 8) {   // block sizes 16 and 32 (use_fast_path, kv_split_of)
+    if constexpr (D == 128 && G > 8) {
+      if (a.kv_split > 1) {   // several units per kv head: plain loads (kL2)
+        if (a.block_size == 16) return launch_fast_bs<TT, D, G, 1, false, false, true>(a, num_seqs, max_items, st);
+        return launch_fast_bs<TT, D, G, 2, false, false, true>(a, num_seqs, max_items, st);
+      }
+    }
     if (a.block_size == 16) return launch_fast_bs<TT, D, G, 1>(a, num_seqs, max_items, st);
     return launch_fast_bs<TT, D, G, 2>(a, num_seqs, max_items, st);
   } else {
