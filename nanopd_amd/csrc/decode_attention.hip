@@ -62,7 +62,7 @@ struct Mfma16<npd::F16> {
                                                  __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
   }
 };
-// S^T = K . Q^T of 16-head units on v_mfma_f32_16x16x32_{bf16,f16}:
+// S^T = K . Q^T of decode_wide_item units on v_mfma_f32_16x16x32_{bf16,f16}:
 // A[m = lane%16][k = 8*(lane/16) + e], B[k = 8*(lane/16) + e][n = lane%16],
 // D[m = 4*(lane/16) + i][n = lane%16].
 template <class TT>
@@ -632,7 +632,7 @@ using npd::st_coherent2;
 // relative to the merged max, not normalised), written to slot dst; else the
 // normalised rows of (sequence s, kv-head kh) go to the output.
 constexpr int kMergeFlight = 4;
-// 16-head units: a head's probability reference moves only when a step's max
+// decode_wide_item units: a head's probability reference moves only when a step's max
 // exceeds it by more than this (log2 units), so probabilities stay <= 2^8
 constexpr float kTauDecode = 8.f;
 constexpr int kMergeGroup = 16;   // partitions per first-level merge (long contexts)
@@ -1152,10 +1152,10 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
 }
 
 
-// LDS of a 16-head unit (decode_wide_item): the 16 x kVRow V tile, then the
-// G x D floats of the O hand-off and G (1/l) values after it, then the
-// merge's [64][GP] weights, each from byte 0 once the one before is no longer
-// read. Independent of the partition.
+// LDS of a decode_wide_item unit: the 16 x kVRow V tile, then the 16 x D
+// floats of the O hand-off (every MFMA column) and 16 (1/l) values after it,
+// then the merge's [64][GP] weights, each from byte 0 once the one before is
+// no longer read. Independent of the partition.
 constexpr int kWideLdsBytes =
     cmax(cmax(16 * kVRow * 2, (kWideGroup * 128 + kWideGroup) * 4), 64 * kWideGroup * 4);
 
