@@ -104,6 +104,8 @@ def test_noalloc_under_graph_capture_after_eager_call(device):
     # (num_seqs, heads, kv_heads, ctx_max, dtype, seed)
     ((96, 32, 8, 4096, torch.bfloat16, 1), (8, 32, 8, 2000, torch.float16, 2)),
     ((8, 32, 8, 32768, torch.bfloat16, 3), (4, 12, 2, 511, torch.float16, 4)),
+    # one-pass units: 16 heads per kv head, then 32 (two units of 16 per kv head)
+    ((12, 128, 8, 2500, torch.bfloat16, 5), (6, 64, 2, 9000, torch.float16, 6)),
 ])
 def test_noalloc_matches_workspace_entry_point(device, first, second):
     for num_seqs, heads, kvh, ctx_max, dtype, seed in (first, second):
