@@ -1152,12 +1152,22 @@ __device__ __forceinline__ void decode_fast_item(const DecodeArgs& a, int unit, 
 }
 
 
-// LDS of a decode_wide_item unit: the 16 x kVRow V tile, then the 16 x D
-// floats of the O hand-off (every MFMA column) and 16 (1/l) values after it,
-// then the merge's [64][GP] weights, each from byte 0 once the one before is
-// no longer read. Independent of the partition.
-constexpr int kWideLdsBytes =
-    cmax(cmax(16 * kVRow * 2, (kWideGroup * 128 + kWideGroup) * 4), 64 * kWideGroup * 4);
+// Units of more than kWideKLdsFrom heads over a 2-byte pool stage K through
+// LDS: coalesced loads (4 rows x 256 B per load), rows of kKRow elements (one
+// 16-byte pad, so the 16 rows a read covers start in different banks). bench.py
+// A/B, config 2's contexts, 8 kv heads (direct -> staged, us): 13 heads
+// 96.6 -> 94.5, 14 97.6 -> 95.7, 16 98.6 -> 95.9, 32 (two 16-head units)
+// 126.6 -> 123.1; but 10 heads 93.5 -> 97.1, 12 94.6 -> 98.1, 6 88.3 -> 90.0,
+// 8 90.0 -> 89.5, so smaller units read K straight into the MFMA operand.
+constexpr int kWideKLdsFrom = 12;
+constexpr int kKRow = 128 + 8;
+
+// LDS of a decode_wide_item unit: the 16 x kVRow V tile and the 16 x kKRow K
+// tile, then the 16 x D floats of the O hand-off (every MFMA column) and 16
+// (1/l) values after it, then the merge's [64][GP] weights, each from byte 0
+// once the one before is no longer read. Independent of the partition.
+constexpr int kWideLdsBytes = cmax(cmax(16 * kVRow * 2 + 16 * kKRow * 2, (kWideGroup * 128 + kWideGroup) * 4),
+                                   64 * kWideGroup * 4);
 
 // Units of 16 heads of a 2-byte pool, and any group of an FP8 pool (padded to
 // 16 with zero queries), D = 128: one pass over the partition. Per 16-token
@@ -1165,8 +1175,9 @@ constexpr int kWideLdsBytes =
 //   S^T = K . Q^T on v_mfma_f32_16x16x32 (4 chunks of 32 dims). Its A
 //     operand comes straight from the pool: lane (g4, n16) loads 16 bytes of
 //     token n16's row (see load_k), so each load covers 64 contiguous bytes of
-//     every row of the step. Lane (g4, n16) ends with the scores of tokens
-//     4*g4 + i of head n16.
+//     every row of the step; units of more than kWideKLdsFrom heads over a
+//     2-byte pool load K coalesced and read the operand from LDS instead.
+//     Lane (g4, n16) ends with the scores of tokens 4*g4 + i of head n16.
 //   The head's step max (its 4 scores, then the 4 rows by v_permlane16/32_swap)
 //     moves the head's reference only when it exceeds it by more than
 //     2^kTauDecode, so probabilities stay <= 2^kTauDecode; a move rescales the
@@ -1174,7 +1185,7 @@ constexpr int kWideLdsBytes =
 //   The 4 probabilities, rounded to TT, are the B operand of O^T += V^T . P^T
 //     on v_mfma_f32_16x16x16 as they stand; the V tile goes through LDS for
 //     the transposing reads (ds_read_b64_tr_b16) of the A operand.
-// No probability or score buffer: LDS is the V tile and the hand-off, so the
+// No probability or score buffer: LDS is the V (and K) tile and the hand-off, so the
 // partition is as long as the 2-byte path's and many waves fit a CU. K and V
 // loads run NBUF steps ahead in a register ring.
 template <class TT, int G, int SPB, bool kF8, bool kHiOcc = false, bool kL2 = false>
@@ -1191,6 +1202,7 @@ __device__ __forceinline__ void decode_wide_item(const DecodeArgs& a, int unit, 
   constexpr int NOB = D / 16;       // 16-dim blocks of O^T
   constexpr int BS = 16 * SPB;
   constexpr int NBUF = wide_ring(kF8, kHiOcc);
+  constexpr bool kKLds = !kF8 && G > kWideKLdsFrom;   // K staged through LDS
   const int lane = threadIdx.x;
   const int r = lane / LPT, j = lane % LPT;
   const int g4 = lane >> 4, n16 = lane & 15;
@@ -1253,10 +1265,17 @@ __device__ __forceinline__ void decode_wide_item(const DecodeArgs& a, int unit, 
     if constexpr (kF8 || kL2) return *p;
     else return ld_stream(p);
   };
+  // (kKLds: coalesced like V, load i of lane (r, j) = row i*TPL + r, chunk j)
   auto load_k = [&](u32x4* buf, int st) {
-    const int64_t b = (kF8 ? step_base(st) / 2 + n16 * (LPT / 2) : step_base(st) + n16 * LPT) + g4;
+    if constexpr (kKLds) {
+      const int64_t b = step_base(st) + lane;
 #pragma unroll
-    for (int c = 0; c < NKL; ++c) buf[c] = ld_kv(static_cast<const u32x4*>(a.k_cache) + b + 4 * c);
+      for (int i = 0; i < NKL; ++i) buf[i] = ld_kv(static_cast<const u32x4*>(a.k_cache) + b + i * 64);
+    } else {
+      const int64_t b = (kF8 ? step_base(st) / 2 + n16 * (LPT / 2) : step_base(st) + n16 * LPT) + g4;
+#pragma unroll
+      for (int c = 0; c < NKL; ++c) buf[c] = ld_kv(static_cast<const u32x4*>(a.k_cache) + b + 4 * c);
+    }
   };
   // V coalesced, 16-byte loads: 2-byte pools: load i of lane (r, j) = row
   // i*TPL + r, chunk j (8 dims); FP8: load i of lane (r8, j8) = row 8i + r8,
@@ -1279,6 +1298,7 @@ __device__ __forceinline__ void decode_wide_item(const DecodeArgs& a, int unit, 
                       : u32x4{0, 0, 0, 0};
   }
   uint16_t* s_vt = reinterpret_cast<uint16_t*>(s_lds);
+  uint16_t* s_kt = s_vt + 16 * kVRow;   // kKLds: the step's K rows
   // A of the P.V MFMA: V^T[dim nb*16 + n16][tokens 4*g4 .. +3] by transposing
   // reads (lane (g4, n16) addresses token 4*g4 + n16/4, dims nb*16 + 4*(n16%4) .. +3)
   const uint16_t* vl = s_vt + (g4 * 4 + (n16 >> 2)) * kVRow + 4 * (n16 & 3);
@@ -1312,6 +1332,11 @@ __device__ __forceinline__ void decode_wide_item(const DecodeArgs& a, int unit, 
         *reinterpret_cast<u32x4*>(&s_vt[(i * TPL + r) * kVRow + j * 8]) = v;
       }
     }
+    if constexpr (kKLds) {   // rows past the context are masked from the scores below
+#pragma unroll
+      for (int i = 0; i < NKL; ++i)
+        *reinterpret_cast<u32x4*>(&s_kt[(i * TPL + r) * kKRow + j * 8]) = kraw[i];
+    }
     // S^T for the step's 16 tokens
     f32x4 sacc = f32x4{0, 0, 0, 0};
 #pragma unroll
@@ -1319,6 +1344,9 @@ __device__ __forceinline__ void decode_wide_item(const DecodeArgs& a, int unit, 
       if constexpr (kF8) {
         sacc = MfmaK32<TT>::mma(e4m3x8_to<TT>(u32x2{kraw[c].x, kraw[c].y}), qb[2 * c], sacc);
         sacc = MfmaK32<TT>::mma(e4m3x8_to<TT>(u32x2{kraw[c].z, kraw[c].w}), qb[2 * c + 1], sacc);
+      } else if constexpr (kKLds) {   // row n16, dims 32c + 8*g4 .. +7
+        sacc = MfmaK32<TT>::mma(*reinterpret_cast<const u32x4*>(&s_kt[n16 * kKRow + (4 * c + g4) * 8]),
+                                qb[c], sacc);
       } else {
         sacc = MfmaK32<TT>::mma(kraw[c], qb[c], sacc);
       }
@@ -1374,8 +1402,8 @@ __device__ __forceinline__ void decode_wide_item(const DecodeArgs& a, int unit, 
 
   // O^T blocks (lane (g4, n16): dims nb*16 + 4*g4 .. +3 of head n16) ->
   // s_o[h][D] and 1/l -> s_il[h], read back per (head, 8-dim chunk). The V
-  // tile is no longer read: the last MFMAs, which consume it, feed these
-  // stores.
+  // and K tiles are no longer read: the last MFMAs, which consume them, feed
+  // these stores.
   float* s_o = s_lds;
   float* s_il = s_lds + kWideGroup * D;   // past all 16 columns' rows
 #pragma unroll

@@ -55,8 +55,18 @@ def wide_item(fp8: bool, g: int, d: int = 128) -> bool:
     return d == 128 and g <= WIDE_GROUP and (fp8 or g >= WIDE_MIN_G_2B)
 
 
-WIDE_LDS_BYTES = max(16 * V_ROW * 2, (WIDE_GROUP * 128 + WIDE_GROUP) * 4, 64 * WIDE_GROUP * 4)
-"""kWideLdsBytes: V tile, then O hand-off + 1/l, then merge weights, each from byte 0."""
+K_ROW = 128 + 8        # kKRow: elements per row of the K tile in LDS
+WIDE_K_LDS_FROM = 12   # kWideKLdsFrom: 2-byte units of more heads stage K through LDS
+
+
+def wide_k_lds(fp8: bool, g: int) -> bool:
+    """decode_wide_item's kKLds for a unit of g heads."""
+    return not fp8 and g > WIDE_K_LDS_FROM
+
+
+WIDE_LDS_BYTES = max(16 * V_ROW * 2 + 16 * K_ROW * 2, (WIDE_GROUP * 128 + WIDE_GROUP) * 4,
+                     64 * WIDE_GROUP * 4)
+"""kWideLdsBytes: V and K tiles, then O hand-off + 1/l, then merge weights, each from byte 0."""
 WIDE_RING_2B = 2   # NPD_WIDE_RING_2B: steps of K and V in flight, 16-head units
 WIDE_RING_FP8 = 4  # NPD_WIDE_RING_FP8
 
@@ -462,6 +472,22 @@ def decode(W: Writes, L: DecodeLaunch, out: Buf, ws: Buf, seq_lens: np.ndarray,
             tr = 2 * (((lane >> 4) * 4 + ((lane & 15) >> 2)) * V_ROW + 4 * (lane & 3))
             W.index(tr[:, None] + 2 * 16 * np.arange(D // 16)[None, :] + 7, L.lds_floats * 4,
                     "decode LDS transposing V reads (bytes)")
+            if wide_k_lds(L.fp8, L.G):
+                # K tile after the V tile: writes of load i by lane (r, j) at
+                # row i*TPL + r, chunk j; operand reads of S MFMA c by lane
+                # (g4, n16) at row n16, chunk 4c + g4 (16 bytes each)
+                k0 = 2 * 16 * V_ROW
+                lpt = D // 8
+                wr = (np.arange(4)[:, None] * (64 // lpt) + lane[None, :] // lpt) * K_ROW + 8 * (lane % lpt)
+                rd = (lane[None, :] & 15) * K_ROW + 8 * (4 * np.arange(4)[:, None] + (lane[None, :] >> 4))
+                assert (wr >= 0).all() and wr.max() // K_ROW == 15
+                for x, what in ((wr, "writes"), (rd, "operand reads")):
+                    W.index(k0 + 2 * x + 15, L.lds_floats * 4, f"decode LDS K tile {what} (bytes)")
+                # every element of the 16 x 128 tile is written before it is read
+                cover = np.zeros((16, K_ROW), dtype=bool)
+                for row, col in zip((wr // K_ROW).ravel(), (wr % K_ROW).ravel()):
+                    cover[row, col:col + 8] = True
+                assert cover[:, :D].all() and not cover[:, D:].any()
         else:
             W.index(nsteps[run] * 16 * gp - 1, L.partition * gp + 16 * ring * gp, "decode LDS scores")
         nb = _ceil(ntok[run], L.bs)
