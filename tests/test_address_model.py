@@ -232,7 +232,8 @@ def test_configs_1_to_4_and_large_batches():
 def test_group_sizes_above_8():
     """One-pass units at head dim 128: 64 q / 4 kv heads (G = 16: one unit
     per pool kv head), 128 / 4 (G = 32: two units of 16), 96 / 4 (two of 12),
-    9 / 1 and 48 / 4 (one unit of 9 or 12, padded to 16 columns), and groups
+    9 / 1 and 48 / 4 (one unit of 9 or 12, padded to 16 columns), 14 / 1 and
+    26 / 1 (units of 14 and 13, whose K goes through the LDS tile), and groups
     of 5 and 8: the decode stores and LDS accesses stay inside their buffers,
     in both work-list forms and both pool types (every FP8 group runs as a
     16-column unit)."""
@@ -242,7 +243,9 @@ def test_group_sizes_above_8():
     assert A.kv_split_of(96, 4) == 2 and A.kv_split_of(9, 1) == 1 and A.kv_split_of(17, 1) == 17
     assert A.kv_split_of(64, 4, D=64) == 2 and A.kv_split_of(64, 4, bs=8) == 2
     assert A.kv_split_of(48, 4, D=64) == 2 and A.kv_split_of(9, 1, bs=64) == 3
-    for h, kv in ((64, 4), (128, 4), (96, 4), (9, 1), (48, 4), (40, 8), (64, 8)):
+    assert A.kv_split_of(26, 1) == 2 and A.wide_k_lds(False, 13) and not A.wide_k_lds(False, 12)
+    assert not A.wide_k_lds(True, 16)
+    for h, kv in ((64, 4), (128, 4), (96, 4), (9, 1), (48, 4), (40, 8), (64, 8), (14, 1), (26, 1)):
         for fp8 in (False, True):
             check_decode(W, 6, 2048, [1, 17, 300, 4097, 32768, 0], fp8, h=h, kv=kv)
             check_decode(W, 70, 400, rng.integers(0, 6400, 70), fp8, h=h, kv=kv)

@@ -120,14 +120,15 @@ def test_group_sizes_and_head_dims(device, dtype, D, G):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("G,kvh", [(12, 2), (16, 4), (16, 1), (9, 1), (11, 1)])
+@pytest.mark.parametrize("G,kvh", [(12, 2), (16, 4), (16, 1), (9, 1), (11, 1), (13, 1), (14, 2),
+                                   (15, 1), (26, 1)])
 def test_group_sizes_above_8(device, dtype, G, kvh):
     """More than 8 query heads per kv head (e.g. 64 q / 4 kv heads): the kv
     head of q-head h is still h // G (PA/csrc/attention/
-    paged_attention_kernel.cu:62); the op serves the group as 16-head units
-    (G = 16) or as equal sub-groups of at most 8 heads (G = 9, 11, 12).
-    Contexts up to 32k tokens (two-level merges), an empty sequence and a
-    one-token one."""
+    paged_attention_kernel.cu:62); the op serves groups of up to 16 heads as
+    one one-pass unit (direct K operand loads up to 12 heads, K staged through
+    LDS for 13-16) and G = 26 as two units of 13. Contexts up to 32k tokens
+    (two-level merges), an empty sequence and a one-token one."""
     lens = [1, 17, 300, 4097, 32768, 0]
     args = make_inputs(len(lens), G * kvh, kvh, 128, lens, 16, dtype, device, seed=G * 10 + kvh)
     q, kc, vc, bt, sl, scale, mb = args
