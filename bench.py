@@ -120,6 +120,19 @@ def cpu_baseline_decode(w, budget_s: float = 15.0) -> dict:
                       f"median of 5 runs = {med * 1e3:.1f} ms; CPU: {_cpu_model()}"}
 
 
+def fast_path(w) -> bool:
+    """Whether the decode op runs decode_fast_kernel for this shape (the
+    library's rule: head dim 128 with power-of-two blocks of 16-256, head dims
+    64 / 256 with blocks of 16 / 32, at most 4096 sequences); otherwise the
+    generic partition and merge kernels."""
+    if w.num_seqs > 4096:
+        return False
+    bs = w.block_size
+    if w.head_dim == 128:
+        return bs % 16 == 0 and bs <= 256 and bs & (bs - 1) == 0
+    return w.head_dim in (64, 256) and bs in (16, 32)
+
+
 def bench_decode(args, w) -> dict:
     from nanopd_amd import paged_kernels as pk
     dev = w.k_cache.device
@@ -176,7 +189,8 @@ def bench_decode(args, w) -> dict:
         "value": step_bytes / (ms_step * 1e-3) / 1e9,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": _profiled_traffic(f"decode_fast_kernel/{w.name}")},
+                     "traffic": _profiled_traffic(f"decode_fast_kernel/{w.name}")
+                     if fast_path(w) else None},
         "detail": {
             "attention_us_mean": round(attn_avg * 1e3, 2),
             "attention_us_in_step_mean": round(statistics.mean(attn_ms) * 1e3, 2),
@@ -189,7 +203,9 @@ def bench_decode(args, w) -> dict:
             "attention_bytes_per_sequence_sum": w.attention_bytes(),
             "store_bytes": w.store_bytes(),
             "kv_tokens": sum(w.seq_lens_list),
-            "kernels": "decode_fast_kernel (partitions + fused log-sum-exp merge)",
+            "kernels": ("decode_fast_kernel (partitions + fused log-sum-exp merge)"
+                        if fast_path(w) else
+                        "decode_partition_kernel + merge_partitions_kernel (generic)"),
         },
     }
 
@@ -681,6 +697,12 @@ def main() -> int:
     ap.add_argument("--num-heads", type=int, default=32,
                     help="decode / decode-fp8: query heads over config 2's 8 kv heads (32: "
                          "config 2 itself; 40 / 64: groups of 5 / 8)")
+    ap.add_argument("--head-dim", type=int, default=128,
+                    help="decode: head dim over config 2's contexts (64 / 128 / 256: the tuned "
+                         "kernel; other multiples of 8 in [32, 256]: the generic one)")
+    ap.add_argument("--block-size", type=int, default=16,
+                    help="decode: block size over config 2's contexts (8, or other than 16 / 32 at "
+                         "head dim 64 / 256: the generic kernel)")
     ap.add_argument("--requests", type=int, default=256, help="e2e: number of requests")
     ap.add_argument("--kv-blocks", type=int, default=12288, help="e2e: KV pool blocks of 16")
     ap.add_argument("--kv-fp8", action="store_true",
@@ -711,7 +733,8 @@ def main() -> int:
     if args.workload == "store":
         return bench_store(args, workloads.config3(dev))
     if args.workload == "decode":
-        w = workloads.config2(dev, num_heads=args.num_heads)
+        w = workloads.config2(dev, num_heads=args.num_heads, head_dim=args.head_dim,
+                              block_size=args.block_size)
     else:
         w = workloads.config4(dev)
         from nanopd_amd import paged_kernels as pk

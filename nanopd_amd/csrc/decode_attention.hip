@@ -236,6 +236,33 @@ __device__ __forceinline__ void merge_unit(const DecodeArgs& a, int unit, int s,
   }
 }
 
+// Reduce-scatter of decode_partition_kernel's partial dot products over the
+// LPT lanes of a token row, stage STEP (partner lane ^ LPT >> (STEP + 1)):
+// the first NH stages halve the values a lane holds (it keeps one half and
+// adds its partner's copy of it), the rest are plain xor-sums. Stages are
+// instantiated one by one, so every index into v is a constant: a loop over
+// them was not unrolled, and its run-time indices into v compiled to
+// compare-and-select chains over the whole array.
+template <int NV, int LPT, int NH, int STEP>
+__device__ __forceinline__ void partition_butterfly(float (&v)[NV], int j) {
+  if constexpr ((LPT >> (STEP + 1)) >= 1) {
+    constexpr int m = LPT >> (STEP + 1);
+    if constexpr (STEP < NH) {
+      constexpr int half = NV >> (STEP + 1);
+      const bool upper = (j & m) != 0;
+#pragma unroll
+      for (int k = 0; k < half; ++k) {
+        const float send = upper ? v[k] : v[k + half];
+        const float keep = upper ? v[k + half] : v[k];
+        v[k] = keep + shfl_xor(send, m);
+      }
+    } else {
+      v[0] += shfl_xor(v[0], m);
+    }
+    partition_butterfly<NV, LPT, NH, STEP + 1>(v, j);
+  }
+}
+
 // LPT: lanes per token row, a power of two >= the row's CPR = D / 8 16-byte
 // chunks (D at run time, a multiple of 8 from 32 to 256); lanes j >= CPR of a
 // row hold a zero query and load its last chunk (an address inside the row),
@@ -308,25 +335,31 @@ __global__ __launch_bounds__(64) void decode_partition_kernel(DecodeArgs a) {
 
   // rows of the unit's pool kv head inside a block
   const int64_t head_off = (int64_t)(kh / a.kv_split) * bs;
+  // power-of-two block sizes (wave-uniform) take a shift, not a division
+  const bool bs_pow2 = (bs & (bs - 1)) == 0;
+  const int bs_log2 = __builtin_ctz(bs);
   auto row_index = [&](int tl) -> int64_t {
     // 16-byte index of chunk j of token tl (clamped to the last valid token)
     const int t = t0 + (tl < ntok ? tl : ntok - 1);
-    const int lb = t / bs;
+    const int lb = bs_pow2 ? t >> bs_log2 : t / bs;
     const int off = t - lb * bs;
     const int blk = s_blk[lb - b0];
     return (((int64_t)blk * a.pool_kv_heads * bs) + head_off + off) * cpr + jc;
   };
+  // K (pass 1) and V (pass 3) rows run R steps ahead in a register ring
+  // (two steps where a step's loads take 32 registers)
+  constexpr int R = NL <= 4 ? 3 : 2;
+  auto load_rows = [&](const u32x4* __restrict__ pool, u32x4* buf, int st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) buf[i] = pool[row_index(st * kStep + i * TPL + r)];
+  };
 
   // ---------------- pass 1: scores ----------------
-  u32x4 kcur[NL];
+  u32x4 kb[R][NL];
 #pragma unroll
-  for (int i = 0; i < NL; ++i) kcur[i] = a.k_cache[row_index(i * TPL + r)];
-  for (int st = 0; st < nsteps; ++st) {
-    u32x4 knext[NL];
-    if (st + 1 < nsteps) {
-#pragma unroll
-      for (int i = 0; i < NL; ++i) knext[i] = a.k_cache[row_index((st + 1) * kStep + i * TPL + r)];
-    }
+  for (int b = 0; b < R; ++b)
+    if (b < nsteps) load_rows(a.k_cache, kb[b], b);
+  auto score_step = [&](const u32x4* kcur, int st) __attribute__((always_inline)) {
     float v[NV];
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
@@ -342,27 +375,7 @@ __global__ __launch_bounds__(64) void decode_partition_kernel(DecodeArgs a) {
         v[i * GP + h] = d;
       }
     }
-    // Butterfly over the LPT lanes of a token: halving steps first (high lane
-    // bits), then plain xor-sums for the remaining bits.
-    int cnt = NV;
-#pragma unroll
-    for (int m = LPT / 2, stepi = 0; m >= 1; m >>= 1, ++stepi) {
-      if (stepi < NH) {
-        const bool upper = (j & m) != 0;
-        const int half = cnt / 2;
-#pragma unroll
-        for (int k = 0; k < NV / 2; ++k) {
-          if (k < half) {
-            const float send = upper ? v[k] : v[k + half];
-            const float keep = upper ? v[k + half] : v[k];
-            v[k] = keep + shfl_xor(send, m);
-          }
-        }
-        cnt = half;
-      } else {
-        v[0] += shfl_xor(v[0], m);
-      }
-    }
+    partition_butterfly<NV, LPT, NH, 0>(v, j);
     const int prefix = j >> (LOG_LPT - NH);
 #pragma unroll
     for (int e = 0; e < HELD; ++e) {
@@ -371,16 +384,23 @@ __global__ __launch_bounds__(64) void decode_partition_kernel(DecodeArgs a) {
       const int tl = st * kStep + i * TPL + r;
       if (h < G) s_p[tl * GP + h] = (tl < ntok) ? v[e] * a.scale_log2 : -INFINITY;
     }
-    if (st + 1 < nsteps) {
+  };
+  for (int st0 = 0; st0 < nsteps; st0 += R) {
 #pragma unroll
-      for (int i = 0; i < NL; ++i) kcur[i] = knext[i];
+    for (int b = 0; b < R; ++b) {
+      const int st = st0 + b;
+      if (st < nsteps) {
+        score_step(kb[b], st);
+        if (st + R < nsteps) load_rows(a.k_cache, kb[b], st + R);
+      }
     }
   }
 
   // Issue the first V loads before the softmax pass so they are in flight.
-  u32x4 vcur[NL];
+  u32x4 vb[R][NL];
 #pragma unroll
-  for (int i = 0; i < NL; ++i) vcur[i] = a.v_cache[row_index(i * TPL + r)];
+  for (int b = 0; b < R; ++b)
+    if (b < nsteps) load_rows(a.v_cache, vb[b], b);
   __syncthreads();
 
   // ---------------- pass 2: softmax over the partition ----------------
@@ -414,12 +434,7 @@ __global__ __launch_bounds__(64) void decode_partition_kernel(DecodeArgs a) {
   for (int h = 0; h < GA; ++h)
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[h][d] = 0.f;
-  for (int st = 0; st < nsteps; ++st) {
-    u32x4 vnext[NL];
-    if (st + 1 < nsteps) {
-#pragma unroll
-      for (int i = 0; i < NL; ++i) vnext[i] = a.v_cache[row_index((st + 1) * kStep + i * TPL + r)];
-    }
+  auto pv_step = [&](const u32x4* vcur, int st) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int tl = st * kStep + i * TPL + r;
@@ -446,9 +461,15 @@ __global__ __launch_bounds__(64) void decode_partition_kernel(DecodeArgs a) {
         }
       }
     }
-    if (st + 1 < nsteps) {
+  };
+  for (int st0 = 0; st0 < nsteps; st0 += R) {
 #pragma unroll
-      for (int i = 0; i < NL; ++i) vcur[i] = vnext[i];
+    for (int b = 0; b < R; ++b) {
+      const int st = st0 + b;
+      if (st < nsteps) {
+        pv_step(vb[b], st);
+        if (st + R < nsteps) load_rows(a.v_cache, vb[b], st + R);
+      }
     }
   }
   // Combine the TPL token rows of the wave.

@@ -179,13 +179,20 @@ def config2_seq_lens(seed: int = 2, batch: int = 64) -> list:
     return [int(x) for x in rng.integers(128, 4096, size=batch, endpoint=True)]
 
 
-def config2(device="cpu", seed: int = 2, batch: int = 64, num_heads: int = 32) -> DecodeWorkload:
-    """Configuration 2 (32 q / 8 kv heads). num_heads other than 32 gives the
-    same contexts, tables and kv heads with another group size (e.g. 64: the
-    64 q / 8 kv heads of larger Qwen models)."""
-    name = "cfg2_qwen3_8b_decode_b64" if num_heads == 32 else f"cfg2_contexts_h{num_heads}_kv8_b64"
+def config2(device="cpu", seed: int = 2, batch: int = 64, num_heads: int = 32,
+            head_dim: int = 128, block_size: int = 16) -> DecodeWorkload:
+    """Configuration 2 (32 q / 8 kv heads, head dim 128, blocks of 16). Other
+    values give the same contexts and kv heads with another group size (e.g.
+    num_heads 64: the 64 q / 8 kv heads of larger Qwen models), head dim or
+    block size."""
+    if (num_heads, head_dim, block_size) == (32, 128, 16):
+        name = "cfg2_qwen3_8b_decode_b64"
+    else:
+        name = f"cfg2_contexts_h{num_heads}_kv8_b64"
+        name += f"_d{head_dim}" if head_dim != 128 else ""
+        name += f"_bs{block_size}" if block_size != 16 else ""
     return make_decode_workload(
-        name, num_heads=num_heads, num_kv_heads=8, head_dim=128, block_size=16,
+        name, num_heads=num_heads, num_kv_heads=8, head_dim=head_dim, block_size=block_size,
         dtype=torch.bfloat16, seq_lens=config2_seq_lens(seed, batch), seed=seed, device=device)
 
 
