@@ -25,12 +25,14 @@
 // group use no MFMA: at one query row per sequence the op is HBM-bound; with
 // 5-8 heads pass 3's fp32 products no longer keep up, and it runs on
 // v_mfma_f32_16x16x16 (the probabilities rounded to the pool type in place).
-// Groups of 16 heads (2-byte pools) and every group of an FP8 pool run as
-// decode_wide_item units instead: one pass per partition with S^T = K.Q^T on
-// v_mfma_f32_16x16x32 (K read straight into the operand layout, the heads
-// padded to 16) and O^T += V^T.P^T on v_mfma_f32_16x16x16 (V staged in LDS),
-// probabilities formed against a per-head reference that moves only by more
-// than 2^8, and no score buffer.
+// At head dim 128, groups of 5-16 heads (2-byte pools; larger groups as
+// units of at most 16) and every group of an FP8 pool run as decode_wide_item
+// units instead: one pass per partition with S^T = K.Q^T on
+// v_mfma_f32_16x16x32 (K read straight into the operand layout, or staged
+// through LDS for 2-byte units of 13-16 heads; the heads padded to 16) and
+// O^T += V^T.P^T on v_mfma_f32_16x16x16 (V staged in LDS), probabilities
+// formed against a per-head reference that moves only by more than 2^8, and
+// no score buffer.
 #include <type_traits>
 
 #include "common.h"
@@ -784,9 +786,10 @@ __device__ __forceinline__ void merge_unit_fast(const DecodeArgs& a, int64_t slo
 }
 
 // decode_wide_item units (head dim 128): S and P.V on the matrix cores, whose
-// 16-wide tiles serve 16 heads as cheaply as 8. Groups of 16 heads (also each
-// 16 of a multiple of 16) read the kv head's K/V rows once instead of once
-// per 8-head sub-group. FP8 pools run every group this way (padded to 16
+// 16-wide tiles serve 16 heads as cheaply as 8. Groups of up to 16 heads
+// (larger ones as the fewest equal units of at most 16) read the kv head's
+// K/V rows once instead of once per 8-head sub-group. FP8 pools run every
+// group this way (padded to 16
 // columns): its 16-byte loads cover whole rows, and at config 2 it beats the
 // LDS-staged two-pass form for every group size (48.0 against 51.0 us with 4
 // heads, 51.4 against 63.5 with 8). 2-byte pools from 5 heads on (88.0
@@ -1190,8 +1193,8 @@ constexpr int kKRow = 128 + 8;
 constexpr int kWideLdsBytes = cmax(cmax(16 * kVRow * 2 + 16 * kKRow * 2, (kWideGroup * 128 + kWideGroup) * 4),
                                    64 * kWideGroup * 4);
 
-// Units of 16 heads of a 2-byte pool, and any group of an FP8 pool (padded to
-// 16 with zero queries), D = 128: one pass over the partition. Per 16-token
+// Units of 5-16 heads of a 2-byte pool, and any group of an FP8 pool (padded
+// to 16 with zero queries), D = 128: one pass over the partition. Per 16-token
 // step of the unit's kv head:
 //   S^T = K . Q^T on v_mfma_f32_16x16x32 (4 chunks of 32 dims). Its A
 //     operand comes straight from the pool: lane (g4, n16) loads 16 bytes of
