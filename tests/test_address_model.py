@@ -435,3 +435,17 @@ def test_prefill_work_list_covers_every_part_once(case):
                     assert max(lens) - min(lens) <= 1
                     assert nsteps == 0 or min(lens) >= 1
     assert len(items) == expected
+
+
+def test_bench_names_the_kernel_the_library_runs():
+    """bench.py's fast_path (which kernel its decode line names and whether a
+    stored counter reading applies) follows the library's use_fast_path for
+    every head dim and block size bench can be given."""
+    from types import SimpleNamespace
+
+    import bench
+    for S in (64, 4096, 4097):
+        for D in (32, 64, 96, 128, 160, 192, 256):
+            for bs in (8, 16, 24, 32, 48, 64, 128, 256):
+                w = SimpleNamespace(num_seqs=S, head_dim=D, block_size=bs)
+                assert bench.fast_path(w) == A.use_fast_path(D, bs, S), (S, D, bs)
