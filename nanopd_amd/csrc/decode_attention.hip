@@ -349,8 +349,10 @@ __global__ __launch_bounds__(64) void decode_partition_kernel(DecodeArgs a) {
     return (((int64_t)blk * a.pool_kv_heads * bs) + head_off + off) * cpr + jc;
   };
   // K (pass 1) and V (pass 3) rows run R steps ahead in a register ring
-  // (two steps where a step's loads take 32 registers)
-  constexpr int R = NL <= 4 ? 3 : 2;
+  // (two steps where a step's loads take 32 registers). bench.py, config 2's
+  // contexts, ring of 3 -> 4: D 96 126.7 -> 109.5 us, D 128 with blocks of 8
+  // 129.4 -> 117.1; a ring of 6 at D 64 with blocks of 8 gained nothing.
+  constexpr int R = NL <= 4 ? 4 : 2;
   auto load_rows = [&](const u32x4* __restrict__ pool, u32x4* buf, int st) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < NL; ++i) buf[i] = pool[row_index(st * kStep + i * TPL + r)];
